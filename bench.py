@@ -1,0 +1,278 @@
+"""Benchmark of the gated-delta path on one MI355X.
+
+Default workload (the headline line): batched single-token decode, B=64
+sequences, Hk=16 key heads, Hv=32 value heads, d=128, K=4 conv taps, bf16
+activations, float32 recurrent state; one step = one fused decode launch
+(conv + SiLU + roll, q/k scaling, gates, recurrence) for all 64 sequences.
+The float32 state rotates through four 128 MiB buffers (step s reads buffer
+s % 4 and writes (s + 1) % 4), so the 512 MiB working set exceeds the 256 MB
+Infinity Cache and the bandwidth figure is HBM's, not the cache's.
+
+Also measured in the same run (reported under "also"):
+  decode_large: B=256, Hv=64, fused conv roll + gated RMSNorm (1 GiB state)
+  prefill:      B=1, T=4096 chunked prefill (bf16 MFMA), when built
+
+python bench.py [--steps K] [--warmup W] [--workload decode|decode_large|prefill|copy]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import mlx_lean_moe_amd as gdn  # noqa: E402
+from mlx_lean_moe_amd import gated_delta  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "gated-delta tokens/s at 1 GPU; decode HBM GB/s %peak; prefill MFMA util %"
+
+
+def decode_bytes(B, Hk, Hv, d, K, with_z):
+    """Algorithmic HBM bytes of one decode step (per-token terms x B plus the
+    per-step parameters)."""
+
+    C = 2 * Hk * d + Hv * d
+    per_token = 8 * Hv * d * d + 4 * (K - 1) * C + 2 * C + 4 * Hv + 2 * Hv * d
+    per_step = C * K * 4 + 8 * Hv
+    if with_z:
+        per_token += 2 * Hv * d
+        per_step += 4 * d
+    return per_token, per_step, B * per_token + per_step
+
+
+class DecodeWorkload:
+    """Synthetic decode inputs resident in HBM, with rotating state buffers."""
+
+    def __init__(self, dev, B, Hk, Hv, with_z, seed=0, n_state=4, n_inputs=8):
+        d, K = 128, 4
+        self.dims = gdn.LinearAttentionDims(Hk, Hv, d, d, K)
+        C = self.dims.conv_dim
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        randn = lambda *s: torch.randn(*s, generator=g, device=dev)
+        self.qkv = [randn(B, C).to(bf) for _ in range(n_inputs)]
+        self.a = [randn(B, Hv).to(bf) for _ in range(n_inputs)]
+        self.b = [randn(B, Hv).to(bf) for _ in range(n_inputs)]
+        self.z = [randn(B, Hv, d).to(bf) for _ in range(n_inputs)] if with_z else None
+        self.states = [randn(B, Hv, d, d) * 0.05 for _ in range(n_state)]
+        self.convs = [randn(B, K - 1, C).to(bf) for _ in range(2)]
+        self.conv_w = randn(C, K) * 0.2
+        self.A_log = torch.rand(Hv, generator=g, device=dev) * float(np.log(16))
+        self.dt_bias = torch.rand(Hv, generator=g, device=dev) * 2 - 1
+        self.norm_w = torch.rand(d, generator=g, device=dev) + 0.5
+        self.B, self.with_z = B, with_z
+        self.out = torch.empty(B, Hv, d, dtype=bf, device=dev)
+        _, _, self.bytes_per_step = decode_bytes(B, Hk, Hv, d, K, with_z)
+        self.args = self._bind()
+
+    def _bind(self):
+        """Pre-resolved C-ABI argument tuples, one per step phase, so the
+        timed loop is a bare sequence of launches."""
+
+        from mlx_lean_moe_amd import _lib
+
+        d = self.dims
+        lib = _lib.load()
+        stream = torch.cuda.current_stream().cuda_stream
+        n_s, n_i = len(self.states), len(self.qkv)
+        phases = []
+        for s in range(np.lcm(np.lcm(n_s, n_i), 2)):
+            phases.append((
+                self.qkv[s % n_i].data_ptr(), self.convs[s % 2].data_ptr(),
+                self.convs[(s + 1) % 2].data_ptr(), self.conv_w.data_ptr(),
+                self.a[s % n_i].data_ptr(), self.b[s % n_i].data_ptr(), self.A_log.data_ptr(),
+                self.dt_bias.data_ptr(), self.states[s % n_s].data_ptr(),
+                self.states[(s + 1) % n_s].data_ptr(),
+                self.z[s % n_i].data_ptr() if self.with_z else None,
+                self.norm_w.data_ptr() if self.with_z else None, 1e-6, self.out.data_ptr(),
+                _lib.GDN_BF16, self.B, d.num_key_heads, d.num_value_heads, 128, 128, 4,
+                _lib.GDN_BF16, stream))
+        self._fn = lib.gdn_decode_step
+        return phases
+
+    def step(self, s):
+        rc = self._fn(*self.args[s % len(self.args)])
+        if rc != 0:
+            raise RuntimeError(f"gdn_decode_step failed with {rc}")
+
+
+def time_steps(step, steps, warmup):
+    """Total time of `steps` back-to-back steps (events on the launch stream)
+    and the mean duration of one launch (event pair around each launch)."""
+
+    stream = torch.cuda.current_stream()
+    for s in range(warmup):
+        step(s)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for s in range(steps):
+        step(warmup + s)
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(steps)]
+    for s, (e0, e1) in enumerate(pairs):
+        e0.record(stream)
+        step(warmup + steps + s)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    launch_ms = float(np.mean([e0.elapsed_time(e1) for e0, e1 in pairs]))
+    return total_ms, launch_ms
+
+
+def bench_decode(dev, B, Hk, Hv, with_z, steps, warmup):
+    w = DecodeWorkload(dev, B, Hk, Hv, with_z)
+    total_ms, launch_ms = time_steps(w.step, steps, warmup)
+    ms = total_ms / steps
+    achieved = w.bytes_per_step / (launch_ms * 1e-3) / 1e9
+    return {
+        "tokens_per_s": B * steps / (total_ms * 1e-3),
+        "ms_per_step": ms,
+        "kernel_us": launch_ms * 1e3,
+        "bytes_per_step": w.bytes_per_step,
+        "hbm_gbs": achieved,
+        "hbm_frac": achieved / HBM_PEAK_GBS,
+    }
+
+
+def cpu_baseline_decode(B, Hk, Hv, budget_s=10.0):
+    """The C restatement of the reference's decode path (fused front-end +
+    recurrence, float32, OpenMP over (sequence, head)) timed on the host on a
+    bounded number of steps of the same workload."""
+
+    from oracle import cref
+
+    rng = np.random.default_rng(0)
+    d, K = 128, 4
+    C = 2 * Hk * d + Hv * d
+    conv_w = (rng.standard_normal((C, K)) * 0.2).astype(np.float32)
+    A_log = rng.uniform(0, np.log(16), Hv).astype(np.float32)
+    dt_bias = rng.uniform(-1, 1, Hv).astype(np.float32)
+    state = (rng.standard_normal((B, Hv, d, d)) * 0.05).astype(np.float32)
+    conv = rng.standard_normal((B, K - 1, C)).astype(np.float32)
+    qkv = rng.standard_normal((B, C)).astype(np.float32)
+    a = rng.standard_normal((B, Hv)).astype(np.float32)
+    b = rng.standard_normal((B, Hv)).astype(np.float32)
+    cref.decode_step(qkv, conv, conv_w, a, b, A_log, dt_bias, state, None, None, 1e-6,
+                     (Hk, Hv, d, d), True, state_out=state)
+    steps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and steps < 1000:
+        _, conv, _ = cref.decode_step(qkv, conv, conv_w, a, b, A_log, dt_bias, state, None, None,
+                                      1e-6, (Hk, Hv, d, d), True, state_out=state)
+        steps += 1
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    return {
+        "value": B * steps / dt,
+        "unit": "tokens/s",
+        "cores": min(threads, len(os.sched_getaffinity(0))),
+        "kind": "port",
+        "sample": f"{steps} fused decode steps of the B={B}, Hv={Hv} workload "
+                  f"({B * steps} tokens, {dt:.1f} s), float32 C/OpenMP restatement",
+    }
+
+
+def load_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "decode_large", "prefill", "copy"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-also", action="store_true", help="skip the secondary workloads")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the gated-delta path needs no collective and this "
+              "build runs on a single MI355X (see the sharding notes); use --gpus 1",
+              file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.workload == "copy":
+        # Plain copy of a known size, used to scale rocprofv3 FETCH/WRITE_SIZE.
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(max(args.steps, 1)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "copy", "bytes_read": src.numel() * 4,
+                          "bytes_written": dst.numel() * 4, "launches": max(args.steps, 1)}))
+        return 0
+
+    if args.workload in ("decode", "decode_large"):
+        big = args.workload == "decode_large"
+        B, Hk, Hv, with_z = (256, 16, 64, True) if big else (64, 16, 32, False)
+        r = bench_decode(dev, B, Hk, Hv, with_z, args.steps, args.warmup)
+        kernel = "gdn_decode_step"
+        line = {
+            "metric": METRIC,
+            "value": r["tokens_per_s"],
+            "unit": "tokens/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": r["ms_per_step"],
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16",
+            "data": "synthetic",
+            "config": {
+                "workload": ("decode B=256 Hk=16 Hv=64 d=128 K=4, fused conv roll + gated RMSNorm"
+                             if big else "decode B=64 Hk=16 Hv=32 d=128 K=4, fused conv roll"),
+                "batch": B, "tokens_per_step": B, "key_heads": Hk, "value_heads": Hv,
+                "head_dim": 128, "state": "float32, 4 rotating buffers",
+            },
+            "roofline": {
+                "bound": "hbm",
+                "achieved": r["hbm_gbs"],
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": r["hbm_frac"],
+                "traffic": load_traffic(f"{kernel}_{'b256_hv64' if big else 'b64_hv32'}_traffic.json"),
+                "kernel": kernel,
+                "kernel_us": r["kernel_us"],
+                "algorithmic_bytes_per_launch": r["bytes_per_step"],
+            },
+        }
+        if not args.no_cpu_baseline:
+            line["cpu_baseline"] = cpu_baseline_decode(B, Hk, Hv, budget_s=10.0)
+        if not args.no_also and not big:
+            lg = bench_decode(dev, 256, 16, 64, True, steps=64, warmup=8)
+            line["also"] = {"decode_large": {
+                "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
+                "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],
+                "hbm_gbs": lg["hbm_gbs"], "hbm_frac": lg["hbm_frac"]}}
+        print(json.dumps(line))
+        return 0
+
+    raise SystemExit(f"workload {args.workload} is not available in this build")
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,177 @@
+/*
+ * gdn.h - C ABI of the MI355X (gfx950) gated-delta linear-attention library.
+ *
+ * The library replaces, on an AMD GPU, the kernel side of the reference's
+ * gated-delta path (mlx-lean-moe, paths relative to its root):
+ *
+ *   src/mlx_lean_moe/model/qwen3_5/_gated_delta_metal.py:35-114  Metal scan kernel
+ *   src/mlx_lean_moe/model/qwen3_5/gated_delta.py:14-109         gates, step, scan
+ *   src/mlx_lean_moe/model/qwen3_5/linear_attention.py:22-124    conv front-end,
+ *                                                                 q/k scaling, gated norm
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are device pointers to caller-allocated, densely
+ *     packed (row-major, last axis contiguous) buffers. The library never
+ *     allocates or frees device memory.
+ *   - Sizes are plain ints / int64; dtypes are gdn_dtype codes.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL is the
+ *     null stream) and is asynchronous; calls on different streams are
+ *     independent (no mutable global state).
+ *   - Return value: 0 on success, GDN_EINVAL (< 0) for an invalid argument
+ *     (nothing is launched), GDN_EUNSUPPORTED (< 0) for a valid call this
+ *     kernel does not specialise, or a positive hipError_t from the launch.
+ *     gdn_last_error() returns a message for the calling thread's last
+ *     failure.
+ *   - Inputs are never written unless an output pointer aliases them where a
+ *     function says aliasing is allowed.
+ */
+#ifndef GDN_H
+#define GDN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    GDN_F32 = 0,
+    GDN_BF16 = 1,
+    GDN_F16 = 2
+} gdn_dtype;
+
+#define GDN_OK 0
+#define GDN_EINVAL (-1)
+#define GDN_EUNSUPPORTED (-2)
+
+/* Library ABI version (bumped on any signature change). */
+int gdn_abi_version(void);
+
+/* Message describing the calling thread's last non-zero return. */
+const char *gdn_last_error(void);
+
+/*
+ * gdn_gates - per-(row, value-head) decay and write strength.
+ *   g[i,h]    = exp(-exp(A_log[h]) * softplus(a[i,h] + dt_bias[h]))   (float32)
+ *   beta[i,h] = sigmoid(b[i,h]) rounded to beta_dtype
+ * a, b: (rows, Hv) in ab_dtype; A_log, dt_bias: (Hv) float32. Either output
+ * may be NULL (then its inputs may be NULL too).
+ * Replaces forget_gate (gated_delta.py:14-21) and mx.sigmoid(b)
+ * (linear_attention.py:116).
+ */
+int gdn_gates(const void *a, const void *b, int ab_dtype, const float *A_log,
+              const float *dt_bias, float *g, void *beta, int beta_dtype, int64_t rows,
+              int Hv, void *stream);
+
+/*
+ * gdn_frontend - causal depthwise conv (K taps) + SiLU + conv-state roll and
+ * q/k scaling for a batch of token runs.
+ *   qkv:            (T_total, C) act_dtype, C = 2*Hk*Dk + Hv*Dv, channel order [q; k; v]
+ *   conv_state_in:  (N, K-1, C) conv_dtype
+ *   conv_state_out: (N, K-1, C) act_dtype (the reference keeps the rolled state in
+ *                   the activation dtype); must not overlap conv_state_in
+ *   conv_weight:    (C, K) float32 (the reference's (C, K, 1)); rounded to act_dtype
+ *   cu_seqlens:     (N+1) int32 token offsets of the N runs, or NULL for N runs of
+ *                   T_total/N tokens each
+ *   q_out, k_out:   (T_total, Hk, Dk) act_dtype;  v_out: (T_total, Hv, Dv) act_dtype
+ * q = Dk^-1 * rms_norm(q, 1e-6), k = Dk^-1/2 * rms_norm(k, 1e-6).
+ * Replaces Qwen3_5LinearAttention._convolve and the split/scale
+ * (linear_attention.py:61-79,103-113).
+ */
+int gdn_frontend(const void *qkv, const void *conv_state_in, void *conv_state_out,
+                 int conv_dtype, const float *conv_weight, const int32_t *cu_seqlens, int N,
+                 int64_t T_total, void *q_out, void *k_out, void *v_out, int Hk, int Hv, int Dk,
+                 int Dv, int K, int act_dtype, void *stream);
+
+/*
+ * gdn_scan_reference - plain sequential recurrence, one thread per state row,
+ * the reference's operation order (gated_delta.py:35-39). Any Dk/Dv, any
+ * dtype mix; arithmetic in float32. A test aid and the use_kernel=False path.
+ *   q, k: (T_total, Hk, Dk); v: (T_total, Hv, Dv); g, beta: (T_total, Hv)
+ *   state_in: (N, Hv, Dv, Dk) state_dtype; state_out: same (may alias state_in)
+ *   y: (T_total, Hv, Dv) y_dtype
+ *   cu_seqlens: (N+1) int32 or NULL (N runs of T_total/N tokens)
+ * Replaces _gated_delta_scan_ops (gated_delta.py:93-109).
+ */
+int gdn_scan_reference(const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
+                       const void *g, int g_dtype, const void *beta, int beta_dtype,
+                       const void *state_in, void *state_out, int state_dtype, void *y,
+                       int y_dtype, const int32_t *cu_seqlens, int N, int64_t T_total, int Hk,
+                       int Hv, int Dk, int Dv, void *stream);
+
+/*
+ * gdn_scan - sequential recurrence with the state held in registers across
+ * the token loop: 32 lanes per state row, 8 rows per workgroup. Same
+ * arguments and layout as gdn_scan_reference; Dk in {32, 64, 128, 256}.
+ * Replaces the Metal kernel lean_moe_gated_delta_scan_f32
+ * (_gated_delta_metal.py:35-114), generalised to a batch of runs and to
+ * bf16/f16 inputs.
+ */
+int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
+             const void *g, int g_dtype, const void *beta, int beta_dtype,
+             const void *state_in, void *state_out, int state_dtype, void *y, int y_dtype,
+             const int32_t *cu_seqlens, int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv,
+             void *stream);
+
+/*
+ * gdn_decode_step - one fused decode token for B sequences: conv + SiLU +
+ * conv-state roll, q/k scaling, gates, the recurrence, and optionally the
+ * gated RMSNorm. One workgroup per (sequence, value head); the float32
+ * Dv x Dk state tile is read once and written once.
+ *   qkv:            (B, C) act_dtype (pre-conv projection output)
+ *   conv_state_in:  (B, K-1, C) act_dtype; conv_state_out must not overlap it
+ *   conv_weight:    (C, K) float32
+ *   a, b:           (B, Hv) act_dtype;  A_log, dt_bias: (Hv) float32
+ *   state_in:       (B, Hv, Dv, Dk) float32; state_out may alias state_in
+ *   z:              (B, Hv, Dv) act_dtype or NULL; norm_weight: (Dv) float32
+ *   out:            (B, Hv, Dv): act_dtype (gated-norm output) when z != NULL,
+ *                   else the recurrence output y in y_dtype
+ * Specialised for Dk = Dv = 128, K = 4; act_dtype in {F32, BF16}.
+ * Replaces one decode call of Qwen3_5LinearAttention.__call__ between the
+ * projections (linear_attention.py:103-124) with the Metal scan at T=1.
+ */
+int gdn_decode_step(const void *qkv, const void *conv_state_in, void *conv_state_out,
+                    const float *conv_weight, const void *a, const void *b,
+                    const float *A_log, const float *dt_bias, const float *state_in,
+                    float *state_out, const void *z, const float *norm_weight, float norm_eps,
+                    void *out, int y_dtype, int B, int Hk, int Hv, int Dk, int Dv, int K,
+                    int act_dtype, void *stream);
+
+/*
+ * gdn_prefill_chunked - chunked (WY/UT, 64-token chunks) prefill on bf16
+ * MFMA with float32 accumulation, for N packed runs.
+ *   q, k: (T_total, Hk, Dk) bf16;  v: (T_total, Hv, Dv) bf16
+ *   gate_mode 0: ga = a (T_total, Hv) bf16, gb = b (T_total, Hv) bf16, with A_log and
+ *                dt_bias (Hv) float32 (gates computed in-kernel)
+ *   gate_mode 1: ga = g (T_total, Hv) float32, gb = beta (T_total, Hv) gb_dtype
+ *   state_in: (N, Hv, Dv, Dk) float32 or NULL (zero state); state_out: (N, Hv, Dv, Dk)
+ *   y: (T_total, Hv, Dv) y_dtype
+ *   workspace: device scratch of gdn_prefill_workspace_size(...) bytes
+ * Specialised for Dk = Dv = 128. Equal, up to rounding, to gdn_scan on the
+ * same inputs. No reference counterpart: the reference prefills with the
+ * sequential scan (_gated_delta_metal.py:64-87).
+ */
+int64_t gdn_prefill_workspace_size(int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv);
+int gdn_prefill_chunked(const void *q, const void *k, const void *v, const void *ga,
+                        const void *gb, int gb_dtype, const float *A_log,
+                        const float *dt_bias, int gate_mode, const float *state_in,
+                        float *state_out, void *y, int y_dtype, const int32_t *cu_seqlens,
+                        int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv, void *workspace,
+                        int64_t workspace_bytes, void *stream);
+
+/*
+ * gdn_gated_rmsnorm - out = silu(z) * rms_norm(x, w, eps) with x first rounded
+ * to out_dtype and the normalised value held in out_dtype; the product is
+ * taken in float32 and stored in out_dtype.
+ *   x: (rows, D) x_dtype; z: (rows, D) z_dtype; w: (D) float32; out: (rows, D) out_dtype
+ * Replaces _gated_rms_norm (linear_attention.py:22-32); with out_dtype = z's
+ * dtype it includes its call site's y.astype(z.dtype) (linear_attention.py:122-124).
+ */
+int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, const float *w,
+                      float eps, void *out, int out_dtype, int64_t rows, int D, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_H */

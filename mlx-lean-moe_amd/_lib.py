@@ -1,0 +1,130 @@
+"""Loads ``libgdn.so`` (the HIP kernels behind ``include/gdn.h``) with ctypes
+and binds its C ABI.
+
+There is no fallback: if the library is missing, or if it would bind a
+second HIP runtime next to torch's, loading raises. Tensors cross the
+boundary as raw device pointers; work goes to torch's current stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgdn.so")
+ABI_VERSION = 1
+
+GDN_F32, GDN_BF16, GDN_F16 = 0, 1, 2
+GDN_EINVAL, GDN_EUNSUPPORTED = -1, -2
+
+_DTYPE_CODES = {torch.float32: GDN_F32, torch.bfloat16: GDN_BF16, torch.float16: GDN_F16}
+
+_c_void_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_c_float = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/gdn.h
+_SIGNATURES = {
+    "gdn_abi_version": (_c_int, []),
+    "gdn_last_error": (ctypes.c_char_p, []),
+    "gdn_gates": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p,
+                           _c_void_p, _c_int, _c_i64, _c_int, _c_void_p]),
+    "gdn_frontend": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                              _c_int, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
+                              _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+    "gdn_scan_reference": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p,
+                                    _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int,
+                                    _c_void_p, _c_int, _c_void_p, _c_int, _c_i64, _c_int, _c_int,
+                                    _c_int, _c_int, _c_void_p]),
+    "gdn_scan": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                          _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int,
+                          _c_void_p, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+    "gdn_decode_step": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                 _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                 _c_void_p, _c_float, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+                                 _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+    "gdn_prefill_workspace_size": (_c_i64, [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int]),
+    "gdn_prefill_chunked": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                     _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                                     _c_void_p, _c_int, _c_void_p, _c_int, _c_i64, _c_int,
+                                     _c_int, _c_int, _c_int, _c_void_p, _c_i64, _c_void_p]),
+    "gdn_gated_rmsnorm": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_float,
+                                   _c_void_p, _c_int, _c_i64, _c_int, _c_void_p]),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+_lock = threading.Lock()
+_lib = None
+
+
+class KernelError(RuntimeError):
+    """A kernel entry point returned a non-zero status."""
+
+
+def _hip_runtimes_mapped() -> set[str]:
+    paths = set()
+    with open("/proc/self/maps") as maps:
+        for line in maps:
+            if "libamdhip64.so" in line:
+                paths.add(os.path.realpath(line.split()[-1]))
+    return paths
+
+
+def load(path: str = LIB_PATH):
+    """Load and bind the library once per process (raises if it is absent)."""
+
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise ImportError(
+                f"{path} is missing: build the HIP kernels first "
+                "(python mlx-lean-moe_amd/build.py, or __graft_entry__.build())")
+        # The module-level `import torch` has mapped torch's libamdhip64; the
+        # library's dependency resolves to it by SONAME, so both share one
+        # HIP runtime (checked below).
+        lib = ctypes.CDLL(path)
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        if lib.gdn_abi_version() != ABI_VERSION:
+            raise ImportError(f"{path}: ABI version {lib.gdn_abi_version()} != {ABI_VERSION}")
+        runtimes = _hip_runtimes_mapped()
+        if len(runtimes) > 1:
+            raise ImportError(f"two HIP runtimes are mapped ({sorted(runtimes)}); "
+                              "libgdn.so must share torch's")
+        _lib = lib
+        return lib
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(device: torch.device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise ``KernelError`` on a non-zero status."""
+
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.gdn_last_error().decode(errors="replace")
+        raise KernelError(f"{name} returned {rc}: {msg}")

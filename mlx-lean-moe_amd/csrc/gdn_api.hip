@@ -1,0 +1,104 @@
+// C-ABI bookkeeping plus the two elementwise kernels of the path: the gates
+// (forget gate and beta) and the gated RMSNorm epilogue.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "gdn_common.h"
+#include "gdn_host.h"
+
+namespace gdn {
+
+static thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t err = hipGetLastError();
+    if (err == hipSuccess) return 0;
+    fail(int(err), "%s: launch failed: %s", what, hipGetErrorString(err));
+    return int(err);
+}
+
+// g = exp(-exp(A_log) * softplus(a + dt_bias)) in float32 and
+// beta = sigmoid(b) in beta's dtype (gated_delta.py:14-21, linear_attention.py:116).
+__global__ void gates_kernel(const void* a, const void* b, int ab_dtype, const float* A_log,
+                             const float* dt_bias, float* g, void* beta, int beta_dtype,
+                             int64_t n, int Hv) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int h = int(i % Hv);
+    if (g) g[i] = expf(log_forget_gate(load_any(a, i, ab_dtype), A_log[h], dt_bias[h]));
+    if (beta) store_any(beta, i, beta_dtype, sigmoid(load_any(b, i, ab_dtype)));
+}
+
+// One wave per row: out = silu(z) * rms_norm(x held in out's dtype, w, eps),
+// the normalised value held in out's dtype before the float product
+// (linear_attention.py:22-32; the call site's y.astype(z.dtype) is the
+// rounding of x to out's dtype, linear_attention.py:122-124).
+__global__ void gated_rmsnorm_kernel(const void* x, int x_dtype, const void* z, int z_dtype,
+                                     const float* w, float eps, void* out, int out_dtype,
+                                     int64_t rows, int D) {
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (row >= rows) return;  // uniform per wave
+    const int64_t base = row * D;
+    float ss = 0.f;
+    for (int i = lane; i < D; i += kWave) {
+        const float v = round_to(load_any(x, base + i, x_dtype), out_dtype);
+        ss += v * v;
+    }
+    ss = group_sum<kWave>(ss);
+    const float r = 1.f / sqrtf(ss / float(D) + eps);
+    for (int i = lane; i < D; i += kWave) {
+        const float v = round_to(load_any(x, base + i, x_dtype), out_dtype);
+        const float normed = round_to(v * r * w[i], out_dtype);
+        const float zz = load_any(z, base + i, z_dtype);
+        store_any(out, base + i, out_dtype, silu(zz) * normed);
+    }
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_abi_version(void) { return 1; }
+
+extern "C" const char* gdn_last_error(void) { return g_last_error; }
+
+extern "C" int gdn_gates(const void* a, const void* b, int ab_dtype, const float* A_log,
+                         const float* dt_bias, float* g, void* beta, int beta_dtype,
+                         int64_t rows, int Hv, void* stream) {
+    GDN_REQUIRE(rows >= 0 && Hv > 0, "gdn_gates: bad sizes rows=%lld Hv=%d", (long long)rows, Hv);
+    GDN_REQUIRE(valid_dtype(ab_dtype) && valid_dtype(beta_dtype), "gdn_gates: bad dtype");
+    if (rows == 0) return 0;
+    GDN_REQUIRE(g || beta, "gdn_gates: neither g nor beta requested");
+    GDN_REQUIRE(!g || (a && A_log && dt_bias), "gdn_gates: g needs a, A_log and dt_bias");
+    GDN_REQUIRE(!beta || b, "gdn_gates: beta needs b");
+    const int64_t n = rows * Hv;
+    const int threads = 256;
+    const int64_t blocks = (n + threads - 1) / threads;
+    hipLaunchKernelGGL(gates_kernel, dim3(unsigned(blocks)), dim3(threads), 0, as_stream(stream),
+                       a, b, ab_dtype, A_log, dt_bias, g, beta, beta_dtype, n, Hv);
+    return check_launch("gdn_gates");
+}
+
+extern "C" int gdn_gated_rmsnorm(const void* x, int x_dtype, const void* z, int z_dtype,
+                                 const float* w, float eps, void* out, int out_dtype,
+                                 int64_t rows, int D, void* stream) {
+    GDN_REQUIRE(rows >= 0 && D > 0, "gdn_gated_rmsnorm: bad sizes");
+    GDN_REQUIRE(valid_dtype(x_dtype) && valid_dtype(z_dtype) && valid_dtype(out_dtype),
+                "gdn_gated_rmsnorm: bad dtype");
+    if (rows == 0) return 0;
+    GDN_REQUIRE(x && z && w && out, "gdn_gated_rmsnorm: null pointer");
+    const int waves = 4;
+    const int64_t blocks = (rows + waves - 1) / waves;
+    hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(unsigned(blocks)), dim3(waves * kWave), 0,
+                       as_stream(stream), x, x_dtype, z, z_dtype, w, eps, out, out_dtype, rows, D);
+    return check_launch("gdn_gated_rmsnorm");
+}

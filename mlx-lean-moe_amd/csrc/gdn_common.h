@@ -1,0 +1,122 @@
+// Shared device helpers for the gated-delta kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gdn.h"
+
+#define GDN_DEV __device__ __forceinline__
+
+namespace gdn {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// storage formats
+// ---------------------------------------------------------------------------
+
+// bfloat16 <-> float with round-to-nearest-even, done on the bit pattern so
+// the rounding is exactly the one the CPU oracle applies.
+GDN_DEV float bf16_bits_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+GDN_DEV uint16_t f32_to_bf16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+GDN_DEV float round_bf16(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+
+GDN_DEV float f16_bits_to_f32(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return float(v);
+}
+
+GDN_DEV uint16_t f32_to_f16_bits(float x) {
+    _Float16 v = _Float16(x);
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+// Load element i of a buffer whose dtype is only known at run time (the
+// branch is uniform across the wave).
+GDN_DEV float load_any(const void* p, int64_t i, int dtype) {
+    if (dtype == GDN_F32) return static_cast<const float*>(p)[i];
+    const uint16_t h = static_cast<const uint16_t*>(p)[i];
+    return dtype == GDN_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+GDN_DEV void store_any(void* p, int64_t i, int dtype, float x) {
+    if (dtype == GDN_F32) {
+        static_cast<float*>(p)[i] = x;
+    } else {
+        static_cast<uint16_t*>(p)[i] = dtype == GDN_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+    }
+}
+
+// Round a float32 value to what `dtype` can hold (identity for float32).
+GDN_DEV float round_to(float x, int dtype) {
+    if (dtype == GDN_F32) return x;
+    return dtype == GDN_BF16 ? round_bf16(x) : f16_bits_to_f32(f32_to_f16_bits(x));
+}
+
+// Compile-time activation formats for the specialised kernels.
+struct ActF32 {
+    using storage = float;
+    static constexpr int code = GDN_F32;
+    static GDN_DEV float load(const storage* p, int64_t i) { return p[i]; }
+    static GDN_DEV void store(storage* p, int64_t i, float x) { p[i] = x; }
+    static GDN_DEV float round(float x) { return x; }
+};
+
+struct ActBF16 {
+    using storage = uint16_t;
+    static constexpr int code = GDN_BF16;
+    static GDN_DEV float load(const storage* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+    static GDN_DEV void store(storage* p, int64_t i, float x) { p[i] = f32_to_bf16_bits(x); }
+    static GDN_DEV float round(float x) { return round_bf16(x); }
+};
+
+// ---------------------------------------------------------------------------
+// math
+// ---------------------------------------------------------------------------
+
+// log(1 + e^x) in the logaddexp(x, 0) form (mlx.nn.softplus).
+GDN_DEV float softplus(float x) { return fmaxf(x, 0.f) + log1pf(expf(-fabsf(x))); }
+
+GDN_DEV float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
+GDN_DEV float silu(float x) { return x * sigmoid(x); }
+
+// -exp(A_log) * softplus(a + dt_bias): log of the forget gate.
+GDN_DEV float log_forget_gate(float a, float A_log, float dt_bias) {
+    return -expf(A_log) * softplus(a + dt_bias);
+}
+
+// ---------------------------------------------------------------------------
+// cross-lane reductions
+// ---------------------------------------------------------------------------
+
+template <int WIDTH>
+GDN_DEV float group_sum(float x) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+    return x;
+}
+
+// Index of the run that holds token t, given run offsets cu[0..n] (binary
+// search; cu is non-decreasing, cu[0] = 0, cu[n] = T_total).
+GDN_DEV int find_run(const int32_t* cu, int n, int64_t t) {
+    int lo = 0, hi = n;  // invariant: cu[lo] <= t < cu[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cu[mid] <= t) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+}  // namespace gdn

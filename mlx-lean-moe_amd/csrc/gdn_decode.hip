@@ -1,0 +1,241 @@
+// Fused single-token decode for B sequences: one workgroup per
+// (sequence, value head) runs the layer's whole per-token path between the
+// projections (linear_attention.py:103-124):
+//
+//   conv(K=4) + SiLU over the head's q/k/v channels, conv-state roll,
+//   q/k scaling, forget gate and beta, the gated-delta step, and (optionally)
+//   the gated RMSNorm.
+//
+// The Dv x Dk = 128 x 128 float32 state tile (64 KiB) is the only large
+// operand. Its 16 float4 loads per thread are issued first, so the HBM
+// latency hides behind the front-end arithmetic; each row is then read once
+// and written once, in 1 KiB-contiguous wave accesses (lanes 0-31 cover one
+// 512-byte row, lanes 32-63 the next).
+//
+// Per thread (wave w, lane l, half = l / 32, l32 = l % 32) the tile rows are
+// r_i = 8 i + 2 w + half, i = 0..15, columns 4 l32 .. 4 l32 + 3. The 32
+// partial dot products a half-wave holds (S.k and S.q for its 16 rows) are
+// reduce-scattered across the 32 lanes (31 exchanges instead of 160), which
+// leaves lane l32 with the full S.k of row r_{l32} (l32 < 16) or the full S.q
+// of row r_{l32-16} (l32 >= 16). Then
+//     delta = beta (v - g S.k),   y = g S.q + delta (k.q),   S <- g S + delta k^T
+// (the reference's decay/read/delta/update/output step, gated_delta.py:35-39,
+// with the output taken from the pre-update row).
+#include "gdn_common.h"
+#include "gdn_host.h"
+
+namespace gdn {
+
+constexpr int kDecodeThreads = 256;
+constexpr int kD = 128;   // Dk = Dv
+constexpr int kTaps = 4;  // conv kernel K
+
+// Sum `vals` (32 per lane) over the 32 lanes of each half-wave, leaving the
+// total of original index (lane % 32) in vals[0].
+GDN_DEV void reduce_scatter32(float (&vals)[32], int l32) {
+#pragma unroll
+    for (int step = 0; step < 5; ++step) {
+        const int off = 16 >> step;
+        const int n = 32 >> step;
+        const bool upper = (l32 & off) != 0;
+#pragma unroll
+        for (int j = 0; j < n / 2; ++j) {
+            const float keep = upper ? vals[j + n / 2] : vals[j];
+            const float send = upper ? vals[j] : vals[j + n / 2];
+            vals[j] = keep + __shfl_xor(send, off, kWave);
+        }
+    }
+}
+
+template <class Act>
+GDN_DEV float conv_channel(const typename Act::storage* __restrict__ x,
+                           const typename Act::storage* __restrict__ cs,
+                           const float4* __restrict__ w4, int C, int c) {
+    const float4 w = w4[c];
+    float acc = Act::round(w.x) * Act::load(cs, c);
+    acc += Act::round(w.y) * Act::load(cs, C + c);
+    acc += Act::round(w.z) * Act::load(cs, 2 * C + c);
+    acc += Act::round(w.w) * Act::load(x, c);
+    acc = Act::round(acc);
+    return Act::round(silu(acc));
+}
+
+template <class Act>
+GDN_DEV void roll_channel(const typename Act::storage* __restrict__ x,
+                          const typename Act::storage* __restrict__ cs,
+                          typename Act::storage* __restrict__ cso, int C, int c) {
+    cso[c] = cs[C + c];
+    cso[C + c] = cs[2 * C + c];
+    cso[2 * C + c] = x[c];
+}
+
+template <class Act, bool kNorm>
+__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
+    const typename Act::storage* __restrict__ qkv, const typename Act::storage* __restrict__ cs_in,
+    typename Act::storage* __restrict__ cs_out, const float* __restrict__ conv_w,
+    const typename Act::storage* __restrict__ a_in, const typename Act::storage* __restrict__ b_in,
+    const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* S_in,
+    float* S_out, const typename Act::storage* __restrict__ z, const float* __restrict__ norm_w,
+    float eps, void* __restrict__ out, int y_dtype, int Hk, int Hv) {
+    __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
+    __shared__ float gate_g, gate_beta, norm_r;
+
+    const int C = 2 * Hk * kD + Hv * kD;
+    const int bh = blockIdx.x;
+    const int b = bh / Hv, h = bh % Hv;
+    const int r = Hv / Hk, hk = h / r;
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, l = tid & 63, half = l >> 5, l32 = l & 31;
+
+    // A. state tile loads, issued before anything else.
+    const float4* Sb = reinterpret_cast<const float4*>(S_in + size_t(bh) * kD * kD);
+    float4 s[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = Sb[(8 * i + 2 * w + half) * (kD / 4) + l32];
+
+    // B. front-end for this head's channels.
+    const typename Act::storage* x = qkv + size_t(b) * C;
+    const typename Act::storage* cs = cs_in + size_t(b) * (kTaps - 1) * C;
+    typename Act::storage* cso = cs_out + size_t(b) * (kTaps - 1) * C;
+    const float4* w4 = reinterpret_cast<const float4*>(conv_w);
+    {
+        const int e = tid & (kD - 1);
+        const int c = (tid < kD ? 0 : Hk * kD) + hk * kD + e;
+        (tid < kD ? qs : ks)[e] = conv_channel<Act>(x, cs, w4, C, c);
+        // q/k channels are shared by the r value heads of a key head: the
+        // first of them rolls their conv state.
+        if (h % r == 0) roll_channel<Act>(x, cs, cso, C, c);
+    }
+    if (tid < kD) {
+        const int c = 2 * Hk * kD + h * kD + tid;
+        vs[tid] = conv_channel<Act>(x, cs, w4, C, c);
+        roll_channel<Act>(x, cs, cso, C, c);
+    } else if (tid == kD) {
+        const float av = Act::load(a_in, bh), bv = Act::load(b_in, bh);
+        gate_g = expf(log_forget_gate(av, A_log[h], dt_bias[h]));
+        gate_beta = Act::round(sigmoid(bv));
+    }
+    __syncthreads();
+    if (w < 2) {
+        float* arr = w == 0 ? qs : ks;
+        const float x0 = arr[l], x1 = arr[l + 64];
+        const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
+        const float rr = 1.f / sqrtf(ss / float(kD) + 1e-6f);
+        const float inv = 1.f / sqrtf(float(kD));
+        const float sc = Act::round(w == 0 ? inv * inv : inv);
+        arr[l] = Act::round(sc * Act::round(x0 * rr));
+        arr[l + 64] = Act::round(sc * Act::round(x1 * rr));
+    }
+    __syncthreads();
+
+    // C. this lane's k and q slice, and k.q.
+    const float4 kk = reinterpret_cast<const float4*>(ks)[l32];
+    const float4 qq = reinterpret_cast<const float4*>(qs)[l32];
+    const float kq = group_sum<32>(kk.x * qq.x + kk.y * qq.y + kk.z * qq.z + kk.w * qq.w);
+    const float g = gate_g, beta = gate_beta;
+
+    // D/E. partial dots, reduce-scattered over the half-wave.
+    float vals[32];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        vals[i] = s[i].x * kk.x + s[i].y * kk.y + s[i].z * kk.z + s[i].w * kk.w;
+        vals[16 + i] = s[i].x * qq.x + s[i].y * qq.y + s[i].z * qq.z + s[i].w * qq.w;
+    }
+    reduce_scatter32(vals, l32);
+
+    // F. per-row delta (lanes < 16) and output (lanes >= 16).
+    {
+        const int i = l32 & 15;
+        const int row = 8 * i + 2 * w + half;
+        const float tot = vals[0];
+        const float delta = (vs[row] - g * tot) * beta;
+        const float delta_pair = __shfl_xor(delta, 16, kWave);
+        if (l32 < 16) deltas[row] = delta;
+        else ys[row] = g * tot + delta_pair * kq;
+    }
+    __syncthreads();
+
+    // H. update and store the tile.
+    float4* So = reinterpret_cast<float4*>(S_out + size_t(bh) * kD * kD);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int row = 8 * i + 2 * w + half;
+        const float d = deltas[row];
+        float4 o;
+        o.x = g * s[i].x + d * kk.x;
+        o.y = g * s[i].y + d * kk.y;
+        o.z = g * s[i].z + d * kk.z;
+        o.w = g * s[i].w + d * kk.w;
+        So[row * (kD / 4) + l32] = o;
+    }
+
+    // I. output: y, or the gated RMSNorm of y held in the activation dtype.
+    if (!kNorm) {
+        if (tid < kD) store_any(out, size_t(bh) * kD + tid, y_dtype, ys[tid]);
+        return;
+    }
+    if (w == 0) {
+        const float y0 = Act::round(ys[l]), y1 = Act::round(ys[l + 64]);
+        const float ss = group_sum<kWave>(y0 * y0 + y1 * y1);
+        if (l == 0) norm_r = 1.f / sqrtf(ss / float(kD) + eps);
+    }
+    __syncthreads();
+    if (tid < kD) {
+        const float yv = Act::round(ys[tid]);
+        const float normed = Act::round(yv * norm_r * norm_w[tid]);
+        const float zz = Act::load(z, size_t(bh) * kD + tid);
+        Act::store(static_cast<typename Act::storage*>(out), size_t(bh) * kD + tid,
+                   silu(zz) * normed);
+    }
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void* conv_state_out,
+                               const float* conv_weight, const void* a, const void* b,
+                               const float* A_log, const float* dt_bias, const float* state_in,
+                               float* state_out, const void* z, const float* norm_weight,
+                               float norm_eps, void* out, int y_dtype, int B, int Hk, int Hv,
+                               int Dk, int Dv, int K, int act_dtype, void* stream) {
+    GDN_REQUIRE(B >= 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, "gdn_decode_step: bad head counts");
+    GDN_REQUIRE(act_dtype == GDN_F32 || act_dtype == GDN_BF16,
+                "gdn_decode_step: activations must be float32 or bfloat16");
+    GDN_REQUIRE(valid_dtype(y_dtype), "gdn_decode_step: bad y dtype");
+    if (Dk != kD || Dv != kD || K != kTaps)
+        return fail(GDN_EUNSUPPORTED, "gdn_decode_step: specialised for Dk=Dv=128, K=4 (got %d, %d, %d)",
+                    Dk, Dv, K);
+    if (B == 0) return 0;
+    GDN_REQUIRE(qkv && conv_state_in && conv_state_out && conv_weight && a && b && A_log &&
+                    dt_bias && state_in && state_out && out,
+                "gdn_decode_step: null pointer");
+    GDN_REQUIRE(!z || norm_weight, "gdn_decode_step: z without norm_weight");
+    const int64_t C = 2LL * Hk * kD + int64_t(Hv) * kD;
+    const int64_t conv_bytes = int64_t(B) * (kTaps - 1) * C * dtype_size(act_dtype);
+    GDN_REQUIRE(!overlaps(conv_state_in, conv_bytes, conv_state_out, conv_bytes),
+                "gdn_decode_step: conv_state_out overlaps conv_state_in");
+    const int64_t state_bytes = int64_t(B) * Hv * kD * kD * 4;
+    GDN_REQUIRE(state_in == state_out || !overlaps(state_in, state_bytes, state_out, state_bytes),
+                "gdn_decode_step: state_out partially overlaps state_in");
+    GDN_REQUIRE((reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out) |
+                 reinterpret_cast<uintptr_t>(conv_weight)) % 16 == 0,
+                "gdn_decode_step: state and conv weight must be 16-byte aligned");
+    const dim3 grid(unsigned(int64_t(B) * Hv)), block(kDecodeThreads);
+    hipStream_t s = as_stream(stream);
+#define GDN_DECODE_LAUNCH(ACT, NORM)                                                          \
+    hipLaunchKernelGGL((decode_kernel<ACT, NORM>), grid, block, 0, s,                         \
+                       static_cast<const ACT::storage*>(qkv),                                 \
+                       static_cast<const ACT::storage*>(conv_state_in),                       \
+                       static_cast<ACT::storage*>(conv_state_out), conv_weight,               \
+                       static_cast<const ACT::storage*>(a), static_cast<const ACT::storage*>(b), \
+                       A_log, dt_bias, state_in, state_out, static_cast<const ACT::storage*>(z), \
+                       norm_weight, norm_eps, out, y_dtype, Hk, Hv)
+    if (act_dtype == GDN_BF16) {
+        if (z) GDN_DECODE_LAUNCH(ActBF16, true); else GDN_DECODE_LAUNCH(ActBF16, false);
+    } else {
+        if (z) GDN_DECODE_LAUNCH(ActF32, true); else GDN_DECODE_LAUNCH(ActF32, false);
+    }
+#undef GDN_DECODE_LAUNCH
+    return check_launch("gdn_decode_step");
+}

@@ -1,0 +1,250 @@
+"""qwen3_5's gated-delta linear-attention layer on MI355X.
+
+Mirrors ``Qwen3_5LinearAttention`` and ``_gated_rms_norm``
+(``src/mlx_lean_moe/model/qwen3_5/linear_attention.py:22-127``): four input
+projections, the causal depthwise conv with SiLU and conv-state roll, q/k
+scaling, the gates, the gated-delta recurrence, the gated RMSNorm and
+out_proj. Projections are dense ``x @ W.T`` products (moe_block.py:44-46) on
+the vendor BLAS; everything between them runs in this library's kernels:
+
+* one decode token (1-D ``x``) with Dk = Dv = 128 and K = 4: the fused decode
+  kernel (front-end, recurrence and gated norm in one launch);
+* otherwise: the front-end kernel, then :func:`gated_delta_update` (chunked
+  prefill or sequential scan), then the gated-norm kernel.
+
+:meth:`Qwen3_5LinearAttention.decode_batch` decodes ``B`` sequences at once
+from a :class:`RecurrentStatePool`.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .config import LinearAttentionDims
+from .gated_delta import _c, _require_device, _stream, gated_delta_update
+from .recurrent_cache import RecurrentCache, RecurrentStatePool
+
+
+def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float,
+                   out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``silu(gate) * rms_norm(x, weight)``, the product in float32, the result
+    in ``out_dtype`` (x's dtype by default) (linear_attention.py:22-32).
+    Passing ``out_dtype=z.dtype`` folds in the call site's ``y.astype(z.dtype)``."""
+
+    if gate.shape != x.shape or weight.shape != x.shape[-1:]:
+        raise ValueError("gate must match x and weight its last axis")
+    device = _require_device(x, gate, weight)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    x, gate = _c(x), _c(gate)
+    w = _c(weight.float())
+    D = x.shape[-1]
+    rows = x.numel() // D if D else 0
+    out = torch.empty(x.shape, dtype=out_dtype, device=device)
+    _lib.call("gdn_gated_rmsnorm", _lib.ptr(x), _lib.dtype_code(x.dtype), _lib.ptr(gate),
+              _lib.dtype_code(gate.dtype), _lib.ptr(w), float(eps), _lib.ptr(out),
+              _lib.dtype_code(out_dtype), rows, D, _stream(device))
+    return out
+
+
+def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torch.Tensor,
+                  dims: LinearAttentionDims, cu_seqlens: torch.Tensor | None = None):
+    """Conv + SiLU + roll and q/k scaling for N packed runs
+    (linear_attention.py:61-79,103-113).
+
+    ``qkv (T, C)`` in the activation dtype; ``conv_state (N, K-1, C)`` (any
+    float dtype); ``conv_weight (C, K)``; ``cu_seqlens`` device int32 offsets
+    or None for N equal runs. Returns ``q, k (T, Hk, Dk)``, ``v (T, Hv, Dv)``
+    and the new conv state ``(N, K-1, C)`` in the activation dtype."""
+
+    device = _require_device(qkv, conv_state, conv_weight)
+    T, C = qkv.shape
+    N = conv_state.shape[0]
+    K = dims.conv_kernel_dim
+    if C != dims.conv_dim or tuple(conv_state.shape[1:]) != (K - 1, C):
+        raise ValueError("qkv/conv_state do not match the layer's conv_dim and kernel")
+    act = qkv.dtype
+    if act not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"activations must be float32 or bfloat16, got {act}")
+    qkv, conv_state = _c(qkv), _c(conv_state)
+    w = _c(conv_weight.float().reshape(C, K))
+    q = torch.empty((T, dims.num_key_heads, dims.key_head_dim), dtype=act, device=device)
+    k = torch.empty_like(q)
+    v = torch.empty((T, dims.num_value_heads, dims.value_head_dim), dtype=act, device=device)
+    new_conv = torch.empty((N, K - 1, C), dtype=act, device=device)
+    _lib.call("gdn_frontend", _lib.ptr(qkv), _lib.ptr(conv_state), _lib.ptr(new_conv),
+              _lib.dtype_code(conv_state.dtype), _lib.ptr(w), _lib.ptr(cu_seqlens), N, T,
+              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), dims.num_key_heads, dims.num_value_heads,
+              dims.key_head_dim, dims.value_head_dim, K, _lib.dtype_code(act), _stream(device))
+    return q, k, v, new_conv
+
+
+def _fused_decode_ok(dims: LinearAttentionDims, act: torch.dtype) -> bool:
+    return (dims.key_head_dim == dims.value_head_dim == 128 and dims.conv_kernel_dim == 4
+            and act in (torch.float32, torch.bfloat16))
+
+
+def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias,
+                      norm_weight, eps, dims: LinearAttentionDims, *, conv_out=None,
+                      state_out=None, y_dtype=None):
+    """One decode token for ``B`` sequences in a single kernel launch: conv +
+    SiLU + roll, q/k scaling, gates, recurrence and gated RMSNorm
+    (linear_attention.py:103-124 at L = 1).
+
+    ``qkv (B, C)``, ``z (B, Hv, Dv)`` or None, ``a, b (B, Hv)`` in the
+    activation dtype; ``conv_state (B, K-1, C)`` in the activation dtype;
+    ``ssm_state (B, Hv, Dv, Dk)`` float32. ``state_out`` may be ``ssm_state``
+    (in-place update); ``conv_out`` must be a different buffer. With ``z`` the
+    result is the gated-norm output in the activation dtype; without, the
+    recurrence output ``y`` in ``y_dtype`` (float32 by default).
+    Returns ``(out (B, Hv, Dv), conv_out, state_out)``."""
+
+    device = _require_device(qkv, z, a, b, conv_state, ssm_state)
+    B = qkv.shape[0]
+    act = qkv.dtype
+    if not _fused_decode_ok(dims, act):
+        raise ValueError("the fused decode kernel needs Dk = Dv = 128, K = 4 and float32 or "
+                         "bfloat16 activations")
+    if (tuple(qkv.shape) != (B, dims.conv_dim) or tuple(a.shape) != (B, dims.num_value_heads)
+            or b.shape != a.shape
+            or tuple(conv_state.shape) != (B, dims.conv_kernel_dim - 1, dims.conv_dim)
+            or tuple(ssm_state.shape) != (B, dims.num_value_heads, dims.value_head_dim,
+                                           dims.key_head_dim)
+            or (z is not None and tuple(z.shape) != (B, dims.num_value_heads, dims.value_head_dim))):
+        raise ValueError("fused_decode_step: inconsistent shapes")
+    if conv_state.dtype != act or a.dtype != act or b.dtype != act or (z is not None and z.dtype != act):
+        raise ValueError("qkv, z, a, b and conv_state must share the activation dtype")
+    if ssm_state.dtype != torch.float32 or not ssm_state.is_contiguous():
+        raise ValueError("ssm state must be contiguous float32")
+    qkv, a, b, conv_state = _c(qkv), _c(a), _c(b), _c(conv_state)
+    z = _c(z) if z is not None else None
+    conv_weight = _c(conv_weight.float().reshape(dims.conv_dim, dims.conv_kernel_dim))
+    A_log, dt_bias = _c(A_log.float()), _c(dt_bias.float())
+    norm_weight = _c(norm_weight.float()) if z is not None else None
+    if conv_out is None:
+        conv_out = torch.empty_like(conv_state)
+    if state_out is None:
+        state_out = torch.empty_like(ssm_state)
+    out_dtype = act if z is not None else (y_dtype or torch.float32)
+    out = torch.empty((B, dims.num_value_heads, dims.value_head_dim), dtype=out_dtype,
+                      device=device)
+    _lib.call("gdn_decode_step", _lib.ptr(qkv), _lib.ptr(conv_state), _lib.ptr(conv_out),
+              _lib.ptr(conv_weight), _lib.ptr(a), _lib.ptr(b), _lib.ptr(A_log),
+              _lib.ptr(dt_bias), _lib.ptr(ssm_state), _lib.ptr(state_out), _lib.ptr(z),
+              _lib.ptr(norm_weight), float(eps), _lib.ptr(out), _lib.dtype_code(out_dtype), B,
+              dims.num_key_heads, dims.num_value_heads, dims.key_head_dim, dims.value_head_dim,
+              dims.conv_kernel_dim, _lib.dtype_code(act), _stream(device))
+    return out, conv_out, state_out
+
+
+class Qwen3_5LinearAttention:
+    """The gated-delta layer. Weights are dense ``(out, in)`` matrices for the
+    projections, ``conv1d_weight (C, K, 1)``, ``A_log``, ``dt_bias``
+    ``(Hv,)`` and ``norm_weight (Dv,)`` (linear_attention.py:35-59)."""
+
+    def __init__(self, dims: LinearAttentionDims, in_proj_qkv, in_proj_z, in_proj_a, in_proj_b,
+                 conv1d_weight, A_log, dt_bias, norm_weight, out_proj,
+                 rms_norm_eps: float = 1e-6) -> None:
+        self.linear = dims
+        self.rms_norm_eps = rms_norm_eps
+        self.in_proj_qkv = in_proj_qkv
+        self.in_proj_z = in_proj_z
+        self.in_proj_a = in_proj_a
+        self.in_proj_b = in_proj_b
+        self.out_proj = out_proj
+        C, K = dims.conv_dim, dims.conv_kernel_dim
+        self.conv1d_weight = conv1d_weight.float().reshape(C, K).contiguous()
+        self.A_log = A_log.float().contiguous()
+        self.dt_bias = dt_bias.float().contiguous()
+        self.norm_weight = norm_weight.float().contiguous()
+
+    def new_cache(self, dtype: torch.dtype = torch.float32) -> RecurrentCache:
+        d = self.linear
+        return RecurrentCache(d.conv_kernel_dim, d.conv_dim, d.num_value_heads, d.value_head_dim,
+                              d.key_head_dim, dtype=dtype, device=self.A_log.device)
+
+    @staticmethod
+    def _proj(rows: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        if weight.dtype != rows.dtype:
+            weight = weight.to(rows.dtype)
+        return rows @ weight.T
+
+    def _project(self, rows: torch.Tensor):
+        d = self.linear
+        L = rows.shape[0]
+        qkv = self._proj(rows, self.in_proj_qkv)
+        z = self._proj(rows, self.in_proj_z).reshape(L, d.num_value_heads, d.value_head_dim)
+        a = self._proj(rows, self.in_proj_a)
+        b = self._proj(rows, self.in_proj_b)
+        return qkv, z, a, b
+
+    def core(self, qkv, z, a, b, conv_state, ssm_state, cu_seqlens=None):
+        """Everything between the projections for N packed runs (one run if
+        ``cu_seqlens`` is None): ``qkv (T, C)``, ``z (T, Hv, Dv)``,
+        ``a, b (T, Hv)``, ``conv_state (N, K-1, C)``, ``ssm_state (N, Hv, Dv, Dk)``.
+        Returns ``(out (T, Hv*Dv), new_conv, new_ssm)``."""
+
+        d = self.linear
+        T = qkv.shape[0]
+        cu_dev = None
+        if cu_seqlens is not None:
+            cu_dev = torch.as_tensor(cu_seqlens, dtype=torch.int32).to(qkv.device)
+        q, k, v, new_conv = conv_frontend(qkv, conv_state, self.conv1d_weight, d, cu_dev)
+        if cu_seqlens is None:
+            y, new_ssm = gated_delta_update(q[None], k[None], v[None], a[None], b[None],
+                                            self.A_log, self.dt_bias, ssm_state)
+            y = y[0]
+        else:
+            y, new_ssm = gated_delta_update(q, k, v, a, b, self.A_log, self.dt_bias, ssm_state,
+                                            cu_seqlens=cu_seqlens)
+        out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out_dtype=z.dtype)
+        return out.reshape(T, d.value_dim), new_conv, new_ssm
+
+    def __call__(self, x: torch.Tensor, cache: RecurrentCache) -> torch.Tensor:
+        """``x``: ``(hidden,)`` for one decode step or ``(L, hidden)`` for a
+        prompt; returns the same rank (linear_attention.py:81-127)."""
+
+        if x.ndim not in (1, 2):
+            raise ValueError(f"Qwen3_5LinearAttention expects 1-D or 2-D x, got shape {tuple(x.shape)}")
+        squeeze = x.ndim == 1
+        rows = x[None, :] if squeeze else x
+        L = rows.shape[0]
+        d = self.linear
+        qkv, z, a, b = self._project(rows)
+        conv_state, ssm_state = cache.state()
+        act = qkv.dtype
+        if L == 1 and _fused_decode_ok(d, act):
+            out, new_conv, new_ssm = self._decode_fused(qkv, z, a, b, conv_state[None].to(act),
+                                                        ssm_state[None], in_place=False)
+            out, new_conv, new_ssm = out.reshape(1, d.value_dim), new_conv[0], new_ssm[0]
+        else:
+            out, new_conv, new_ssm = self.core(qkv, z, a, b, conv_state[None], ssm_state[None])
+            new_conv, new_ssm = new_conv[0], new_ssm[0]
+        cache.update(new_conv, new_ssm, advance=L)
+        out = self._proj(out, self.out_proj)
+        return out[0] if squeeze else out
+
+    def _decode_fused(self, qkv, z, a, b, conv_state, ssm_state, in_place: bool,
+                      conv_out: torch.Tensor | None = None):
+        return fused_decode_step(qkv, z, a, b, conv_state, ssm_state, self.conv1d_weight,
+                                 self.A_log, self.dt_bias, self.norm_weight, self.rms_norm_eps,
+                                 self.linear, conv_out=conv_out,
+                                 state_out=ssm_state if in_place else None)
+
+    def decode_batch(self, x: torch.Tensor, pool: RecurrentStatePool) -> torch.Tensor:
+        """One decode token for each of the pool's ``B`` sequences: ``x (B, hidden)``
+        -> ``(B, hidden)``. The ssm slots are updated in place; the conv state
+        is double-buffered."""
+
+        if x.ndim != 2 or x.shape[0] != pool.batch:
+            raise ValueError("decode_batch expects x of shape (pool.batch, hidden)")
+        d = self.linear
+        qkv, z, a, b = self._project(x)
+        if not _fused_decode_ok(d, qkv.dtype) or pool.conv_state.dtype != qkv.dtype:
+            raise ValueError("decode_batch needs Dk = Dv = 128, K = 4 and a pool in the "
+                             "activation dtype (float32 or bfloat16)")
+        out, _, _ = self._decode_fused(qkv, z, a, b, pool.conv_state, pool.ssm_state,
+                                       in_place=True, conv_out=pool.conv_spare)
+        pool.swap_conv()
+        pool.size += 1
+        return self._proj(out.reshape(pool.batch, d.value_dim), self.out_proj)

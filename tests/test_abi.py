@@ -1,0 +1,67 @@
+"""The C-ABI library loads, exports every symbol include/gdn.h declares, and
+rejects invalid arguments before launching anything (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from mlx_lean_moe_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions() -> list[str]:
+    text = open(os.path.join(ROOT, "include", "gdn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s+\**\s*(gdn_[a-z_0-9]+)\s*\(", text, flags=re.M)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert len(declared) >= 9
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.EXPORTED), "ctypes signatures out of sync with gdn.h"
+
+
+def test_abi_version_and_single_hip_runtime():
+    lib = _lib.load()
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION
+    assert len(_lib._hip_runtimes_mapped()) == 1
+
+
+def _err(lib) -> str:
+    return lib.gdn_last_error().decode()
+
+
+def test_invalid_arguments_return_einval_without_launching():
+    lib = _lib.load()
+    # bad head ratio
+    rc = lib.gdn_scan(None, None, 0, None, 0, None, 0, None, 0, None, None, 0, None, 0, None, 1,
+                      4, 3, 4, 32, 8, None)
+    assert rc == _lib.GDN_EINVAL and "multiple" in _err(lib)
+    # bad dtype code
+    rc = lib.gdn_gates(None, None, 7, None, None, None, None, 0, 4, 2, None)
+    assert rc == _lib.GDN_EINVAL
+    # T not divisible by N without cu_seqlens
+    rc = lib.gdn_scan_reference(None, None, 0, None, 0, None, 0, None, 0, ctypes.c_void_p(16),
+                                ctypes.c_void_p(16), 0, None, 0, None, 3, 4, 1, 1, 32, 8, None)
+    assert rc == _lib.GDN_EINVAL and "divisible" in _err(lib)
+    # the fused decode kernel is specialised for Dk = Dv = 128
+    rc = lib.gdn_decode_step(*([None] * 12), 1e-6, None, 0, 1, 2, 4, 64, 64, 4, 1, None)
+    assert rc == _lib.GDN_EUNSUPPORTED
+    # overlapping conv state buffers are rejected
+    p = ctypes.c_void_p(4096)
+    rc = lib.gdn_frontend(p, p, p, 1, p, None, 1, 1, p, p, p, 1, 2, 32, 32, 4, 1, None)
+    assert rc == _lib.GDN_EINVAL and "overlaps" in _err(lib)
+
+
+def test_empty_work_is_a_no_op():
+    lib = _lib.load()
+    assert lib.gdn_gates(None, None, 0, None, None, None, None, 0, 0, 4, None) == 0
+    assert lib.gdn_gated_rmsnorm(None, 0, None, 0, None, 1e-6, None, 0, 0, 8, None) == 0

@@ -1,0 +1,160 @@
+"""GPU parity of the fused decode kernel, the prefill front-end and the
+gated RMSNorm against the oracle (seeded inputs, production head shape)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mlx_lean_moe_amd as gdn
+from oracle import cref
+from oracle import gated_delta_ref as R
+from tests.helpers import layer_inputs, layer_params, max_rel
+
+pytestmark = pytest.mark.gpu
+
+DIMS_PROD = gdn.LinearAttentionDims(16, 32, 128, 128, 4)
+
+
+def _dims_tuple(d):
+    return (d.num_key_heads, d.num_value_heads, d.key_head_dim, d.value_head_dim)
+
+
+def _t(x, dev, dtype=torch.float32):
+    return torch.tensor(np.asarray(x, np.float32), device=dev).to(dtype)
+
+
+def _decode_case(seed, dims, B, act_bf16):
+    rng = np.random.default_rng(seed)
+    dt = _dims_tuple(dims)
+    conv_w, A_log, dt_bias, norm_w = layer_params(rng, dt)
+    qkv, z, a, b = layer_inputs(rng, dt, L=1, act_bf16=act_bf16, B=B)
+    conv = rng.standard_normal((B, 3, dims.conv_dim)).astype(np.float32)
+    if act_bf16:
+        conv = R.bf16_round(conv)
+    state = (rng.standard_normal((B,) + (dims.num_value_heads, 128, 128)) * 0.05).astype(np.float32)
+    return dict(qkv=qkv[:, 0], z=z[:, 0], a=a[:, 0], b=b[:, 0], conv=conv, state=state,
+                conv_w=conv_w, A_log=A_log, dt_bias=dt_bias, norm_w=norm_w)
+
+
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+@pytest.mark.parametrize("with_z", [False, True])
+def test_fused_decode_matches_oracle(gpu, act, with_z):
+    dims = gdn.LinearAttentionDims(2, 4, 128, 128, 4)
+    B = 3
+    c = _decode_case(0, dims, B, act == "bf16")
+    adt = torch.bfloat16 if act == "bf16" else torch.float32
+    out, conv_out, state_out = gdn.fused_decode_step(
+        _t(c["qkv"], gpu, adt), _t(c["z"], gpu, adt) if with_z else None, _t(c["a"], gpu, adt),
+        _t(c["b"], gpu, adt), _t(c["conv"], gpu, adt), _t(c["state"], gpu), _t(c["conv_w"], gpu),
+        _t(c["A_log"], gpu), _t(c["dt_bias"], gpu), _t(c["norm_w"], gpu), 1e-6, dims)
+    oracle_act = "bf16" if act == "bf16" else None
+    for i in range(B):
+        ycore = R.linear_attention_core(c["qkv"][i:i + 1], c["z"][i:i + 1], c["a"][i:i + 1],
+                                        c["b"][i:i + 1], c["conv"][i], c["state"][i],
+                                        c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"],
+                                        _dims_tuple(dims), 1e-6, oracle_act)
+        o, nc, ns = ycore
+        assert max_rel(state_out[i].cpu().numpy(), ns) < 1e-5
+        np.testing.assert_array_equal(conv_out[i].float().cpu().numpy(), nc)
+        if with_z:
+            tol = 2e-2 if act == "bf16" else 1e-4
+            np.testing.assert_allclose(out[i].float().cpu().numpy().reshape(-1), o.reshape(-1),
+                                       atol=tol)
+    if not with_z:
+        # y itself: the recurrence output before the norm
+        q, k, v = _frontend_oracle(c, dims, oracle_act)
+        g = R.forget_gate(c["a"], c["A_log"], c["dt_bias"])
+        beta = R.beta_gate(c["b"], oracle_act)
+        for i in range(B):
+            y, _ = R.gated_delta_scan_ops(q[i:i + 1], k[i:i + 1], v[i:i + 1], g[i:i + 1],
+                                          beta[i:i + 1], c["state"][i])
+            np.testing.assert_allclose(out[i].cpu().numpy(), y[0], rtol=1e-4, atol=1e-5)
+
+
+def _frontend_oracle(c, dims, act):
+    Hk, Hv, Dk, Dv = _dims_tuple(dims)
+    qs, ks, vs = [], [], []
+    for i in range(c["qkv"].shape[0]):
+        out, _ = R.convolve(c["qkv"][i:i + 1], c["conv"][i], c["conv_w"], act)
+        q = out[:, :Hk * Dk].reshape(1, Hk, Dk)
+        k = out[:, Hk * Dk:2 * Hk * Dk].reshape(1, Hk, Dk)
+        q, k = R.qk_scale(q, k, act)
+        qs.append(q[0])
+        ks.append(k[0])
+        vs.append(out[0, 2 * Hk * Dk:].reshape(Hv, Dv))
+    return np.stack(qs), np.stack(ks), np.stack(vs)
+
+
+@pytest.mark.parametrize("with_z", [False, True])
+def test_fused_decode_production_shape_matches_c_oracle_over_steps(gpu, with_z):
+    """B=8 sequences, Hk=16/Hv=32, four chained decode steps with the state
+    updated in place (the decode loop's own pattern) against the C oracle."""
+
+    B = 8
+    dims = DIMS_PROD
+    c = _decode_case(1, dims, B, True)
+    adt = torch.bfloat16
+    rng = np.random.default_rng(2)
+    state_dev = _t(c["state"], gpu)
+    conv_dev = _t(c["conv"], gpu, adt)
+    conv_spare = torch.empty_like(conv_dev)
+    state_ref, conv_ref = c["state"].copy(), c["conv"].copy()
+    params = [_t(c[n], gpu) for n in ("conv_w", "A_log", "dt_bias", "norm_w")]
+    for step in range(4):
+        qkv, z, a, b = layer_inputs(rng, _dims_tuple(dims), L=1, act_bf16=True, B=B)
+        out, _, _ = gdn.fused_decode_step(
+            _t(qkv[:, 0], gpu, adt), _t(z[:, 0], gpu, adt) if with_z else None,
+            _t(a[:, 0], gpu, adt), _t(b[:, 0], gpu, adt), conv_dev, state_dev, *params, 1e-6,
+            dims, conv_out=conv_spare, state_out=state_dev)
+        conv_dev, conv_spare = conv_spare, conv_dev
+        out_ref, conv_ref, state_ref = cref.decode_step(
+            qkv[:, 0], conv_ref, c["conv_w"], a[:, 0], b[:, 0], c["A_log"], c["dt_bias"],
+            state_ref, z[:, 0] if with_z else None, c["norm_w"], 1e-6, _dims_tuple(dims), True)
+        tol = 2e-2 if with_z else 1e-4
+        np.testing.assert_allclose(out.float().cpu().numpy(), out_ref, atol=tol, rtol=tol)
+        np.testing.assert_array_equal(conv_dev.float().cpu().numpy(), conv_ref)
+    assert max_rel(state_dev.cpu().numpy(), state_ref) < 1e-4
+
+
+def test_frontend_matches_oracle_varlen_with_short_runs(gpu):
+    dims = gdn.LinearAttentionDims(2, 4, 32, 32, 4)
+    rng = np.random.default_rng(4)
+    lens = [1, 0, 2, 9, 5]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T, C = int(cu[-1]), dims.conv_dim
+    qkv = R.bf16_round(rng.standard_normal((T, C)))
+    conv = rng.standard_normal((len(lens), 3, C)).astype(np.float32)  # float32 state in
+    w = (rng.standard_normal((C, 4)) * 0.2).astype(np.float32)
+    q, k, v, new_conv = gdn.conv_frontend(_t(qkv, gpu, torch.bfloat16), _t(conv, gpu), _t(w, gpu),
+                                          dims, torch.tensor(cu, device=gpu))
+    assert new_conv.dtype == torch.bfloat16
+    for i in range(len(lens)):
+        s0, s1 = cu[i], cu[i + 1]
+        out, nc = R.convolve(qkv[s0:s1], conv[i], w, "bf16")
+        np.testing.assert_array_equal(new_conv[i].float().cpu().numpy(), nc)
+        if s1 == s0:
+            continue
+        qe = out[:, :64].reshape(-1, 2, 32)
+        ke = out[:, 64:128].reshape(-1, 2, 32)
+        qe, ke = R.qk_scale(qe, ke, "bf16")
+        np.testing.assert_allclose(q[s0:s1].float().cpu().numpy(), qe, atol=2e-3, rtol=1e-2)
+        np.testing.assert_allclose(k[s0:s1].float().cpu().numpy(), ke, atol=2e-3, rtol=1e-2)
+        # fp32 vs fp64 accumulation may move a value across a bf16 rounding boundary
+        np.testing.assert_allclose(v[s0:s1].float().cpu().numpy(), out[:, 128:].reshape(-1, 4, 32),
+                                   rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_rms_norm_matches_oracle(gpu, dtype):
+    rng = np.random.default_rng(6)
+    y = rng.standard_normal((5, 4, 128)).astype(np.float32)
+    z = R.bf16_round(rng.standard_normal((5, 4, 128)))
+    w = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    out = gdn.gated_rms_norm(_t(y, gpu), _t(z, gpu, dtype), _t(w, gpu), 1e-6, out_dtype=dtype)
+    act = "bf16" if dtype == torch.bfloat16 else None
+    expected = R.gated_rms_norm(R.act_round(y, act), z, w, 1e-6, act)
+    assert out.dtype == dtype
+    tol = 2e-2 if act else 1e-5
+    np.testing.assert_allclose(out.float().cpu().numpy(), expected, atol=tol, rtol=tol)

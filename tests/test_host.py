@@ -1,0 +1,94 @@
+"""Host-side behaviour of the Python surface without a GPU: shape errors are
+ValueError before any kernel call (as tests/test_gated_delta_metal.py:137-156
+requires of the reference), and CPU tensors are refused loudly."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mlx_lean_moe_amd as gdn
+from mlx_lean_moe_amd import _lib, gated_delta
+from oracle.gated_delta_ref import metal_test_inputs
+
+
+@pytest.fixture
+def no_launch(monkeypatch):
+    def unexpected(*args):
+        pytest.fail("a kernel was reached")
+
+    monkeypatch.setattr(_lib, "call", unexpected)
+
+
+def _inputs(n=5):
+    return [torch.tensor(a) for a in metal_test_inputs(n)]
+
+
+@pytest.mark.parametrize("invalid", ["k", "v", "g", "beta", "state", "heads", "empty"])
+def test_invalid_shapes_are_rejected_before_kernel_dispatch(invalid, no_launch):
+    inputs = _inputs()
+    index = {"k": 1, "v": 2, "g": 3, "beta": 4, "state": 5}
+    if invalid in index:
+        inputs[index[invalid]] = inputs[index[invalid]][:1]
+    elif invalid == "heads":
+        inputs[0] = inputs[0][:, :1].repeat_interleave(3, dim=1)
+        inputs[1] = inputs[0]
+    else:
+        inputs = [a[:0] for a in inputs[:-1]] + inputs[-1:]
+    with pytest.raises(ValueError):
+        gdn.gated_delta_scan(*inputs)
+
+
+def test_cpu_tensors_are_refused(no_launch):
+    with pytest.raises(RuntimeError, match="ROCm"):
+        gdn.gated_delta_scan(*_inputs())
+
+
+@pytest.mark.parametrize("bad", ["a_shape", "A_log", "heads", "state", "cu_order", "cu_end"])
+def test_update_shape_errors(bad, no_launch):
+    q = torch.zeros(2, 3, 2, 16)
+    k, v = q.clone(), torch.zeros(2, 3, 4, 8)
+    a = b = torch.zeros(2, 3, 4)
+    A_log = dt = torch.zeros(4)
+    state = None
+    cu = None
+    if bad == "a_shape":
+        a = torch.zeros(2, 3, 5)
+    elif bad == "A_log":
+        A_log = torch.zeros(3)
+    elif bad == "heads":
+        v = torch.zeros(2, 3, 3, 8)
+        a = b = torch.zeros(2, 3, 3)
+        A_log = dt = torch.zeros(3)
+    elif bad == "state":
+        state = torch.zeros(2, 4, 8, 8)
+    else:
+        q, k, v = q[0], k[0], v[0]
+        a = b = a[0]
+        cu = [0, 2, 1, 3] if bad == "cu_order" else [0, 2]
+    with pytest.raises(ValueError):
+        gdn.gated_delta_update(q, k, v, a, b, A_log, dt, state, cu_seqlens=cu)
+
+
+def test_layer_rejects_bad_rank(no_launch):
+    dims = gdn.LinearAttentionDims(2, 4, 32, 32, 4)
+    C = dims.conv_dim
+    layer = gdn.Qwen3_5LinearAttention(
+        dims, torch.zeros(C, 16), torch.zeros(128, 16), torch.zeros(4, 16), torch.zeros(4, 16),
+        torch.zeros(C, 4, 1), torch.zeros(4), torch.zeros(4), torch.ones(32), torch.zeros(16, 128))
+    with pytest.raises(ValueError):
+        layer(torch.zeros(2, 2, 16), None)
+
+
+def test_dims_mirror_the_reference_dataclass():
+    d = gdn.QWEN3_5_LINEAR
+    assert (d.key_dim, d.value_dim, d.conv_dim) == (2048, 4096, 8192)
+
+
+def test_promotion_matches_reference_ops_dtypes():
+    f32, bf16, f16 = torch.float32, torch.bfloat16, torch.float16
+    t = lambda dt: torch.zeros(1, dtype=dt)
+    assert gated_delta._promote(t(bf16), t(bf16), t(f16)) == f32
+    assert gated_delta._promote(t(bf16), t(bf16)) == bf16
+    assert gated_delta._promote(t(bf16), t(f32)) == f32
