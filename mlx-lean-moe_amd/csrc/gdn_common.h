@@ -12,6 +12,9 @@ namespace gdn {
 
 constexpr int kWave = 64;
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
 // ---------------------------------------------------------------------------
 // storage formats
 // ---------------------------------------------------------------------------
@@ -20,12 +23,8 @@ constexpr int kWave = 64;
 // the rounding is exactly the one the CPU oracle applies.
 GDN_DEV float bf16_bits_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
 
-GDN_DEV uint16_t f32_to_bf16_bits(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return uint16_t((u >> 16) | 0x40u);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
-}
+// Round-to-nearest-even float32 -> bfloat16 (gfx950's v_cvt_pk_bf16_f32).
+GDN_DEV uint16_t f32_to_bf16_bits(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
 
 GDN_DEV float round_bf16(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
 
@@ -100,6 +99,19 @@ GDN_DEV float log_forget_gate(float a, float A_log, float dt_bias) {
 // ---------------------------------------------------------------------------
 // cross-lane reductions
 // ---------------------------------------------------------------------------
+
+// Per-lane choice between two values by an all-ones / all-zeros mask. The
+// mask is hidden from the optimiser so that a choice between two elements of
+// a register array is not rewritten into a dynamically indexed array.
+GDN_DEV uint32_t opaque_mask(bool take_first) {
+    uint32_t m = take_first ? 0xFFFFFFFFu : 0u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
+GDN_DEV float mask_select(uint32_t m, float a, float b) {
+    return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+}
 
 template <int WIDTH>
 GDN_DEV float group_sum(float x) {

@@ -30,6 +30,30 @@ constexpr int kDecodeThreads = 256;
 constexpr int kD = 128;   // Dk = Dv
 constexpr int kTaps = 4;  // conv kernel K
 
+#ifndef GDN_DECODE_NT
+#define GDN_DECODE_NT 1
+#endif
+
+// The state is streamed exactly once per launch: optionally mark its loads
+// and stores non-temporal.
+GDN_DEV float4 load_state(const float4* p) {
+#if GDN_DECODE_NT
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v[0], v[1], v[2], v[3]);
+#else
+    return *p;
+#endif
+}
+
+GDN_DEV void store_state(float4* p, float4 v) {
+#if GDN_DECODE_NT
+    const f32x4 x = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(p));
+#else
+    *p = v;
+#endif
+}
+
 // Sum `vals` (32 per lane) over the 32 lanes of each half-wave, leaving the
 // total of original index (lane % 32) in vals[0].
 GDN_DEV void reduce_scatter32(float (&vals)[32], int l32) {
@@ -37,36 +61,49 @@ GDN_DEV void reduce_scatter32(float (&vals)[32], int l32) {
     for (int step = 0; step < 5; ++step) {
         const int off = 16 >> step;
         const int n = 32 >> step;
-        const bool upper = (l32 & off) != 0;
+        const uint32_t upper = opaque_mask((l32 & off) != 0);
 #pragma unroll
         for (int j = 0; j < n / 2; ++j) {
-            const float keep = upper ? vals[j + n / 2] : vals[j];
-            const float send = upper ? vals[j] : vals[j + n / 2];
+            const float keep = mask_select(upper, vals[j + n / 2], vals[j]);
+            const float send = mask_select(upper, vals[j], vals[j + n / 2]);
             vals[j] = keep + __shfl_xor(send, off, kWave);
         }
     }
 }
 
+// One conv channel's inputs: its K = 4 weights, the three conv-state taps and
+// the current token.
+struct ConvTaps {
+    float4 w;
+    float x0, x1, x2, x3;
+};
+
 template <class Act>
-GDN_DEV float conv_channel(const typename Act::storage* __restrict__ x,
+GDN_DEV ConvTaps load_taps(const typename Act::storage* __restrict__ x,
                            const typename Act::storage* __restrict__ cs,
                            const float4* __restrict__ w4, int C, int c) {
-    const float4 w = w4[c];
-    float acc = Act::round(w.x) * Act::load(cs, c);
-    acc += Act::round(w.y) * Act::load(cs, C + c);
-    acc += Act::round(w.z) * Act::load(cs, 2 * C + c);
-    acc += Act::round(w.w) * Act::load(x, c);
+    return {w4[c], Act::load(cs, c), Act::load(cs, C + c), Act::load(cs, 2 * C + c),
+            Act::load(x, c)};
+}
+
+// conv (cross-correlation, last tap on the current token) + SiLU, with the
+// weights and the result held in the activation dtype.
+template <class Act>
+GDN_DEV float conv_silu(const ConvTaps& t) {
+    float acc = Act::round(t.w.x) * t.x0;
+    acc += Act::round(t.w.y) * t.x1;
+    acc += Act::round(t.w.z) * t.x2;
+    acc += Act::round(t.w.w) * t.x3;
     acc = Act::round(acc);
     return Act::round(silu(acc));
 }
 
+// New conv state of a channel: the last K - 1 = 3 inputs.
 template <class Act>
-GDN_DEV void roll_channel(const typename Act::storage* __restrict__ x,
-                          const typename Act::storage* __restrict__ cs,
-                          typename Act::storage* __restrict__ cso, int C, int c) {
-    cso[c] = cs[C + c];
-    cso[C + c] = cs[2 * C + c];
-    cso[2 * C + c] = x[c];
+GDN_DEV void roll_taps(const ConvTaps& t, typename Act::storage* __restrict__ cso, int C, int c) {
+    Act::store(cso, c, t.x1);
+    Act::store(cso, C + c, t.x2);
+    Act::store(cso, 2 * C + c, t.x3);
 }
 
 template <class Act, bool kNorm>
@@ -87,32 +124,38 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const int tid = threadIdx.x;
     const int w = tid >> 6, l = tid & 63, half = l >> 5, l32 = l & 31;
 
-    // A. state tile loads, issued before anything else.
-    const float4* Sb = reinterpret_cast<const float4*>(S_in + size_t(bh) * kD * kD);
-    float4 s[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = Sb[(8 * i + 2 * w + half) * (kD / 4) + l32];
-
-    // B. front-end for this head's channels.
+    // A. the front-end's few inputs first, then the 16 float4 state loads:
+    // waiting for the former does not wait for the latter.
     const typename Act::storage* x = qkv + size_t(b) * C;
     const typename Act::storage* cs = cs_in + size_t(b) * (kTaps - 1) * C;
     typename Act::storage* cso = cs_out + size_t(b) * (kTaps - 1) * C;
     const float4* w4 = reinterpret_cast<const float4*>(conv_w);
-    {
-        const int e = tid & (kD - 1);
-        const int c = (tid < kD ? 0 : Hk * kD) + hk * kD + e;
-        (tid < kD ? qs : ks)[e] = conv_channel<Act>(x, cs, w4, C, c);
-        // q/k channels are shared by the r value heads of a key head: the
-        // first of them rolls their conv state.
-        if (h % r == 0) roll_channel<Act>(x, cs, cso, C, c);
-    }
+    const int e = tid & (kD - 1);
+    // pass 1: q channel (tid < 128) or k channel (tid >= 128) of key head hk;
+    // pass 2: v channel of value head h (tid < 128).
+    const int c1 = (tid < kD ? 0 : Hk * kD) + hk * kD + e;
+    const int c2 = 2 * Hk * kD + h * kD + e;
+    // (unconditional, so no branch forces a wait before the state loads)
+    const ConvTaps t1 = load_taps<Act>(x, cs, w4, C, c1);
+    const ConvTaps t2 = load_taps<Act>(x, cs, w4, C, c2);
+    const float av = Act::load(a_in, bh), bv = Act::load(b_in, bh);
+    const float alog = A_log[h], dtb = dt_bias[h];
+
+    const float4* Sb = reinterpret_cast<const float4*>(S_in + size_t(bh) * kD * kD);
+    float4 s[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = load_state(&Sb[(8 * i + 2 * w + half) * (kD / 4) + l32]);
+
+    // B. front-end for this head's channels.
+    (tid < kD ? qs : ks)[e] = conv_silu<Act>(t1);
+    // q/k channels are shared by the r value heads of a key head: the first
+    // of them rolls their conv state.
+    if (h % r == 0) roll_taps<Act>(t1, cso, C, c1);
     if (tid < kD) {
-        const int c = 2 * Hk * kD + h * kD + tid;
-        vs[tid] = conv_channel<Act>(x, cs, w4, C, c);
-        roll_channel<Act>(x, cs, cso, C, c);
+        vs[e] = conv_silu<Act>(t2);
+        roll_taps<Act>(t2, cso, C, c2);
     } else if (tid == kD) {
-        const float av = Act::load(a_in, bh), bv = Act::load(b_in, bh);
-        gate_g = expf(log_forget_gate(av, A_log[h], dt_bias[h]));
+        gate_g = expf(log_forget_gate(av, alog, dtb));
         gate_beta = Act::round(sigmoid(bv));
     }
     __syncthreads();
@@ -166,7 +209,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
         o.y = g * s[i].y + d * kk.y;
         o.z = g * s[i].z + d * kk.z;
         o.w = g * s[i].w + d * kk.w;
-        So[row * (kD / 4) + l32] = o;
+        store_state(&So[row * (kD / 4) + l32], o);
     }
 
     // I. output: y, or the gated RMSNorm of y held in the activation dtype.
