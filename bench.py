@@ -147,6 +147,67 @@ def bench_decode(dev, B, Hk, Hv, with_z, steps, warmup):
     }
 
 
+def prefill_flops(T, Hv, d=128, chunk=64):
+    """Algorithmic flops of the chunked prefill: the GEMMs K K^T, Q K^T,
+    T(beta K), T(beta V), (Q K^T o M) U', W S, Q S and K^T U' per token
+    (the triangular solve excluded)."""
+
+    return T * Hv * (10 * chunk * d + 6 * d * d)
+
+
+class PrefillWorkload:
+    """Synthetic chunked-prefill inputs resident in HBM: N runs of L tokens,
+    bf16 q/k/v (q, k L2-normalised), bf16 a/b, zero initial state; y in bf16."""
+
+    def __init__(self, dev, N, L, Hk, Hv, seed=0):
+        d = 128
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        T = N * L
+        randn = lambda *s: torch.randn(*s, generator=g, device=dev)
+        q = randn(T, Hk, d)
+        k = randn(T, Hk, d)
+        self.q = (q / q.norm(dim=-1, keepdim=True) / d ** 0.5).to(bf)
+        self.k = (k / k.norm(dim=-1, keepdim=True)).to(bf)
+        self.v = randn(T, Hv, d).to(bf)
+        self.a = randn(T, Hv).to(bf)
+        self.b = randn(T, Hv).to(bf)
+        self.A_log = torch.rand(Hv, generator=g, device=dev) * float(np.log(16))
+        self.dt_bias = torch.rand(Hv, generator=g, device=dev) * 2 - 1
+        self.state_out = torch.empty(N, Hv, d, d, device=dev)
+        self.y = torch.empty(T, Hv, d, dtype=bf, device=dev)
+        nbytes = gated_delta.prefill_workspace_bytes(N, T, Hk, Hv, d, d)
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        self.T, self.flops = T, prefill_flops(T, Hv)
+        from mlx_lean_moe_amd import _lib
+
+        self._fn = _lib.load().gdn_prefill_chunked
+        self._args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.a.data_ptr(),
+                      self.b.data_ptr(), _lib.GDN_BF16, self.A_log.data_ptr(),
+                      self.dt_bias.data_ptr(), 0, None, self.state_out.data_ptr(),
+                      self.y.data_ptr(), _lib.GDN_BF16, None, N, T, Hk, Hv, d, d,
+                      self.ws.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)
+
+    def step(self, s):
+        rc = self._fn(*self._args)
+        if rc != 0:
+            raise RuntimeError(f"gdn_prefill_chunked failed with {rc}")
+
+
+def bench_prefill(dev, N, L, Hk, Hv, steps, warmup):
+    w = PrefillWorkload(dev, N, L, Hk, Hv)
+    total_ms, launch_ms = time_steps(w.step, steps, warmup)
+    tflops = w.flops / (launch_ms * 1e-3) / 1e12
+    return {
+        "tokens_per_s": w.T * steps / (total_ms * 1e-3),
+        "ms_per_step": total_ms / steps,
+        "call_us": launch_ms * 1e3,
+        "flops_per_call": w.flops,
+        "tflops": tflops,
+        "mfma_frac": tflops / BF16_PEAK_TFLOPS,
+    }
+
+
 def cpu_baseline_decode(B, Hk, Hv, budget_s=10.0):
     """The C restatement of the reference's decode path (fused front-end +
     recurrence, float32, OpenMP over (sequence, head)) timed on the host on a
@@ -264,11 +325,33 @@ def main(argv=None):
             line["cpu_baseline"] = cpu_baseline_decode(B, Hk, Hv, budget_s=10.0)
         if not args.no_also and not big:
             lg = bench_decode(dev, 256, 16, 64, True, steps=64, warmup=8)
-            line["also"] = {"decode_large": {
-                "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
-                "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],
-                "hbm_gbs": lg["hbm_gbs"], "hbm_frac": lg["hbm_frac"]}}
+            pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
+            line["also"] = {
+                "decode_large": {
+                    "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
+                    "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],
+                    "hbm_gbs": lg["hbm_gbs"], "hbm_frac": lg["hbm_frac"]},
+                "prefill": {
+                    "workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64, bf16 MFMA",
+                    "tokens_per_s": pf["tokens_per_s"], "call_us": pf["call_us"],
+                    "tflops": pf["tflops"], "mfma_frac": pf["mfma_frac"],
+                    "flops_per_call": pf["flops_per_call"]}}
         print(json.dumps(line))
+        return 0
+
+    if args.workload == "prefill":
+        r = bench_prefill(dev, 1, 4096, 16, 32, args.steps, args.warmup)
+        print(json.dumps({"metric": METRIC, "value": r["tokens_per_s"], "unit": "tokens/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["ms_per_step"], "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic",
+                          "config": {"workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64"},
+                          "roofline": {"bound": "mfma", "achieved": r["tflops"],
+                                       "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": r["mfma_frac"], "traffic": None,
+                                       "kernel": "gdn_prefill_chunked (3 launches)",
+                                       "call_us": r["call_us"]}}))
         return 0
 
     raise SystemExit(f"workload {args.workload} is not available in this build")

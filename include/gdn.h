@@ -141,10 +141,12 @@ int gdn_decode_step(const void *qkv, const void *conv_state_in, void *conv_state
  * gdn_prefill_chunked - chunked (WY/UT, 64-token chunks) prefill on bf16
  * MFMA with float32 accumulation, for N packed runs.
  *   q, k: (T_total, Hk, Dk) bf16;  v: (T_total, Hv, Dv) bf16
- *   gate_mode 0: ga = a (T_total, Hv) bf16, gb = b (T_total, Hv) bf16, with A_log and
- *                dt_bias (Hv) float32 (gates computed in-kernel)
+ *   gate_mode 0: ga = a, gb = b, both (T_total, Hv) in gb_dtype, with A_log and
+ *                dt_bias (Hv) float32 (gates computed in-kernel, beta held in gb_dtype)
  *   gate_mode 1: ga = g (T_total, Hv) float32, gb = beta (T_total, Hv) gb_dtype
- *   state_in: (N, Hv, Dv, Dk) float32 or NULL (zero state); state_out: (N, Hv, Dv, Dk)
+ *   state_in: (N, Hv, Dv, Dk) float32 or NULL (zero state); state_out: (N, Hv, Dv, Dk),
+ *             not aliasing state_in
+ *   Hv / Hk <= 8; q, k, states and workspace 16-byte aligned
  *   y: (T_total, Hv, Dv) y_dtype
  *   workspace: device scratch of gdn_prefill_workspace_size(...) bytes
  * Specialised for Dk = Dv = 128. Equal, up to rounding, to gdn_scan on the

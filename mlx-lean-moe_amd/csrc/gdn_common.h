@@ -14,6 +14,7 @@ constexpr int kWave = 64;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 // ---------------------------------------------------------------------------
 // storage formats
@@ -78,6 +79,14 @@ struct ActBF16 {
     static GDN_DEV float load(const storage* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
     static GDN_DEV void store(storage* p, int64_t i, float x) { p[i] = f32_to_bf16_bits(x); }
     static GDN_DEV float round(float x) { return round_bf16(x); }
+};
+
+struct ActF16 {
+    using storage = uint16_t;
+    static constexpr int code = GDN_F16;
+    static GDN_DEV float load(const storage* p, int64_t i) { return f16_bits_to_f32(p[i]); }
+    static GDN_DEV void store(storage* p, int64_t i, float x) { p[i] = f32_to_f16_bits(x); }
+    static GDN_DEV float round(float x) { return f16_bits_to_f32(f32_to_f16_bits(x)); }
 };
 
 // ---------------------------------------------------------------------------

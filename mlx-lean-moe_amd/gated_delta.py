@@ -29,7 +29,6 @@ from . import _lib
 # Token runs at least this long (bf16, Dk = Dv = 128) take the chunked MFMA
 # prefill instead of the sequential scan.
 PREFILL_MIN_TOKENS = 64
-_PREFILL_BUILT = False
 
 
 def _promote(*tensors: torch.Tensor) -> torch.dtype:
@@ -150,9 +149,10 @@ def _launch_prefill(q, k, v, ga, gb, A_log, dt_bias, gate_mode, state_in, state_
               _lib.ptr(workspace), workspace.numel(), _stream(device))
 
 
-def _prefill_eligible(q, k, v, min_tokens_per_run: float) -> bool:
-    return (_PREFILL_BUILT and q.dtype == k.dtype == v.dtype == torch.bfloat16 and q.shape[-1] == 128
-            and v.shape[-1] == 128 and min_tokens_per_run >= PREFILL_MIN_TOKENS)
+def _prefill_eligible(q, k, v, tokens_per_run: float) -> bool:
+    return (q.dtype == k.dtype == v.dtype == torch.bfloat16 and q.shape[-1] == 128
+            and v.shape[-1] == 128 and q.shape[-2] * 8 >= v.shape[-2]
+            and tokens_per_run >= PREFILL_MIN_TOKENS)
 
 
 # ---------------------------------------------------------------------------
@@ -168,8 +168,8 @@ def gated_delta_scan(q, k, v, g, beta, state, *, use_kernel: bool = True):
     to. The input state is never modified.
 
     ``use_kernel=True`` picks the register-resident scan (``Dk`` in
-    {32, 64, 128, 256}) or, for bf16 runs of at least ``PREFILL_MIN_TOKENS``
-    tokens with ``Dk = Dv = 128``, the chunked MFMA prefill;
+    {32, 64, 128, 256}) or, for bf16 q/k/v with ``Dk = Dv = 128`` and at
+    least ``PREFILL_MIN_TOKENS`` tokens, the chunked MFMA prefill;
     ``use_kernel=False`` (or any other ``Dk``) runs the plain per-row kernel."""
 
     _check_scan_shapes(q, k, v, g, beta, state)
@@ -247,11 +247,11 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
         T = q.shape[0]
         offsets = _check_cu_seqlens(cu_seqlens, T)
         N = len(offsets) - 1
-        min_run = min(b_ - a_ for a_, b_ in zip(offsets, offsets[1:]))
+        mean_run = T / N
     else:
         N, L = q.shape[:2]
         T = N * L
-        min_run = L
+        mean_run = L
     if N == 0:
         raise ValueError("gated_delta_update needs at least one sequence")
     if state is not None and tuple(state.shape) != (N, Hv, Dv, Dk):
@@ -270,7 +270,7 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
     state_out = torch.empty((N, Hv, Dv, Dk), dtype=s_dtype, device=device)
     if T > 0:
         if (use_kernel and s_dtype == torch.float32 and a.dtype == b.dtype == torch.bfloat16
-                and _prefill_eligible(q, k, v, min_run)):
+                and _prefill_eligible(q, k, v, mean_run)):
             _launch_prefill(q, k, v, a, b, _c(A_log.float()), _c(dt_bias.float()), 0, state_in,
                             state_out, y, cu, N, T, Hk, Hv, Dk, Dv, device)
         else:
