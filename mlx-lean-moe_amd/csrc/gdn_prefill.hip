@@ -13,17 +13,16 @@
 // Two kernels:
 //   chunk pass (parallel over chunks x key heads): K K^T and Q K^T on MFMA,
 //     the gates, the blocked triangular inverse, and per value head the
-//     records Tb (bf16 hi + lo) and P = lower(Q K^T o G) (bf16) plus l.
+//     records Tb and P = lower(Q K^T o G) (each bf16 hi + lo) plus l.
 //   state pass (per run x value head x 16-row slice of the state, sequential
 //     over the run's chunks): K S^T and Q S^T, Tb R, P D and the state update
 //     on MFMA, the state tile resident in accumulators.
 //
 // Operands that are exact in bf16 (q, k, v) enter the MFMAs as they are;
-// float32 operands are split into a bf16 high part and a bf16 residual, with
-// the residual products added (S in K S^T, Tb and R in Tb R, D in the state
-// update), which keeps the state within 1e-5 relative of the sequential
-// recurrence; Q S^T and P D feed only the output and take S and D in one
-// bf16 part.
+// float32 operands (S, Tb, R, P, D) are split into a bf16 high part and a
+// bf16 residual, with the residual products added (hi.hi + hi.lo + lo.hi),
+// which keeps state and output within ~1e-5 relative of the sequential
+// recurrence.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+j],
 // B[8(l/16)+j][l%16] (j = 0..7) and D[4(l/16)+i][l%16] (i = 0..3).
@@ -41,8 +40,9 @@ constexpr float kLogGateFloor = -80.f;   // exp(-80) ~ 1.8e-35: a reset state
 
 // Per (chunk, value head) record written by the chunk pass.
 constexpr int64_t kMatBytes = int64_t(kChunk) * kChunk * 2;
-constexpr int64_t kRecTbHi = 0, kRecTbLo = kMatBytes, kRecP = 2 * kMatBytes, kRecL = 3 * kMatBytes;
-constexpr int64_t kRecBytes = 3 * kMatBytes + kChunk * 4;
+constexpr int64_t kRecTbHi = 0, kRecTbLo = kMatBytes, kRecPHi = 2 * kMatBytes, kRecPLo = 3 * kMatBytes;
+constexpr int64_t kRecL = 4 * kMatBytes;
+constexpr int64_t kRecBytes = 4 * kMatBytes + kChunk * 4;
 
 GDN_DEV int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
@@ -205,7 +205,8 @@ __global__ __launch_bounds__(256) void prefill_chunk_kernel(
     for (int e = 0; e < r; ++e) {
         const int hv = hk * r + e;
         char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
-        uint16_t* rec_p = reinterpret_cast<uint16_t*>(rec + kRecP);
+        uint16_t* rec_ph = reinterpret_cast<uint16_t*>(rec + kRecPHi);
+        uint16_t* rec_pl = reinterpret_cast<uint16_t*>(rec + kRecPLo);
         // P and A from the accumulators: element (i, j) with
         // i = 16w + 4(l/16) + ii, j = 16jt + l%16.
 #pragma unroll
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void prefill_chunk_kernel(
             for (int ii = 0; ii < 4; ++ii) {
                 const int i = 16 * w + 4 * (l >> 4) + ii, j = 16 * jt + lr;
                 const float dec = i >= j ? expf(l_sh[e][i] - l_sh[e][j]) : 0.f;
-                rec_p[i * kChunk + j] = bf16_bits(qk[jt][ii] * dec);
+                split_bf16(qk[jt][ii] * dec, rec_ph[i * kChunk + j], rec_pl[i * kChunk + j]);
                 As[i * kFS + j] = i > j ? beta_sh[e][i] * kk[jt][ii] * dec : 0.f;
             }
         }
@@ -285,7 +286,7 @@ constexpr int kTS = kChunk + 8;  // bf16 row stride of token-major operand tiles
 struct ChunkOperands {
     bf16x8 ka[4], qa[4];    // K / Q rows 16w + l%16, dk 32s + 8(l/16) .. +7
     bf16x8 tbh[2], tbl[2];  // Tb rows 16w + l%16 (hi, lo), tokens 32s + 8(l/16) .. +7
-    bf16x8 pa[2];           // P rows 16w + l%16
+    bf16x8 pah[2], pal[2];  // P rows 16w + l%16 (hi, lo)
     uint32_t v[4];          // V (bf16 bits) at (token 16w + 4(l/16) + i, dv0 + l%16)
     float l;                // l[tid] (tid < 64)
 };
@@ -320,12 +321,14 @@ GDN_DEV void fetch_chunk(ChunkOperands& op, const StatePassCtx& cx, int c, int t
     }
     const uint16_t* tb_hi = reinterpret_cast<const uint16_t*>(rec + kRecTbHi);
     const uint16_t* tb_lo = reinterpret_cast<const uint16_t*>(rec + kRecTbLo);
-    const uint16_t* p = reinterpret_cast<const uint16_t*>(rec + kRecP);
+    const uint16_t* p_hi = reinterpret_cast<const uint16_t*>(rec + kRecPHi);
+    const uint16_t* p_lo = reinterpret_cast<const uint16_t*>(rec + kRecPLo);
 #pragma unroll
     for (int s = 0; s < kChunk / 32; ++s) {
         op.tbh[s] = load8(tb_hi + tok * kChunk + 32 * s + lg8);
         op.tbl[s] = load8(tb_lo + tok * kChunk + 32 * s + lg8);
-        op.pa[s] = load8(p + tok * kChunk + 32 * s + lg8);
+        op.pah[s] = load8(p_hi + tok * kChunk + 32 * s + lg8);
+        op.pal[s] = load8(p_lo + tok * kChunk + 32 * s + lg8);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -344,7 +347,7 @@ struct StatePassLds {
     uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];
     uint16_t Kt[kHD * kTS];
     uint16_t Rs_hi[kSliceRows * kTS], Rs_lo[kSliceRows * kTS];
-    uint16_t Ds[kSliceRows * kTS];
+    uint16_t Ds_hi[kSliceRows * kTS], Ds_lo[kSliceRows * kTS];
     uint16_t D2_hi[kSliceRows * kTS], D2_lo[kSliceRows * kTS];
     float l[kChunk];
 };
@@ -387,16 +390,20 @@ GDN_DEV void compute_chunk(const ChunkOperands& op, f32x4 (&acc)[2], StatePassLd
     const int64_t t0 = cx.rs + int64_t(c) * kChunk;
     const int len = cx.re - t0 < kChunk ? int(cx.re - t0) : kChunk;
 
-    // X_K = K S^T (S in hi + lo), X_Q = Q S^T (S in hi): token rows 16w..16w+15.
-    f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xq = {0.f, 0.f, 0.f, 0.f};
+    // X_K = K S^T, X_Q = Q S^T (S in hi + lo): token rows 16w..16w+15, the
+    // hi and lo products in separate accumulators (shorter dependency chains).
+    f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xk2 = xk, xq = xk, xq2 = xk;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
         const bf16x8 bh = load8(sm.Ss_hi + lr * kSS + 32 * s + lg8);
         const bf16x8 bl = load8(sm.Ss_lo + lr * kSS + 32 * s + lg8);
         xk = mfma16(op.ka[s], bh, xk);
-        xk = mfma16(op.ka[s], bl, xk);
+        xk2 = mfma16(op.ka[s], bl, xk2);
         xq = mfma16(op.qa[s], bh, xq);
+        xq2 = mfma16(op.qa[s], bl, xq2);
     }
+    xk += xk2;
+    xq += xq2;
     // R = V - exp(l) X_K, stored hi + lo as R[dv][token].
     float el[4];
     {
@@ -412,27 +419,29 @@ GDN_DEV void compute_chunk(const ChunkOperands& op, f32x4 (&acc)[2], StatePassLd
     }
     __syncthreads();
 
-    // D = Tb R, three products (hi.hi + hi.lo + lo.hi).
-    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+    // D = Tb R, three products (hi.hi + hi.lo + lo.hi) in two accumulators.
+    f32x4 d = {0.f, 0.f, 0.f, 0.f}, d2 = d;
 #pragma unroll
     for (int s = 0; s < kChunk / 32; ++s) {
         const bf16x8 bh = load8(sm.Rs_hi + lr * kTS + 32 * s + lg8);
         const bf16x8 bl = load8(sm.Rs_lo + lr * kTS + 32 * s + lg8);
         d = mfma16(op.tbh[s], bh, d);
-        d = mfma16(op.tbh[s], bl, d);
-        d = mfma16(op.tbl[s], bh, d);
+        d2 = mfma16(op.tbh[s], bl, d2);
+        d2 = mfma16(op.tbl[s], bh, d2);
     }
-    // D (one bf16 part, for Y) and D'' = exp(l_C - l) D (hi + lo, for the update).
+    d += d2;
+    // D (hi + lo, for Y) and D'' = exp(l_C - l) D (hi + lo, for the update).
     const float lC = sm.l[kChunk - 1];
     {
-        uint16_t d1[4], hi[4], lo[4];
+        uint16_t dh[4], dl[4], hi[4], lo[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            d1[i] = bf16_bits(d[i]);
+            split_bf16(d[i], dh[i], dl[i]);
             split_bf16(expf(lC - sm.l[16 * w + 4 * lq + i]) * d[i], hi[i], lo[i]);
         }
         const int tok0 = 16 * w + 4 * lq;
-        *reinterpret_cast<uint2*>(sm.Ds + lr * kTS + tok0) = pack4(d1);
+        *reinterpret_cast<uint2*>(sm.Ds_hi + lr * kTS + tok0) = pack4(dh);
+        *reinterpret_cast<uint2*>(sm.Ds_lo + lr * kTS + tok0) = pack4(dl);
         *reinterpret_cast<uint2*>(sm.D2_hi + lr * kTS + tok0) = pack4(hi);
         *reinterpret_cast<uint2*>(sm.D2_lo + lr * kTS + tok0) = pack4(lo);
     }
@@ -443,9 +452,16 @@ GDN_DEV void compute_chunk(const ChunkOperands& op, f32x4 (&acc)[2], StatePassLd
         f32x4 yacc;
 #pragma unroll
         for (int i = 0; i < 4; ++i) yacc[i] = el[i] * xq[i];
+        f32x4 y2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < kChunk / 32; ++s)
-            yacc = mfma16(op.pa[s], load8(sm.Ds + lr * kTS + 32 * s + lg8), yacc);
+        for (int s = 0; s < kChunk / 32; ++s) {
+            const bf16x8 bh = load8(sm.Ds_hi + lr * kTS + 32 * s + lg8);
+            const bf16x8 bl = load8(sm.Ds_lo + lr * kTS + 32 * s + lg8);
+            yacc = mfma16(op.pah[s], bh, yacc);
+            y2 = mfma16(op.pah[s], bl, y2);
+            y2 = mfma16(op.pal[s], bh, y2);
+        }
+        yacc += y2;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tok = 16 * w + 4 * lq + i;
@@ -457,12 +473,14 @@ GDN_DEV void compute_chunk(const ChunkOperands& op, f32x4 (&acc)[2], StatePassLd
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         acc[t] *= eC;
+        f32x4 lo_acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < kChunk / 32; ++s) {
             const bf16x8 a = load8(sm.Kt + (32 * w + 16 * t + lr) * kTS + 32 * s + lg8);
             acc[t] = mfma16(a, load8(sm.D2_hi + lr * kTS + 32 * s + lg8), acc[t]);
-            acc[t] = mfma16(a, load8(sm.D2_lo + lr * kTS + 32 * s + lg8), acc[t]);
+            lo_acc = mfma16(a, load8(sm.D2_lo + lr * kTS + 32 * s + lg8), lo_acc);
         }
+        acc[t] += lo_acc;
     }
 }
 

@@ -38,3 +38,24 @@ def layer_params(rng, dims, K=4):
     dt_bias = rng.uniform(-1, 1, Hv).astype(np.float32)
     norm_w = rng.uniform(0.5, 1.5, Dv).astype(np.float32)
     return conv_w, A_log, dt_bias, norm_w
+
+
+def bf16_ulp(x) -> np.ndarray:
+    """Spacing of bfloat16 values at |x| (8 significant bits)."""
+
+    ax = np.maximum(np.abs(np.asarray(x, np.float64)), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(ax)) - 7)
+
+
+def assert_bf16_out_close(got, ref, atol: float = 2e-2) -> None:
+    """The bf16 output bar: |got - ref| <= 2e-2, or one bf16 ulp of the value
+    where an ulp is larger (a value of magnitude >= 4 has an ulp >= 2^-5, so
+    a single rounding flip there exceeds 2e-2)."""
+
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    tol = np.maximum(atol, bf16_ulp(ref))
+    err = np.abs(got - ref)
+    bad = err > tol
+    assert not bad.any(), (f"{int(bad.sum())} of {bad.size} values outside max(2e-2, 1 ulp); "
+                           f"worst {err.max():.3g} at |ref| {np.abs(ref).flat[err.argmax()]:.3g}")

@@ -87,6 +87,7 @@ def test_prefill_matches_sequential_oracle(gpu, T):
     y, s = _prefill(t)
     ye, se = _oracle(arrays)
     assert np.abs(y.cpu().numpy() - ye).max() < Y_ATOL
+    assert max_rel(y.cpu().numpy(), ye) < 1e-3
     assert max_rel(s.cpu().numpy(), se) < STATE_REL
 
 
@@ -173,6 +174,7 @@ def test_prefill_full_size_against_c_oracle(gpu):
     beta = R.beta_gate(b, "bf16").astype(np.float32)
     ye, se = cref.scan(q[None], k[None], v[None], g[None], beta[None], state)
     assert np.abs(y.cpu().numpy() - ye).max() < Y_ATOL
+    assert max_rel(y.cpu().numpy(), ye) < 1e-3
     assert max_rel(s.cpu().numpy(), se) < STATE_REL
     # and against this library's sequential scan on the same device inputs
     y2, s2 = gdn.gated_delta_update(t["q"][None], t["k"][None], t["v"][None], t["a"][None],
