@@ -208,6 +208,38 @@ def bench_prefill(dev, N, L, Hk, Hv, steps, warmup):
     }
 
 
+def cpu_baseline_prefill(Hk, Hv, budget_s=10.0):
+    """The C restatement of the reference's sequential recurrence
+    (gated_delta.py:93-109; float32, OpenMP over value heads) timed on the
+    host over a bounded number of tokens of the same prefill workload."""
+
+    from oracle import cref
+
+    rng = np.random.default_rng(0)
+    d, L = 128, 64
+    q = rng.standard_normal((1, L, Hk, d)).astype(np.float32) * 0.01
+    k = rng.standard_normal((1, L, Hk, d)).astype(np.float32) * 0.09
+    v = rng.standard_normal((1, L, Hv, d)).astype(np.float32)
+    g = rng.uniform(0.3, 0.9, (1, L, Hv)).astype(np.float32)
+    beta = rng.uniform(0, 1, (1, L, Hv)).astype(np.float32)
+    state = np.zeros((1, Hv, d, d), np.float32)
+    cref.scan(q, k, v, g, beta, state)
+    tokens, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        _, state = cref.scan(q, k, v, g, beta, state)
+        tokens += L
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    return {
+        "value": tokens / dt,
+        "unit": "tokens/s",
+        "cores": min(threads, len(os.sched_getaffinity(0))),
+        "kind": "port",
+        "sample": f"{tokens} tokens ({tokens // L} runs of {L}) of the T=4096 Hk={Hk} Hv={Hv} "
+                  f"prefill recurrence, {dt:.1f} s, float32 C/OpenMP restatement",
+    }
+
+
 def cpu_baseline_decode(B, Hk, Hv, budget_s=10.0):
     """The C restatement of the reference's decode path (fused front-end +
     recurrence, float32, OpenMP over (sequence, head)) timed on the host on a
@@ -275,14 +307,17 @@ def main(argv=None):
     torch.cuda.set_device(dev)
 
     if args.workload == "copy":
-        # Plain copy of a known size, used to scale rocprofv3 FETCH/WRITE_SIZE.
+        # Plain 1 GiB device copy: the HBM read+write ceiling a copy reaches,
+        # and the known byte counts that scale rocprofv3's FETCH/WRITE_SIZE.
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev).normal_()
         dst = torch.empty_like(src)
-        for _ in range(max(args.steps, 1)):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"workload": "copy", "bytes_read": src.numel() * 4,
-                          "bytes_written": dst.numel() * 4, "launches": max(args.steps, 1)}))
+        n = max(args.steps, 1)
+        total_ms, launch_ms = time_steps(lambda s: dst.copy_(src), n, max(args.warmup, 1))
+        nbytes = 2 * src.numel() * 4
+        print(json.dumps({"workload": "copy 1 GiB float32 (torch copy_)", "bytes_read": nbytes // 2,
+                          "bytes_written": nbytes // 2, "launches": n,
+                          "copy_us": launch_ms * 1e3,
+                          "gbs": nbytes / (launch_ms * 1e-3) / 1e9}))
         return 0
 
     if args.workload in ("decode", "decode_large"):
@@ -351,7 +386,9 @@ def main(argv=None):
                                        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                        "frac": r["mfma_frac"], "traffic": None,
                                        "kernel": "gdn_prefill_chunked (3 launches)",
-                                       "call_us": r["call_us"]}}))
+                                       "call_us": r["call_us"]},
+                          **({} if args.no_cpu_baseline else
+                             {"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)})}))
         return 0
 
     raise SystemExit(f"workload {args.workload} is not available in this build")
