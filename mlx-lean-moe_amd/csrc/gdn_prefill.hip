@@ -13,7 +13,8 @@
 // Two kernels:
 //   chunk pass (parallel over chunks x key heads): K K^T and Q K^T on MFMA,
 //     the gates, the blocked triangular inverse, and per value head the
-//     records Tb and P = lower(Q K^T o G) (each bf16 hi + lo) plus l.
+//     records Tb and P = lower(Q K^T o G) (each bf16 hi + lo) plus exp(l)
+//     and exp(l_C - l).
 //   state pass (per run x value head x 16-row slice of the state, sequential
 //     over the run's chunks): K S^T and Q S^T, Tb R, P D and the state update
 //     on MFMA, the state tile resident in accumulators.
@@ -41,8 +42,9 @@ constexpr float kLogGateFloor = -80.f;   // exp(-80) ~ 1.8e-35: a reset state
 // Per (chunk, value head) record written by the chunk pass.
 constexpr int64_t kMatBytes = int64_t(kChunk) * kChunk * 2;
 constexpr int64_t kRecTbHi = 0, kRecTbLo = kMatBytes, kRecPHi = 2 * kMatBytes, kRecPLo = 3 * kMatBytes;
-constexpr int64_t kRecL = 4 * kMatBytes;
-constexpr int64_t kRecBytes = 4 * kMatBytes + kChunk * 4;
+// exp(l_i) and exp(l_C - l_i) per token (l_C = l of the chunk's last token).
+constexpr int64_t kRecEl = 4 * kMatBytes, kRecEd = kRecEl + kChunk * 4;
+constexpr int64_t kRecBytes = 4 * kMatBytes + 2 * kChunk * 4;
 
 GDN_DEV int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
@@ -179,7 +181,10 @@ __global__ __launch_bounds__(256) void prefill_chunk_kernel(
         }
         l_sh[e][l] = lg;
         beta_sh[e][l] = beta;
-        reinterpret_cast<float*>(records + (int64_t(g) * Hv + hv) * kRecBytes + kRecL)[l] = lg;
+        const float lC = __shfl(lg, kChunk - 1, kWave);
+        char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
+        reinterpret_cast<float*>(rec + kRecEl)[l] = expf(lg);
+        reinterpret_cast<float*>(rec + kRecEd)[l] = expf(lC - lg);
     }
     __syncthreads();
 
@@ -279,18 +284,35 @@ __global__ __launch_bounds__(256) void prefill_chunk_kernel(
 // state pass
 // ---------------------------------------------------------------------------
 
-constexpr int kSS = kHD + 8;     // bf16 row stride of the S^T operand tiles
-constexpr int kTS = kChunk + 8;  // bf16 row stride of token-major operand tiles
+constexpr int kSS = kHD + 8;     // bf16 row stride of the S operand tile
+constexpr int kKS2 = kHD + 8;    // bf16 row stride of the row-major K tile
+constexpr int kTS = kChunk + 8;  // bf16 row stride of token-minor operand tiles
 
-// One chunk's operands as this lane needs them (fetched a chunk ahead).
-struct ChunkOperands {
-    bf16x8 ka[4], qa[4];    // K / Q rows 16w + l%16, dk 32s + 8(l/16) .. +7
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// The state pass runs 8 waves per workgroup: waves 0-3 carry the state
+// recurrence (K S^T -> R -> Tb R -> state update), waves 4-7 the output
+// (Q S^T, P D, y). Both halves meet at the same three barriers per chunk, so
+// every SIMD holds one wave of each and their latencies overlap.
+constexpr int kStateThreads = 512;
+
+// Operands of the state waves for one chunk (fetched a chunk ahead).
+struct StateOperands {
+    bf16x8 ka[4];           // K rows 16w + l%16, dk 32s + 8(l/16) .. +7
     bf16x8 tbh[2], tbl[2];  // Tb rows 16w + l%16 (hi, lo), tokens 32s + 8(l/16) .. +7
-    bf16x8 pah[2], pal[2];  // P rows 16w + l%16 (hi, lo)
     uint32_t v[4];          // V (bf16 bits) at (token 16w + 4(l/16) + i, dv0 + l%16)
-    float l;                // l[tid] (tid < 64)
+    float4 el, ed;          // exp(l), exp(l_C - l) at tokens 16w + 4(l/16) + i
+    float eC;               // exp(l_C)
 };
 
+// Operands of the output waves for one chunk.
+struct OutputOperands {
+    bf16x8 qa[4];           // Q rows 16w + l%16
+    bf16x8 pah[2], pal[2];  // P rows 16w + l%16 (hi, lo)
+    float4 el;              // exp(l) at tokens 16w + 4(l/16) + i
+};
+
+// Per-run constants of a state-pass workgroup.
 struct StatePassCtx {
     const uint16_t* q;
     const uint16_t* k;
@@ -298,6 +320,13 @@ struct StatePassCtx {
     const char* records;
     int64_t rs, re, qk_stride;
     int c0, h, hk, Hv, dv0;
+
+    GDN_DEV int64_t t0(int c) const { return rs + int64_t(c) * kChunk; }
+    GDN_DEV int len(int c) const {
+        const int64_t r = re - t0(c);
+        return r < kChunk ? int(r) : kChunk;
+    }
+    GDN_DEV const char* rec(int c) const { return records + (int64_t(c0 + c) * Hv + h) * kRecBytes; }
 };
 
 // Every load is unconditional, from a token index clamped into the chunk: a
@@ -305,38 +334,60 @@ struct StatePassCtx {
 // outstanding loads (the prefetch included), and consuming a loaded value
 // here would do the same. Rows past the run then hold copies of the last
 // token, which contribute nothing: their beta and log-decay are zero, so
-// their columns of Tb and P and their rows of D vanish.
-GDN_DEV void fetch_chunk(ChunkOperands& op, const StatePassCtx& cx, int c, int tid, int w, int lr,
-                         int lq, int lg8) {
-    const int64_t t0 = cx.rs + int64_t(c) * kChunk;
-    const int len = cx.re - t0 < kChunk ? int(cx.re - t0) : kChunk;
-    const char* rec = cx.records + (int64_t(cx.c0 + c) * cx.Hv + cx.h) * kRecBytes;
+// their columns of Tb and P and their rows of D vanish. Addresses are a
+// uniform per-chunk base plus a 32-bit lane offset.
+GDN_DEV void fetch_state(StateOperands& op, const StatePassCtx& cx, int c, int w, int lr, int lq,
+                         int lg8) {
+    const int64_t t0 = cx.t0(c);
+    const int len = cx.len(c);
+    const char* rec = cx.rec(c);
     const int tok = 16 * w + lr;
     const int tok_c = tok < len ? tok : len - 1;
-    const int64_t base = (t0 + tok_c) * cx.qk_stride + cx.hk * kHD + lg8;
+    const uint16_t* kb = cx.k + t0 * cx.qk_stride + cx.hk * kHD;
+    const uint32_t koff = uint32_t(tok_c) * uint32_t(cx.qk_stride) + uint32_t(lg8);
 #pragma unroll
-    for (int s = 0; s < kHD / 32; ++s) {
-        op.ka[s] = load8(cx.k + base + 32 * s);
-        op.qa[s] = load8(cx.q + base + 32 * s);
-    }
+    for (int s = 0; s < kHD / 32; ++s) op.ka[s] = load8(kb + koff + 32 * s);
     const uint16_t* tb_hi = reinterpret_cast<const uint16_t*>(rec + kRecTbHi);
     const uint16_t* tb_lo = reinterpret_cast<const uint16_t*>(rec + kRecTbLo);
-    const uint16_t* p_hi = reinterpret_cast<const uint16_t*>(rec + kRecPHi);
-    const uint16_t* p_lo = reinterpret_cast<const uint16_t*>(rec + kRecPLo);
+    const uint32_t roff = uint32_t(tok * kChunk + lg8);
 #pragma unroll
     for (int s = 0; s < kChunk / 32; ++s) {
-        op.tbh[s] = load8(tb_hi + tok * kChunk + 32 * s + lg8);
-        op.tbl[s] = load8(tb_lo + tok * kChunk + 32 * s + lg8);
-        op.pah[s] = load8(p_hi + tok * kChunk + 32 * s + lg8);
-        op.pal[s] = load8(p_lo + tok * kChunk + 32 * s + lg8);
+        op.tbh[s] = load8(tb_hi + roff + 32 * s);
+        op.tbl[s] = load8(tb_lo + roff + 32 * s);
     }
+    const uint16_t* vb = cx.v + t0 * cx.Hv * kHD + cx.h * kHD + cx.dv0 + lr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tv = 16 * w + 4 * lq + i;
         const int tv_c = tv < len ? tv : len - 1;
-        op.v[i] = cx.v[((t0 + tv_c) * cx.Hv + cx.h) * kHD + cx.dv0 + lr];
+        op.v[i] = vb[uint32_t(tv_c) * uint32_t(cx.Hv * kHD)];
     }
-    op.l = reinterpret_cast<const float*>(rec + kRecL)[tid & (kChunk - 1)];
+    const int tok4 = 16 * w + 4 * lq;
+    op.el = *reinterpret_cast<const float4*>(rec + kRecEl + tok4 * 4);
+    op.ed = *reinterpret_cast<const float4*>(rec + kRecEd + tok4 * 4);
+    op.eC = reinterpret_cast<const float*>(rec + kRecEl)[kChunk - 1];
+}
+
+GDN_DEV void fetch_output(OutputOperands& op, const StatePassCtx& cx, int c, int w, int lr, int lq,
+                          int lg8) {
+    const int64_t t0 = cx.t0(c);
+    const int len = cx.len(c);
+    const char* rec = cx.rec(c);
+    const int tok = 16 * w + lr;
+    const int tok_c = tok < len ? tok : len - 1;
+    const uint16_t* qb = cx.q + t0 * cx.qk_stride + cx.hk * kHD;
+    const uint32_t qoff = uint32_t(tok_c) * uint32_t(cx.qk_stride) + uint32_t(lg8);
+#pragma unroll
+    for (int s = 0; s < kHD / 32; ++s) op.qa[s] = load8(qb + qoff + 32 * s);
+    const uint16_t* p_hi = reinterpret_cast<const uint16_t*>(rec + kRecPHi);
+    const uint16_t* p_lo = reinterpret_cast<const uint16_t*>(rec + kRecPLo);
+    const uint32_t roff = uint32_t(tok * kChunk + lg8);
+#pragma unroll
+    for (int s = 0; s < kChunk / 32; ++s) {
+        op.pah[s] = load8(p_hi + roff + 32 * s);
+        op.pal[s] = load8(p_lo + roff + 32 * s);
+    }
+    op.el = *reinterpret_cast<const float4*>(rec + kRecEl + (16 * w + 4 * lq) * 4);
 }
 
 GDN_DEV uint2 pack4(const uint16_t (&x)[4]) {
@@ -344,20 +395,19 @@ GDN_DEV uint2 pack4(const uint16_t (&x)[4]) {
 }
 
 struct StatePassLds {
-    uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];
-    uint16_t Kt[kHD * kTS];
-    uint16_t Rs_hi[kSliceRows * kTS], Rs_lo[kSliceRows * kTS];
-    uint16_t Ds_hi[kSliceRows * kTS], Ds_lo[kSliceRows * kTS];
-    uint16_t D2_hi[kSliceRows * kTS], D2_lo[kSliceRows * kTS];
-    float l[kChunk];
+    uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];  // S[dv][dk]
+    uint16_t Kr[2][kChunk * kKS2];                                // K[token][dk], two buffers
+    uint16_t Rs_hi[kSliceRows * kTS], Rs_lo[kSliceRows * kTS];    // R[dv][token]
+    uint16_t Ds_hi[kSliceRows * kTS], Ds_lo[kSliceRows * kTS];    // D[dv][token]
+    uint16_t D2_hi[kSliceRows * kTS], D2_lo[kSliceRows * kTS];    // D''[dv][token]
 };
 
-// Chunk step, part 1: the S^T operand (hi + lo), the chunk's K^T and its
-// log-decays into LDS. Consuming the chunk's K registers and l here means its
-// loads are complete before the next chunk's prefetch is issued.
-GDN_DEV void stage_chunk(const ChunkOperands& op, const f32x4 (&acc)[2], StatePassLds& sm, int tid,
+// State waves, chunk part 1: the S operand (hi + lo) and the chunk's K rows
+// into LDS. Consuming the chunk's K registers here completes its loads
+// before the next chunk's prefetch is issued; K alternates between two
+// buffers so the previous chunk's state update may still read the other.
+GDN_DEV void state_stage(const StateOperands& op, const f32x4 (&acc)[2], StatePassLds& sm, int buf,
                          int w, int lr, int lq, int lg8) {
-    __syncthreads();  // the previous chunk's readers of the LDS tiles are done
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int dk = 32 * w + 16 * t + 4 * lq;
@@ -367,59 +417,32 @@ GDN_DEV void stage_chunk(const ChunkOperands& op, const f32x4 (&acc)[2], StatePa
         *reinterpret_cast<uint2*>(sm.Ss_hi + lr * kSS + dk) = pack4(hi);
         *reinterpret_cast<uint2*>(sm.Ss_lo + lr * kSS + dk) = pack4(lo);
     }
-    {
-        const int tok = 16 * w + lr;
+    uint16_t* kr = sm.Kr[buf] + (16 * w + lr) * kKS2 + lg8;
 #pragma unroll
-        for (int s = 0; s < kHD / 32; ++s) {
-            // Whole-vector bit cast: this compiler miscompiles a bit cast of a
-            // single __bf16 vector element (it repeats element 0).
-            const u16x8 kv = __builtin_bit_cast(u16x8, op.ka[s]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sm.Kt[(32 * s + lg8 + j) * kTS + tok] = kv[j];
-        }
-    }
-    sm.l[tid & (kChunk - 1)] = op.l;  // all four waves store the same values: no branch
-    __syncthreads();
+    for (int s = 0; s < kHD / 32; ++s) *reinterpret_cast<bf16x8*>(kr + 32 * s) = op.ka[s];
 }
 
-// Chunk step, part 2: S^T (acc) advances by the chunk, y is written.
-template <class Y>
-GDN_DEV void compute_chunk(const ChunkOperands& op, f32x4 (&acc)[2], StatePassLds& sm,
-                           const StatePassCtx& cx, int c, typename Y::storage* __restrict__ y,
-                           int w, int lr, int lq, int lg8) {
-    const int64_t t0 = cx.rs + int64_t(c) * kChunk;
-    const int len = cx.re - t0 < kChunk ? int(cx.re - t0) : kChunk;
-
-    // X_K = K S^T, X_Q = Q S^T (S in hi + lo): token rows 16w..16w+15, the
-    // hi and lo products in separate accumulators (shorter dependency chains).
-    f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xk2 = xk, xq = xk, xq2 = xk;
+// State waves, part 2 (between the staging and R barriers): R = V - exp(l) K S^T.
+GDN_DEV void state_residual(const StateOperands& op, StatePassLds& sm, int w, int lr, int lq, int lg8) {
+    f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xk2 = xk;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        const bf16x8 bh = load8(sm.Ss_hi + lr * kSS + 32 * s + lg8);
-        const bf16x8 bl = load8(sm.Ss_lo + lr * kSS + 32 * s + lg8);
-        xk = mfma16(op.ka[s], bh, xk);
-        xk2 = mfma16(op.ka[s], bl, xk2);
-        xq = mfma16(op.qa[s], bh, xq);
-        xq2 = mfma16(op.qa[s], bl, xq2);
+        xk = mfma16(op.ka[s], load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), xk);
+        xk2 = mfma16(op.ka[s], load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xk2);
     }
     xk += xk2;
-    xq += xq2;
-    // R = V - exp(l) X_K, stored hi + lo as R[dv][token].
-    float el[4];
-    {
-        uint16_t hi[4], lo[4];
+    const float el[4] = {op.el.x, op.el.y, op.el.z, op.el.w};
+    uint16_t hi[4], lo[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            el[i] = expf(sm.l[16 * w + 4 * lq + i]);
-            split_bf16(bf16_bits_to_f32(op.v[i]) - el[i] * xk[i], hi[i], lo[i]);
-        }
-        const int tok0 = 16 * w + 4 * lq;
-        *reinterpret_cast<uint2*>(sm.Rs_hi + lr * kTS + tok0) = pack4(hi);
-        *reinterpret_cast<uint2*>(sm.Rs_lo + lr * kTS + tok0) = pack4(lo);
-    }
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) split_bf16(__uint_as_float(op.v[i] << 16) - el[i] * xk[i], hi[i], lo[i]);
+    const int tok0 = 16 * w + 4 * lq;
+    *reinterpret_cast<uint2*>(sm.Rs_hi + lr * kTS + tok0) = pack4(hi);
+    *reinterpret_cast<uint2*>(sm.Rs_lo + lr * kTS + tok0) = pack4(lo);
+}
 
-    // D = Tb R, three products (hi.hi + hi.lo + lo.hi) in two accumulators.
+// State waves, part 3 (between the R and D barriers): D = Tb R, stored as
+// D (hi + lo, for Y) and D'' = exp(l_C - l) D (hi + lo, for the update).
+GDN_DEV void state_delta(const StateOperands& op, StatePassLds& sm, int w, int lr, int lq, int lg8) {
     f32x4 d = {0.f, 0.f, 0.f, 0.f}, d2 = d;
 #pragma unroll
     for (int s = 0; s < kChunk / 32; ++s) {
@@ -430,53 +453,45 @@ GDN_DEV void compute_chunk(const ChunkOperands& op, f32x4 (&acc)[2], StatePassLd
         d2 = mfma16(op.tbl[s], bh, d2);
     }
     d += d2;
-    // D (hi + lo, for Y) and D'' = exp(l_C - l) D (hi + lo, for the update).
-    const float lC = sm.l[kChunk - 1];
-    {
-        uint16_t dh[4], dl[4], hi[4], lo[4];
+    const float ed[4] = {op.ed.x, op.ed.y, op.ed.z, op.ed.w};
+    uint16_t dh[4], dl[4], hi[4], lo[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            split_bf16(d[i], dh[i], dl[i]);
-            split_bf16(expf(lC - sm.l[16 * w + 4 * lq + i]) * d[i], hi[i], lo[i]);
-        }
-        const int tok0 = 16 * w + 4 * lq;
-        *reinterpret_cast<uint2*>(sm.Ds_hi + lr * kTS + tok0) = pack4(dh);
-        *reinterpret_cast<uint2*>(sm.Ds_lo + lr * kTS + tok0) = pack4(dl);
-        *reinterpret_cast<uint2*>(sm.D2_hi + lr * kTS + tok0) = pack4(hi);
-        *reinterpret_cast<uint2*>(sm.D2_lo + lr * kTS + tok0) = pack4(lo);
+    for (int i = 0; i < 4; ++i) {
+        split_bf16(d[i], dh[i], dl[i]);
+        split_bf16(ed[i] * d[i], hi[i], lo[i]);
     }
-    __syncthreads();
+    const int tok0 = 16 * w + 4 * lq;
+    *reinterpret_cast<uint2*>(sm.Ds_hi + lr * kTS + tok0) = pack4(dh);
+    *reinterpret_cast<uint2*>(sm.Ds_lo + lr * kTS + tok0) = pack4(dl);
+    *reinterpret_cast<uint2*>(sm.D2_hi + lr * kTS + tok0) = pack4(hi);
+    *reinterpret_cast<uint2*>(sm.D2_lo + lr * kTS + tok0) = pack4(lo);
+}
 
-    // Y = exp(l) X_Q + P D.
-    {
-        f32x4 yacc;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) yacc[i] = el[i] * xq[i];
-        f32x4 y2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < kChunk / 32; ++s) {
-            const bf16x8 bh = load8(sm.Ds_hi + lr * kTS + 32 * s + lg8);
-            const bf16x8 bl = load8(sm.Ds_lo + lr * kTS + 32 * s + lg8);
-            yacc = mfma16(op.pah[s], bh, yacc);
-            y2 = mfma16(op.pah[s], bl, y2);
-            y2 = mfma16(op.pal[s], bh, y2);
-        }
-        yacc += y2;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tok = 16 * w + 4 * lq + i;
-            if (tok < len) Y::store(y, ((t0 + tok) * cx.Hv + cx.h) * kHD + cx.dv0 + lr, yacc[i]);
-        }
-    }
-    // S^T <- exp(l_C) S^T + K^T D'' (D'' in hi + lo).
-    const float eC = expf(lC);
+// State waves, part 4 (after the D barrier): S^T <- exp(l_C) S^T + K^T D''.
+// The K^T operand is read from the row-major K tile with the transposing LDS
+// read: within each 16-lane group, lane i of a ds_read_b64_tr_b16 receives
+// element i%4 of source lane i/4 + 4k (k = 0..3); source lane s of group g
+// points at K[8g + 4h + s/4][dk0 + 4(s%4)] for the tokens 8g + 4h .. +3.
+GDN_DEV void state_update(const StateOperands& op, f32x4 (&acc)[2], const StatePassLds& sm, int buf,
+                          int w, int l, int lr, int lg8) {
+    const int g = l >> 4, sl = l & 15;
+    const uint16_t* kr = sm.Kr[buf];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        acc[t] *= eC;
+        acc[t] *= op.eC;
         f32x4 lo_acc = {0.f, 0.f, 0.f, 0.f};
+        const int dk0 = 32 * w + 16 * t;
 #pragma unroll
         for (int s = 0; s < kChunk / 32; ++s) {
-            const bf16x8 a = load8(sm.Kt + (32 * w + 16 * t + lr) * kTS + 32 * s + lg8);
+            v4s parts[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const uint16_t* src = kr + (32 * s + 8 * g + 4 * hh + (sl >> 2)) * kKS2 + dk0 + 4 * (sl & 3);
+                parts[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) v4s*)(src));
+            }
+            const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(
+                parts[0], parts[1], 0, 1, 2, 3, 4, 5, 6, 7));
             acc[t] = mfma16(a, load8(sm.D2_hi + lr * kTS + 32 * s + lg8), acc[t]);
             lo_acc = mfma16(a, load8(sm.D2_lo + lr * kTS + 32 * s + lg8), lo_acc);
         }
@@ -484,8 +499,48 @@ GDN_DEV void compute_chunk(const ChunkOperands& op, f32x4 (&acc)[2], StatePassLd
     }
 }
 
+// Output waves, part 1 (between the staging and R barriers): exp(l) Q S^T.
+GDN_DEV f32x4 output_project(const OutputOperands& op, const StatePassLds& sm, int lr, int lg8) {
+    f32x4 xq = {0.f, 0.f, 0.f, 0.f}, xq2 = xq;
+#pragma unroll
+    for (int s = 0; s < kHD / 32; ++s) {
+        xq = mfma16(op.qa[s], load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), xq);
+        xq2 = mfma16(op.qa[s], load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xq2);
+    }
+    xq += xq2;
+    xq[0] *= op.el.x;
+    xq[1] *= op.el.y;
+    xq[2] *= op.el.z;
+    xq[3] *= op.el.w;
+    return xq;
+}
+
+// Output waves, part 2 (after the D barrier): y = exp(l) Q S^T + P D.
 template <class Y>
-__global__ __launch_bounds__(256) void prefill_state_kernel(
+GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassLds& sm,
+                          const StatePassCtx& cx, int c, typename Y::storage* __restrict__ y, int w,
+                          int lr, int lq, int lg8) {
+    f32x4 y2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kChunk / 32; ++s) {
+        const bf16x8 bh = load8(sm.Ds_hi + lr * kTS + 32 * s + lg8);
+        const bf16x8 bl = load8(sm.Ds_lo + lr * kTS + 32 * s + lg8);
+        yacc = mfma16(op.pah[s], bh, yacc);
+        y2 = mfma16(op.pah[s], bl, y2);
+        y2 = mfma16(op.pal[s], bh, y2);
+    }
+    yacc += y2;
+    const int64_t t0 = cx.t0(c);
+    const int len = cx.len(c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tok = 16 * w + 4 * lq + i;
+        if (tok < len) Y::store(y, ((t0 + tok) * cx.Hv + cx.h) * kHD + cx.dv0 + lr, yacc[i]);
+    }
+}
+
+template <class Y>
+__global__ __launch_bounds__(kStateThreads) void prefill_state_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const float* __restrict__ state_in, float* __restrict__ state_out,
     typename Y::storage* __restrict__ y, const int32_t* __restrict__ cu, int N, int64_t L_uniform,
@@ -507,7 +562,9 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
         slice = id % kSlices;
     }
     const int run = hr / Hv, h = hr % Hv;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int tid = threadIdx.x;
+    const bool state_wave = tid < 256;
+    const int w = (tid >> 6) & 3, l = tid & 63;
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
 
     StatePassCtx cx;
@@ -525,38 +582,56 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
     cx.dv0 = slice * kSliceRows;
     const int nch = chunk_off[run + 1] - cx.c0;
 
-    // S^T tile in accumulators: acc[t][i] = S^T[dk = 32w + 16t + 4(l/16) + i][dv = dv0 + l%16].
-    f32x4 acc[2];
+    // State waves keep S^T in accumulators:
+    // acc[t][i] = S^T[dk = 32w + 16t + 4(l/16) + i][dv = dv0 + l%16].
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     const int64_t sbase = ((int64_t(run) * Hv + h) * kHD + cx.dv0 + lr) * kHD;
+    if (state_wave && state_in) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int dk = 32 * w + 16 * t + 4 * lq;
-        if (state_in) {
-            const float4 s4 = *reinterpret_cast<const float4*>(state_in + sbase + dk);
+        for (int t = 0; t < 2; ++t) {
+            const float4 s4 = *reinterpret_cast<const float4*>(state_in + sbase + 32 * w + 16 * t + 4 * lq);
             acc[t] = f32x4{s4.x, s4.y, s4.z, s4.w};
-        } else {
-            acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
 
-    // Two operand sets, alternated: chunk c computes from one while chunk
-    // c + 1's loads land in the other.
-    ChunkOperands opa, opb;
-    if (nch > 0) fetch_chunk(opa, cx, 0, tid, w, lr, lq, lg8);
+    // Chunk c: [stage] B1 [R | Q S^T] B2 [D] B3 [update | y]. Operands of
+    // chunk c + 1 are fetched right after B1, into the other register set.
+    StateOperands sa, sb;
+    OutputOperands oa, ob;
+    auto step = [&](int c, int buf, const StateOperands& sc, StateOperands& sn,
+                    const OutputOperands& oc, OutputOperands& on) {
+        if (state_wave) state_stage(sc, acc, sm, buf, w, lr, lq, lg8);
+        __syncthreads();
+        f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
+        if (state_wave) {
+            if (c + 1 < nch) fetch_state(sn, cx, c + 1, w, lr, lq, lg8);
+            state_residual(sc, sm, w, lr, lq, lg8);
+        } else {
+            if (c + 1 < nch) fetch_output(on, cx, c + 1, w, lr, lq, lg8);
+            yacc = output_project(oc, sm, lr, lg8);
+        }
+        __syncthreads();
+        if (state_wave) state_delta(sc, sm, w, lr, lq, lg8);
+        __syncthreads();
+        if (state_wave) state_update(sc, acc, sm, buf, w, l, lr, lg8);
+        else output_store<Y>(oc, yacc, sm, cx, c, y, w, lr, lq, lg8);
+    };
+    if (nch > 0) {
+        if (state_wave) fetch_state(sa, cx, 0, w, lr, lq, lg8);
+        else fetch_output(oa, cx, 0, w, lr, lq, lg8);
+    }
     for (int c = 0; c < nch; c += 2) {
-        stage_chunk(opa, acc, sm, tid, w, lr, lq, lg8);
-        if (c + 1 < nch) fetch_chunk(opb, cx, c + 1, tid, w, lr, lq, lg8);
-        compute_chunk<Y>(opa, acc, sm, cx, c, y, w, lr, lq, lg8);
+        step(c, 0, sa, sb, oa, ob);
         if (c + 1 >= nch) break;
-        stage_chunk(opb, acc, sm, tid, w, lr, lq, lg8);
-        if (c + 2 < nch) fetch_chunk(opa, cx, c + 2, tid, w, lr, lq, lg8);
-        compute_chunk<Y>(opb, acc, sm, cx, c + 1, y, w, lr, lq, lg8);
+        step(c + 1, 1, sb, sa, ob, oa);
     }
 
+    if (state_wave) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int dk = 32 * w + 16 * t + 4 * lq;
-        *reinterpret_cast<float4*>(state_out + sbase + dk) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        for (int t = 0; t < 2; ++t) {
+            const int dk = 32 * w + 16 * t + 4 * lq;
+            *reinterpret_cast<float4*>(state_out + sbase + dk) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        }
     }
 }
 
@@ -617,7 +692,7 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     if (int rc = check_launch("gdn_prefill_chunked/chunk")) return rc;
     const dim3 sgrid(unsigned(int64_t(N) * Hv * kSlices));
 #define GDN_STATE_LAUNCH(YT)                                                                      \
-    hipLaunchKernelGGL(prefill_state_kernel<YT>, sgrid, dim3(256), 0, s,                          \
+    hipLaunchKernelGGL(prefill_state_kernel<YT>, sgrid, dim3(kStateThreads), 0, s,                          \
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),           \
                        static_cast<const uint16_t*>(v), state_in, state_out,                       \
                        static_cast<YT::storage*>(y), cu_seqlens, N, L_uniform, chunk_off, records, \
