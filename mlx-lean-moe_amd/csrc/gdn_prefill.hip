@@ -39,7 +39,12 @@ constexpr int kSlices = kHD / kSliceRows;
 constexpr int kMaxGroup = 8;             // value heads per key head handled by the chunk pass
 constexpr float kLogGateFloor = -80.f;   // exp(-80) ~ 1.8e-35: a reset state
 
-// Per (chunk, value head) record written by the chunk pass.
+// Per (chunk, value head) record written by the chunk pass. Tb and P are
+// stored as MFMA A-operand fragments: fragment f = 2 rb + kb holds rows
+// 16 rb .. +15 and columns 32 kb .. +31, lane l of it the 8 values of row
+// 16 rb + l%16, columns 32 kb + 8(l/16) .. +7 (16 bytes at 16 (64 f + l)), so
+// that a wave loads its operand as one contiguous 1 KiB. Fragments (0, 1) and
+// (1, 1) lie above the diagonal (all zero) and are neither written nor read.
 constexpr int64_t kMatBytes = int64_t(kChunk) * kChunk * 2;
 constexpr int64_t kRecTbHi = 0, kRecTbLo = kMatBytes, kRecPHi = 2 * kMatBytes, kRecPLo = 3 * kMatBytes;
 // exp(l_i) and exp(l_C - l_i) per token (l_C = l of the chunk's last token).
@@ -121,6 +126,33 @@ GDN_DEV void block_mma(float (&acc)[4], const float* A, const float* B, int m, i
         const float a = A[m * kFS + k];
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[q] += a * B[k * kFS + n0 + q];
+    }
+}
+
+// Stores a lower-triangular 64 x 64 float32 tile held in LDS (row stride
+// kFS) as bf16 hi + lo fragments (layout above), 16 bytes per lane. With
+// col_scale (T diag(beta)): the diagonal is taken as 1 and column j is
+// scaled by col_scale[j]; without it, entries above the diagonal are zero.
+GDN_DEV void store_fragments(const float* M, uint16_t* hi_out, uint16_t* lo_out,
+                             const float* col_scale, int tid) {
+    for (int item = tid; item < 6 * 64; item += 256) {
+        const int fi = item >> 6, ln = item & 63;
+        const int f = fi < 2 ? 2 * fi : fi + 2;  // skip fragments 1 and 3
+        const int i = 16 * (f >> 1) + (ln & 15), j0 = 32 * (f & 1) + 8 * (ln >> 4);
+        u16x8 h, o;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const int j = j0 + jj;
+            float x = i > j ? M[i * kFS + j] : 0.f;
+            if (col_scale) x = (i == j ? 1.f : x) * col_scale[j];
+            else if (i == j) x = M[i * kFS + j];
+            uint16_t a, b;
+            split_bf16(x, a, b);
+            h[jj] = a;
+            o[jj] = b;
+        }
+        *reinterpret_cast<u16x8*>(hi_out + (64 * f + ln) * 8) = h;
+        *reinterpret_cast<u16x8*>(lo_out + (64 * f + ln) * 8) = o;
     }
 }
 
@@ -210,21 +242,23 @@ __global__ __launch_bounds__(256) void prefill_chunk_kernel(
     for (int e = 0; e < r; ++e) {
         const int hv = hk * r + e;
         char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
-        uint16_t* rec_ph = reinterpret_cast<uint16_t*>(rec + kRecPHi);
-        uint16_t* rec_pl = reinterpret_cast<uint16_t*>(rec + kRecPLo);
         // P and A from the accumulators: element (i, j) with
-        // i = 16w + 4(l/16) + ii, j = 16jt + l%16.
+        // i = 16w + 4(l/16) + ii, j = 16jt + l%16. P goes through LDS (the
+        // off-diagonal scratch, free until then) to be stored as fragments.
+        float* Ps = &wtmp[0][0];
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
                 const int i = 16 * w + 4 * (l >> 4) + ii, j = 16 * jt + lr;
                 const float dec = i >= j ? expf(l_sh[e][i] - l_sh[e][j]) : 0.f;
-                split_bf16(qk[jt][ii] * dec, rec_ph[i * kChunk + j], rec_pl[i * kChunk + j]);
+                Ps[i * kFS + j] = qk[jt][ii] * dec;
                 As[i * kFS + j] = i > j ? beta_sh[e][i] * kk[jt][ii] * dec : 0.f;
             }
         }
         __syncthreads();
+        store_fragments(Ps, reinterpret_cast<uint16_t*>(rec + kRecPHi),
+                        reinterpret_cast<uint16_t*>(rec + kRecPLo), nullptr, tid);
 
         // T = (I + A)^-1 by 16 x 16 blocks. Diagonal blocks by forward
         // substitution (lane n < 16 owns column n).
@@ -266,17 +300,9 @@ __global__ __launch_bounds__(256) void prefill_chunk_kernel(
             __syncthreads();
         }
         // Tb = T diag(beta), split into bf16 hi + lo.
-        uint16_t* tb_hi = reinterpret_cast<uint16_t*>(rec + kRecTbHi);
-        uint16_t* tb_lo = reinterpret_cast<uint16_t*>(rec + kRecTbLo);
-        for (int idx = tid; idx < kChunk * kChunk; idx += 256) {
-            const int i = idx / kChunk, j = idx % kChunk;
-            const float t = i == j ? 1.f : (i > j ? Ts[i * kFS + j] : 0.f);
-            uint16_t hi, lo;
-            split_bf16(t * beta_sh[e][j], hi, lo);
-            tb_hi[idx] = hi;
-            tb_lo[idx] = lo;
-        }
-        __syncthreads();  // As / Ts are reused by the next value head
+        store_fragments(Ts, reinterpret_cast<uint16_t*>(rec + kRecTbHi),
+                        reinterpret_cast<uint16_t*>(rec + kRecTbLo), beta_sh[e], tid);
+        __syncthreads();  // As / Ts / Ps are reused by the next value head
     }
 }
 
@@ -289,27 +315,35 @@ constexpr int kKS2 = kHD + 8;    // bf16 row stride of the row-major K tile
 constexpr int kTS = kChunk + 8;  // bf16 row stride of token-minor operand tiles
 
 typedef short v4s __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// The state pass runs 8 waves per workgroup: waves 0-3 carry the state
-// recurrence (K S^T -> R -> Tb R -> state update), waves 4-7 the output
-// (Q S^T, P D, y). Both halves meet at the same three barriers per chunk, so
-// every SIMD holds one wave of each and their latencies overlap.
+// The state pass runs 8 waves per workgroup. Waves 0-3 carry the state
+// recurrence (S K^T -> R -> Tb R -> state update) and touch only LDS and
+// their accumulators. Waves 4-7 compute the output (Q S^T, P D, y) and fetch
+// every chunk operand from global memory for both halves: those of the
+// state waves (K, V, Tb, the decay factors) two chunks ahead into registers,
+// then into LDS one chunk ahead. Issuing the loads is what the state
+// recurrence cannot afford (the vector-memory queue stalls the issuing
+// wave); the output waves have slack. Both halves meet at the same three
+// barriers per chunk. Output wave w fetches the rows state wave w consumes;
+// Tb and P are lower triangular, so the waves of token rows 0-31
+// (kUpper = false) fetch and multiply only their first 32 columns.
 constexpr int kStateThreads = 512;
 
-// Operands of the state waves for one chunk (fetched a chunk ahead).
-struct StateOperands {
-    bf16x8 ka[4];           // K rows 16w + l%16, dk 32s + 8(l/16) .. +7
-    bf16x8 tbh[2], tbl[2];  // Tb rows 16w + l%16 (hi, lo), tokens 32s + 8(l/16) .. +7
-    uint32_t v[4];          // V (bf16 bits) at (token 16w + 4(l/16) + i, dv0 + l%16)
-    float4 el, ed;          // exp(l), exp(l_C - l) at tokens 16w + 4(l/16) + i
-    float eC;               // exp(l_C)
+// Chunk operands of state wave w, fetched by output wave w. They only pass
+// through registers on the way to LDS, so each load covers whole rows (full
+// cache lines): 16 lanes per 256-byte K row, 8 per 128-byte Tb row.
+struct StagedOperands {
+    bf16x8 ka[4];           // K row 16w + 4i + l/16, dk 8(l%16) .. +7
+    bf16x8 tbh[2], tbl[2];  // Tb fragments (2w + s) (hi, lo): row 16w + l%16, tokens 32s + 8(l/16) .. +7
+    u32x2 v;                // V (bf16) at token 16w + l%16, dv dv0 + 4(l/16) .. +3
+    f32x4 e;                // words 32w + 4(l%8) .. +3 of the record's [exp(l) | exp(l_C - l)]
 };
 
-// Operands of the output waves for one chunk.
+// Operands of output wave w itself.
 struct OutputOperands {
     bf16x8 qa[4];           // Q rows 16w + l%16
     bf16x8 pah[2], pal[2];  // P rows 16w + l%16 (hi, lo)
-    float4 el;              // exp(l) at tokens 16w + 4(l/16) + i
 };
 
 // Per-run constants of a state-pass workgroup.
@@ -336,58 +370,49 @@ struct StatePassCtx {
 // token, which contribute nothing: their beta and log-decay are zero, so
 // their columns of Tb and P and their rows of D vanish. Addresses are a
 // uniform per-chunk base plus a 32-bit lane offset.
-GDN_DEV void fetch_state(StateOperands& op, const StatePassCtx& cx, int c, int w, int lr, int lq,
-                         int lg8) {
-    const int64_t t0 = cx.t0(c);
+template <bool kUpper>
+GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int w, int l) {
     const int len = cx.len(c);
-    const char* rec = cx.rec(c);
-    const int tok = 16 * w + lr;
-    const int tok_c = tok < len ? tok : len - 1;
-    const uint16_t* kb = cx.k + t0 * cx.qk_stride + cx.hk * kHD;
-    const uint32_t koff = uint32_t(tok_c) * uint32_t(cx.qk_stride) + uint32_t(lg8);
-#pragma unroll
-    for (int s = 0; s < kHD / 32; ++s) op.ka[s] = load8(kb + koff + 32 * s);
-    const uint16_t* tb_hi = reinterpret_cast<const uint16_t*>(rec + kRecTbHi);
-    const uint16_t* tb_lo = reinterpret_cast<const uint16_t*>(rec + kRecTbLo);
-    const uint32_t roff = uint32_t(tok * kChunk + lg8);
-#pragma unroll
-    for (int s = 0; s < kChunk / 32; ++s) {
-        op.tbh[s] = load8(tb_hi + roff + 32 * s);
-        op.tbl[s] = load8(tb_lo + roff + 32 * s);
-    }
-    const uint16_t* vb = cx.v + t0 * cx.Hv * kHD + cx.h * kHD + cx.dv0 + lr;
+    const uint16_t* kb = cx.k + cx.t0(c) * cx.qk_stride + cx.hk * kHD + 8 * (l & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int tv = 16 * w + 4 * lq + i;
-        const int tv_c = tv < len ? tv : len - 1;
-        op.v[i] = vb[uint32_t(tv_c) * uint32_t(cx.Hv * kHD)];
+        const int tok = 16 * w + 4 * i + (l >> 4);
+        const int tok_c = tok < len ? tok : len - 1;
+        op.ka[i] = load8(kb + uint32_t(tok_c) * uint32_t(cx.qk_stride));
     }
-    const int tok4 = 16 * w + 4 * lq;
-    op.el = *reinterpret_cast<const float4*>(rec + kRecEl + tok4 * 4);
-    op.ed = *reinterpret_cast<const float4*>(rec + kRecEd + tok4 * 4);
-    op.eC = reinterpret_cast<const float*>(rec + kRecEl)[kChunk - 1];
+    const int tv = 16 * w + (l & 15);
+    const int tv_c = tv < len ? tv : len - 1;
+    const uint16_t* vb = cx.v + cx.t0(c) * cx.Hv * kHD + cx.h * kHD + cx.dv0 + 4 * (l >> 4);
+    op.v = *reinterpret_cast<const u32x2*>(vb + uint32_t(tv_c) * uint32_t(cx.Hv * kHD));
+    const char* rec = cx.rec(c);
+    op.e = *reinterpret_cast<const f32x4*>(rec + kRecEl + 128 * w + 16 * (l & 7));
+    const uint16_t* tb_hi = reinterpret_cast<const uint16_t*>(rec + kRecTbHi);
+    const uint16_t* tb_lo = reinterpret_cast<const uint16_t*>(rec + kRecTbLo);
+#pragma unroll
+    for (int s = 0; s < (kUpper ? 2 : 1); ++s) {
+        op.tbh[s] = load8(tb_hi + (64 * (2 * w + s) + l) * 8);
+        op.tbl[s] = load8(tb_lo + (64 * (2 * w + s) + l) * 8);
+    }
 }
 
-GDN_DEV void fetch_output(OutputOperands& op, const StatePassCtx& cx, int c, int w, int lr, int lq,
-                          int lg8) {
-    const int64_t t0 = cx.t0(c);
+template <bool kUpper>
+GDN_DEV void fetch_output(OutputOperands& op, const StatePassCtx& cx, int c, int w, int l) {
+    const int lr = l & 15, lg8 = 8 * (l >> 4);
     const int len = cx.len(c);
-    const char* rec = cx.rec(c);
     const int tok = 16 * w + lr;
     const int tok_c = tok < len ? tok : len - 1;
-    const uint16_t* qb = cx.q + t0 * cx.qk_stride + cx.hk * kHD;
+    const uint16_t* qb = cx.q + cx.t0(c) * cx.qk_stride + cx.hk * kHD;
     const uint32_t qoff = uint32_t(tok_c) * uint32_t(cx.qk_stride) + uint32_t(lg8);
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) op.qa[s] = load8(qb + qoff + 32 * s);
+    const char* rec = cx.rec(c);
     const uint16_t* p_hi = reinterpret_cast<const uint16_t*>(rec + kRecPHi);
     const uint16_t* p_lo = reinterpret_cast<const uint16_t*>(rec + kRecPLo);
-    const uint32_t roff = uint32_t(tok * kChunk + lg8);
 #pragma unroll
-    for (int s = 0; s < kChunk / 32; ++s) {
-        op.pah[s] = load8(p_hi + roff + 32 * s);
-        op.pal[s] = load8(p_lo + roff + 32 * s);
+    for (int s = 0; s < (kUpper ? 2 : 1); ++s) {
+        op.pah[s] = load8(p_hi + (64 * (2 * w + s) + l) * 8);
+        op.pal[s] = load8(p_lo + (64 * (2 * w + s) + l) * 8);
     }
-    op.el = *reinterpret_cast<const float4*>(rec + kRecEl + (16 * w + 4 * lq) * 4);
 }
 
 GDN_DEV uint2 pack4(const uint16_t (&x)[4]) {
@@ -397,17 +422,42 @@ GDN_DEV uint2 pack4(const uint16_t (&x)[4]) {
 struct StatePassLds {
     uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];  // S[dv][dk]
     uint16_t Kr[2][kChunk * kKS2];                                // K[token][dk], two buffers
+    uint16_t Tb_hi[kChunk * kTS], Tb_lo[kChunk * kTS];            // Tb[token][token]
+    uint16_t Vs[kChunk * kSliceRows];                             // V[token][dv]
     uint16_t Rs_hi[kSliceRows * kTS], Rs_lo[kSliceRows * kTS];    // R[dv][token]
     uint16_t Ds_hi[kSliceRows * kTS], Ds_lo[kSliceRows * kTS];    // D[dv][token]
     uint16_t D2_hi[kSliceRows * kTS], D2_lo[kSliceRows * kTS];    // D''[dv][token]
+    float ex[2 * kChunk];                                         // exp(l), exp(l_C - l)
 };
 
-// State waves, chunk part 1: the S operand (hi + lo) and the chunk's K rows
-// into LDS. Consuming the chunk's K registers here completes its loads
-// before the next chunk's prefetch is issued; K alternates between two
-// buffers so the previous chunk's state update may still read the other.
-GDN_DEV void state_stage(const StateOperands& op, const f32x4 (&acc)[2], StatePassLds& sm, int buf,
-                         int w, int lr, int lq, int lg8) {
+// Output waves: staged operands into LDS, in the layouts the state waves
+// read them with.
+GDN_DEV void stage_k(const StagedOperands& op, StatePassLds& sm, int buf, int w, int l) {
+    uint16_t* kr = sm.Kr[buf] + (16 * w + (l >> 4)) * kKS2 + 8 * (l & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<bf16x8*>(kr + 4 * i * kKS2) = op.ka[i];
+}
+
+GDN_DEV void stage_v(const StagedOperands& op, StatePassLds& sm, int w, int l) {
+    *reinterpret_cast<u32x2*>(sm.Vs + (16 * w + (l & 15)) * kSliceRows + 4 * (l >> 4)) = op.v;
+}
+
+// Lanes 8-63 repeat lanes 0-7 for the decay words (same words, same values):
+// an unconditional store keeps the operand registers out of any branch.
+template <bool kUpper>
+GDN_DEV void stage_tb_e(const StagedOperands& op, StatePassLds& sm, int w, int l) {
+    const int row = (16 * w + (l & 15)) * kTS + 8 * (l >> 4);
+#pragma unroll
+    for (int s = 0; s < (kUpper ? 2 : 1); ++s) {
+        *reinterpret_cast<bf16x8*>(sm.Tb_hi + row + 32 * s) = op.tbh[s];
+        *reinterpret_cast<bf16x8*>(sm.Tb_lo + row + 32 * s) = op.tbl[s];
+    }
+    *reinterpret_cast<f32x4*>(sm.ex + 32 * w + 4 * (l & 7)) = op.e;
+}
+
+// State waves, chunk part 1: the S operand (hi + lo) into LDS.
+GDN_DEV void state_stage(const f32x4 (&acc)[2], StatePassLds& sm, int w, int l) {
+    const int lr = l & 15, lq = l >> 4;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int dk = 32 * w + 16 * t + 4 * lq;
@@ -417,50 +467,62 @@ GDN_DEV void state_stage(const StateOperands& op, const f32x4 (&acc)[2], StatePa
         *reinterpret_cast<uint2*>(sm.Ss_hi + lr * kSS + dk) = pack4(hi);
         *reinterpret_cast<uint2*>(sm.Ss_lo + lr * kSS + dk) = pack4(lo);
     }
-    uint16_t* kr = sm.Kr[buf] + (16 * w + lr) * kKS2 + lg8;
-#pragma unroll
-    for (int s = 0; s < kHD / 32; ++s) *reinterpret_cast<bf16x8*>(kr + 32 * s) = op.ka[s];
 }
 
-// State waves, part 2 (between the staging and R barriers): R = V - exp(l) K S^T.
-GDN_DEV void state_residual(const StateOperands& op, StatePassLds& sm, int w, int lr, int lq, int lg8) {
+// State waves, part 2 (between the staging and R barriers):
+// R^T = V^T - S K^T diag(exp l), lane (dv = 4(l/16) + i, token = 16w + l%16).
+GDN_DEV void state_residual(const StatePassLds& sm, StatePassLds& smw, int buf, int w, int l) {
+    const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
+    const int tok = 16 * w + lr;
+    const uint16_t* kr = sm.Kr[buf] + tok * kKS2 + lg8;
     f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xk2 = xk;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        xk = mfma16(op.ka[s], load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), xk);
-        xk2 = mfma16(op.ka[s], load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xk2);
+        const bf16x8 kb = load8(kr + 32 * s);
+        xk = mfma16(load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), kb, xk);
+        xk2 = mfma16(load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), kb, xk2);
     }
     xk += xk2;
-    const float el[4] = {op.el.x, op.el.y, op.el.z, op.el.w};
-    uint16_t hi[4], lo[4];
+    const float el = sm.ex[tok];
+    const u32x2 vv = *reinterpret_cast<const u32x2*>(sm.Vs + tok * kSliceRows + 4 * lq);
+    const float v[4] = {__uint_as_float(vv[0] << 16), __uint_as_float(vv[0] & 0xffff0000u),
+                        __uint_as_float(vv[1] << 16), __uint_as_float(vv[1] & 0xffff0000u)};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) split_bf16(__uint_as_float(op.v[i] << 16) - el[i] * xk[i], hi[i], lo[i]);
-    const int tok0 = 16 * w + 4 * lq;
-    *reinterpret_cast<uint2*>(sm.Rs_hi + lr * kTS + tok0) = pack4(hi);
-    *reinterpret_cast<uint2*>(sm.Rs_lo + lr * kTS + tok0) = pack4(lo);
+    for (int i = 0; i < 4; ++i) {
+        uint16_t hi, lo;
+        split_bf16(v[i] - el * xk[i], hi, lo);
+        smw.Rs_hi[(4 * lq + i) * kTS + tok] = hi;
+        smw.Rs_lo[(4 * lq + i) * kTS + tok] = lo;
+    }
 }
 
 // State waves, part 3 (between the R and D barriers): D = Tb R, stored as
 // D (hi + lo, for Y) and D'' = exp(l_C - l) D (hi + lo, for the update).
-GDN_DEV void state_delta(const StateOperands& op, StatePassLds& sm, int w, int lr, int lq, int lg8) {
+template <bool kUpper>
+GDN_DEV void state_delta(StatePassLds& sm, int w, int l) {
+    const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
+    const int row = (16 * w + lr) * kTS + lg8;
     f32x4 d = {0.f, 0.f, 0.f, 0.f}, d2 = d;
 #pragma unroll
-    for (int s = 0; s < kChunk / 32; ++s) {
+    for (int s = 0; s < (kUpper ? 2 : 1); ++s) {
+        const bf16x8 th = load8(sm.Tb_hi + row + 32 * s);
+        const bf16x8 tl = load8(sm.Tb_lo + row + 32 * s);
         const bf16x8 bh = load8(sm.Rs_hi + lr * kTS + 32 * s + lg8);
         const bf16x8 bl = load8(sm.Rs_lo + lr * kTS + 32 * s + lg8);
-        d = mfma16(op.tbh[s], bh, d);
-        d2 = mfma16(op.tbh[s], bl, d2);
-        d2 = mfma16(op.tbl[s], bh, d2);
+        d = mfma16(th, bh, d);
+        d2 = mfma16(th, bl, d2);
+        d2 = mfma16(tl, bh, d2);
     }
     d += d2;
-    const float ed[4] = {op.ed.x, op.ed.y, op.ed.z, op.ed.w};
+    const int tok0 = 16 * w + 4 * lq;
+    const float4 ed = *reinterpret_cast<const float4*>(sm.ex + kChunk + tok0);
+    const float e4[4] = {ed.x, ed.y, ed.z, ed.w};
     uint16_t dh[4], dl[4], hi[4], lo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         split_bf16(d[i], dh[i], dl[i]);
-        split_bf16(ed[i] * d[i], hi[i], lo[i]);
+        split_bf16(e4[i] * d[i], hi[i], lo[i]);
     }
-    const int tok0 = 16 * w + 4 * lq;
     *reinterpret_cast<uint2*>(sm.Ds_hi + lr * kTS + tok0) = pack4(dh);
     *reinterpret_cast<uint2*>(sm.Ds_lo + lr * kTS + tok0) = pack4(dl);
     *reinterpret_cast<uint2*>(sm.D2_hi + lr * kTS + tok0) = pack4(hi);
@@ -472,13 +534,13 @@ GDN_DEV void state_delta(const StateOperands& op, StatePassLds& sm, int w, int l
 // read: within each 16-lane group, lane i of a ds_read_b64_tr_b16 receives
 // element i%4 of source lane i/4 + 4k (k = 0..3); source lane s of group g
 // points at K[8g + 4h + s/4][dk0 + 4(s%4)] for the tokens 8g + 4h .. +3.
-GDN_DEV void state_update(const StateOperands& op, f32x4 (&acc)[2], const StatePassLds& sm, int buf,
-                          int w, int l, int lr, int lg8) {
-    const int g = l >> 4, sl = l & 15;
+GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds& sm, int buf, float eC, int w,
+                          int l) {
+    const int g = l >> 4, sl = l & 15, lr = sl, lg8 = 8 * g;
     const uint16_t* kr = sm.Kr[buf];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        acc[t] *= op.eC;
+        acc[t] *= eC;
         f32x4 lo_acc = {0.f, 0.f, 0.f, 0.f};
         const int dk0 = 32 * w + 16 * t;
 #pragma unroll
@@ -500,7 +562,8 @@ GDN_DEV void state_update(const StateOperands& op, f32x4 (&acc)[2], const StateP
 }
 
 // Output waves, part 1 (between the staging and R barriers): exp(l) Q S^T.
-GDN_DEV f32x4 output_project(const OutputOperands& op, const StatePassLds& sm, int lr, int lg8) {
+GDN_DEV f32x4 output_project(const OutputOperands& op, const StatePassLds& sm, int w, int l) {
+    const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
     f32x4 xq = {0.f, 0.f, 0.f, 0.f}, xq2 = xq;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
@@ -508,21 +571,23 @@ GDN_DEV f32x4 output_project(const OutputOperands& op, const StatePassLds& sm, i
         xq2 = mfma16(op.qa[s], load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xq2);
     }
     xq += xq2;
-    xq[0] *= op.el.x;
-    xq[1] *= op.el.y;
-    xq[2] *= op.el.z;
-    xq[3] *= op.el.w;
+    const float4 el = *reinterpret_cast<const float4*>(sm.ex + 16 * w + 4 * lq);
+    xq[0] *= el.x;
+    xq[1] *= el.y;
+    xq[2] *= el.z;
+    xq[3] *= el.w;
     return xq;
 }
 
 // Output waves, part 2 (after the D barrier): y = exp(l) Q S^T + P D.
-template <class Y>
+template <class Y, bool kUpper>
 GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassLds& sm,
                           const StatePassCtx& cx, int c, typename Y::storage* __restrict__ y, int w,
-                          int lr, int lq, int lg8) {
+                          int l) {
+    const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
     f32x4 y2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < kChunk / 32; ++s) {
+    for (int s = 0; s < (kUpper ? 2 : 1); ++s) {
         const bf16x8 bh = load8(sm.Ds_hi + lr * kTS + 32 * s + lg8);
         const bf16x8 bl = load8(sm.Ds_lo + lr * kTS + 32 * s + lg8);
         yacc = mfma16(op.pah[s], bh, yacc);
@@ -537,6 +602,69 @@ GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassL
         const int tok = 16 * w + 4 * lq + i;
         if (tok < len) Y::store(y, ((t0 + tok) * cx.Hv + cx.h) * kHD + cx.dv0 + lr, yacc[i]);
     }
+}
+
+// Chunk c: [S] B1 [R | Q S^T, K(c+1)] B2 [D | V(c+1), fetch c+2] B3
+// [update | Tb(c+1), y]. Both loops are straight-line code (wave-uniform
+// roles), so the compiler's waits for loaded operands are exact and never
+// cover a later prefetch; both steps of the unrolled body are unconditional
+// (an odd last chunk runs after the loop), because a conditional second step
+// lets the compiler sink the first step's prefetch (invariant loads) to just
+// before its use. Chunk indices past the run repeat its last chunk, so every
+// fetch is unconditional.
+template <bool kUpper>
+GDN_DEV void state_loop(int nch, StatePassLds& sm, f32x4 (&acc)[2], int w, int l) {
+    auto step = [&](int buf) {
+        state_stage(acc, sm, w, l);
+        __syncthreads();
+        state_residual(sm, sm, buf, w, l);
+        const float eC = sm.ex[kChunk - 1];  // read before the next chunk restages it
+        __syncthreads();
+        state_delta<kUpper>(sm, w, l);
+        __syncthreads();
+        state_update(acc, sm, buf, eC, w, l);
+    };
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        step(0);
+        step(1);
+    }
+    if (c < nch) step(0);
+}
+
+template <class Y, bool kUpper>
+GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
+                         typename Y::storage* __restrict__ y, int w, int l) {
+    const int last = nch - 1;
+    StagedOperands ga, gb;
+    OutputOperands oa, ob;
+    // gn: staged operands of chunk c + 1 (in registers), gf: receives chunk c + 2
+    auto step = [&](int c, int buf, const OutputOperands& oc, OutputOperands& on,
+                    const StagedOperands& gn, StagedOperands& gf) {
+        __syncthreads();
+        const f32x4 yacc = output_project(oc, sm, w, l);
+        stage_k(gn, sm, buf ^ 1, w, l);
+        fetch_output<kUpper>(on, cx, c + 1 < last ? c + 1 : last, w, l);
+        __syncthreads();
+        stage_v(gn, sm, w, l);
+        fetch_staged<kUpper>(gf, cx, c + 2 < last ? c + 2 : last, w, l);
+        __syncthreads();
+        stage_tb_e<kUpper>(gn, sm, w, l);
+        output_store<Y, kUpper>(oc, yacc, sm, cx, c, y, w, l);
+    };
+    // chunk 0 into LDS; chunk 1 (or 0 again) into registers
+    fetch_staged<kUpper>(gb, cx, 0, w, l);
+    fetch_staged<kUpper>(ga, cx, 1 < last ? 1 : last, w, l);
+    fetch_output<kUpper>(oa, cx, 0, w, l);
+    stage_k(gb, sm, 0, w, l);
+    stage_v(gb, sm, w, l);
+    stage_tb_e<kUpper>(gb, sm, w, l);
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        step(c, 0, oa, ob, ga, gb);
+        step(c + 1, 1, ob, oa, gb, ga);
+    }
+    if (c < nch) step(c, 0, oa, ob, ga, gb);
 }
 
 template <class Y>
@@ -563,9 +691,10 @@ __global__ __launch_bounds__(kStateThreads) void prefill_state_kernel(
     }
     const int run = hr / Hv, h = hr % Hv;
     const int tid = threadIdx.x;
-    const bool state_wave = tid < 256;
-    const int w = (tid >> 6) & 3, l = tid & 63;
-    const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
+    // wave-uniform (scalar) so that the wave roles take scalar branches
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool state_wave = wave < 4;
+    const int w = wave & 3, l = tid & 63, lq = l >> 4, lr = l & 15;
 
     StatePassCtx cx;
     cx.q = q;
@@ -582,56 +711,29 @@ __global__ __launch_bounds__(kStateThreads) void prefill_state_kernel(
     cx.dv0 = slice * kSliceRows;
     const int nch = chunk_off[run + 1] - cx.c0;
 
-    // State waves keep S^T in accumulators:
-    // acc[t][i] = S^T[dk = 32w + 16t + 4(l/16) + i][dv = dv0 + l%16].
-    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    const int64_t sbase = ((int64_t(run) * Hv + h) * kHD + cx.dv0 + lr) * kHD;
-    if (state_wave && state_in) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const float4 s4 = *reinterpret_cast<const float4*>(state_in + sbase + 32 * w + 16 * t + 4 * lq);
-            acc[t] = f32x4{s4.x, s4.y, s4.z, s4.w};
-        }
-    }
-
-    // Chunk c: [stage] B1 [R | Q S^T] B2 [D] B3 [update | y]. Operands of
-    // chunk c + 1 are fetched right after B1, into the other register set.
-    StateOperands sa, sb;
-    OutputOperands oa, ob;
-    auto step = [&](int c, int buf, const StateOperands& sc, StateOperands& sn,
-                    const OutputOperands& oc, OutputOperands& on) {
-        if (state_wave) state_stage(sc, acc, sm, buf, w, lr, lq, lg8);
-        __syncthreads();
-        f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
-        if (state_wave) {
-            if (c + 1 < nch) fetch_state(sn, cx, c + 1, w, lr, lq, lg8);
-            state_residual(sc, sm, w, lr, lq, lg8);
-        } else {
-            if (c + 1 < nch) fetch_output(on, cx, c + 1, w, lr, lq, lg8);
-            yacc = output_project(oc, sm, lr, lg8);
-        }
-        __syncthreads();
-        if (state_wave) state_delta(sc, sm, w, lr, lq, lg8);
-        __syncthreads();
-        if (state_wave) state_update(sc, acc, sm, buf, w, l, lr, lg8);
-        else output_store<Y>(oc, yacc, sm, cx, c, y, w, lr, lq, lg8);
-    };
-    if (nch > 0) {
-        if (state_wave) fetch_state(sa, cx, 0, w, lr, lq, lg8);
-        else fetch_output(oa, cx, 0, w, lr, lq, lg8);
-    }
-    for (int c = 0; c < nch; c += 2) {
-        step(c, 0, sa, sb, oa, ob);
-        if (c + 1 >= nch) break;
-        step(c + 1, 1, sb, sa, ob, oa);
-    }
-
     if (state_wave) {
+        // S^T in accumulators: acc[t][i] = S^T[dk = 32w + 16t + 4(l/16) + i][dv = dv0 + l%16].
+        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        const int64_t sbase = ((int64_t(run) * Hv + h) * kHD + cx.dv0 + lr) * kHD;
+        if (state_in) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float4 s4 = *reinterpret_cast<const float4*>(state_in + sbase + 32 * w + 16 * t + 4 * lq);
+                acc[t] = f32x4{s4.x, s4.y, s4.z, s4.w};
+            }
+        }
+        if (nch > 0) {
+            if (w >= 2) state_loop<true>(nch, sm, acc, w, l);
+            else state_loop<false>(nch, sm, acc, w, l);
+        }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int dk = 32 * w + 16 * t + 4 * lq;
             *reinterpret_cast<float4*>(state_out + sbase + dk) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
         }
+    } else if (nch > 0) {
+        if (w >= 2) output_loop<Y, true>(cx, nch, sm, y, w, l);
+        else output_loop<Y, false>(cx, nch, sm, y, w, l);
     }
 }
 
@@ -668,6 +770,7 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
                  reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out) |
                  reinterpret_cast<uintptr_t>(workspace)) % 16 == 0,
                 "gdn_prefill_chunked: q, k, states and workspace must be 16-byte aligned");
+    GDN_REQUIRE(reinterpret_cast<uintptr_t>(v) % 8 == 0, "gdn_prefill_chunked: v must be 8-byte aligned");
     const int64_t need = records_offset(N) + chunks_bound(T_total, N) * Hv * kRecBytes;
     GDN_REQUIRE(workspace && workspace_bytes >= need,
                 "gdn_prefill_chunked: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
