@@ -146,7 +146,7 @@ int gdn_decode_step(const void *qkv, const void *conv_state_in, void *conv_state
  *   gate_mode 1: ga = g (T_total, Hv) float32, gb = beta (T_total, Hv) gb_dtype
  *   state_in: (N, Hv, Dv, Dk) float32 or NULL (zero state); state_out: (N, Hv, Dv, Dk),
  *             not aliasing state_in
- *   Hv / Hk <= 8; q, k, states and workspace 16-byte aligned, v 8-byte aligned
+ *   q, k, states and workspace 16-byte aligned, v 8-byte aligned
  *   y: (T_total, Hv, Dv) y_dtype
  *   workspace: device scratch of gdn_prefill_workspace_size(...) bytes
  * Specialised for Dk = Dv = 128. Equal, up to rounding, to gdn_scan on the

@@ -36,7 +36,6 @@ constexpr int kChunk = 64;
 constexpr int kHD = 128;                 // Dk = Dv
 constexpr int kSliceRows = 16;           // state rows per state-pass workgroup
 constexpr int kSlices = kHD / kSliceRows;
-constexpr int kMaxGroup = 8;             // value heads per key head handled by the chunk pass
 constexpr float kLogGateFloor = -80.f;   // exp(-80) ~ 1.8e-35: a reset state
 
 // Per (chunk, value head) record written by the chunk pass. Tb and P are
@@ -66,6 +65,10 @@ GDN_DEV uint16_t bf16_bits(float x) { return f32_to_bf16_bits(x); }
 GDN_DEV void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
     hi = bf16_bits(x);
     lo = bf16_bits(x - bf16_bits_to_f32(hi));
+}
+
+GDN_DEV uint2 pack4(const uint16_t (&x)[4]) {
+    return uint2{uint32_t(x[0]) | (uint32_t(x[1]) << 16), uint32_t(x[2]) | (uint32_t(x[3]) << 16)};
 }
 
 GDN_DEV bf16x8 load8(const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); }
@@ -116,26 +119,17 @@ GDN_DEV ChunkPos locate_chunk(const int32_t* chunk_off, const int32_t* cu, int N
 // ---------------------------------------------------------------------------
 
 constexpr int kKS = kHD + 8;    // bf16 row stride of the K/Q tiles
-constexpr int kFS = kChunk + 1; // float row stride of the A/T tiles
-
-// One wave: acc += A_blk * B_blk for 16 x 16 blocks held in LDS with row
-// stride kFS; lane (m = l/4, n0 = 4 (l%4)) owns acc = out[m][n0..n0+3].
-GDN_DEV void block_mma(float (&acc)[4], const float* A, const float* B, int m, int n0) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const float a = A[m * kFS + k];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] += a * B[k * kFS + n0 + q];
-    }
-}
+constexpr int kFS = kChunk + 1; // float row stride of the A/T/P tiles
+constexpr float kLog2e = 1.4426950408889634f;
 
 // Stores a lower-triangular 64 x 64 float32 tile held in LDS (row stride
-// kFS) as bf16 hi + lo fragments (layout above), 16 bytes per lane. With
-// col_scale (T diag(beta)): the diagonal is taken as 1 and column j is
-// scaled by col_scale[j]; without it, entries above the diagonal are zero.
+// kFS) as bf16 hi + lo fragments (layout above), 16 bytes per lane, by
+// `nthreads` threads numbered `t`. With col_scale (T diag(beta)): the
+// diagonal is taken as 1 and column j is scaled by col_scale[j]; without it,
+// entries above the diagonal are zero.
 GDN_DEV void store_fragments(const float* M, uint16_t* hi_out, uint16_t* lo_out,
-                             const float* col_scale, int tid) {
-    for (int item = tid; item < 6 * 64; item += 256) {
+                             const float* col_scale, int t, int nthreads) {
+    for (int item = t; item < 6 * 64; item += nthreads) {
         const int fi = item >> 6, ln = item & 63;
         const int f = fi < 2 ? 2 * fi : fi + 2;  // skip fragments 1 and 3
         const int i = 16 * (f >> 1) + (ln & 15), j0 = 32 * (f & 1) + 8 * (ln >> 4);
@@ -156,154 +150,204 @@ GDN_DEV void store_fragments(const float* M, uint16_t* hi_out, uint16_t* lo_out,
     }
 }
 
-__global__ __launch_bounds__(256) void prefill_chunk_kernel(
+// The four diagonal blocks of T = (I + A)^-1 (A strictly lower triangular),
+// by one wave: lane (b = l/16, n = l%16) solves (I + A_bb) x = e_n by
+// column-oriented forward substitution and writes x as column n of T_bb.
+GDN_DEV void diag_inverse(const float* As, float* Ts, int l) {
+    const int b = l >> 4, n = l & 15;
+    const float* Ab = As + 16 * b * kFS + 16 * b;
+    float s[16], x[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) s[m] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        x[k] = k == n ? 1.f : (k > n ? -s[k] : 0.f);
+#pragma unroll
+        for (int m = k + 1; m < 16; ++m) s[m] += Ab[m * kFS + k] * x[k];
+    }
+    float* Tb = Ts + 16 * b * kFS + 16 * b;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) Tb[m * kFS + n] = x[m];
+}
+
+// acc += X Y for 16 x 16 float32 blocks in LDS (row stride kFS), on
+// v_mfma_f32_16x16x4f32 (lane l: X[l%16][4kb + l/16], Y[4kb + l/16][l%16];
+// acc[i] = (XY)[4(l/16) + i][l%16]).
+GDN_DEV f32x4 mma_f32(const float* X, const float* Y, f32x4 acc, int l) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        const float a = X[(l & 15) * kFS + 4 * kb + (l >> 4)];
+        const float b = Y[(4 * kb + (l >> 4)) * kFS + (l & 15)];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+    }
+    return acc;
+}
+
+GDN_DEV void put_block(float* O, f32x4 v, float scale, int l) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) O[(4 * (l >> 4) + i) * kFS + (l & 15)] = scale * v[i];
+}
+
+GDN_DEV float* blk(float* M, int bi, int bj) { return M + 16 * bi * kFS + 16 * bj; }
+GDN_DEV const float* blk(const float* M, int bi, int bj) { return M + 16 * bi * kFS + 16 * bj; }
+
+// Off-diagonal blocks of T from its diagonal blocks, by recursive doubling
+// over 16 x 16 blocks (T_ij = -T_ii sum_k A_ik T_kj): first the two 32 x 32
+// diagonal halves, then T[2:4, 0:2] = -T[2:4, 2:4] (A[2:4, 0:2] T[0:2, 0:2]).
+// The intermediate product X_ij is kept in A's (all-zero, unread) block
+// (j, i) above the diagonal. Ends with a barrier.
+GDN_DEV void offdiag_inverse(float* As, float* Ts, int w, int l) {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    if (w < 2) {  // T_10 (wave 0), T_32 (wave 1)
+        const int j = 2 * w, i = j + 1;
+        put_block(blk(As, j, i), mma_f32(blk(As, i, j), blk(Ts, j, j), zero, l), 1.f, l);
+        put_block(blk(Ts, i, j), mma_f32(blk(Ts, i, i), blk(As, j, i), zero, l), -1.f, l);
+    }
+    __syncthreads();
+    const int i = 2 + (w >> 1), j = w & 1;  // one block of T[2:4, 0:2] per wave
+    f32x4 x = zero;
+    for (int k = j; k < 2; ++k) x = mma_f32(blk(As, i, k), blk(Ts, k, j), x, l);
+    put_block(blk(As, j, i), x, 1.f, l);
+    __syncthreads();
+    f32x4 t = zero;
+    for (int k = 2; k <= i; ++k) t = mma_f32(blk(Ts, i, k), blk(As, j, k), t, l);
+    put_block(blk(Ts, i, j), t, -1.f, l);
+    __syncthreads();
+}
+
+// One workgroup per (chunk, value head). K K^T and K Q^T depend only on the
+// key head, but recomputing them per value head (32 MFMAs per wave) keeps
+// each workgroup small enough for several to share a CU. Workgroup ids go
+// round-robin over the 8 XCDs, so the r = Hv/Hk value heads of one
+// (chunk, key head) take ids 8 apart: same XCD, dispatched together, so all
+// but the first read that chunk's K and Q from the XCD's L2.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_chunk_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const void* __restrict__ ga,
     const void* __restrict__ gb, int gb_dtype, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, const int32_t* __restrict__ cu, int N,
     int64_t L_uniform, const int32_t* __restrict__ chunk_off, char* __restrict__ records, int Hk,
     int Hv) {
-    // K/Q tiles first; once K K^T and Q K^T are in registers the same bytes
-    // hold the A and T matrices of one value head at a time.
+    // K/Q tiles first; once K K^T and K Q^T are in registers the same bytes
+    // hold the A and T matrices.
     __shared__ __attribute__((aligned(16))) char smem[2 * kChunk * kKS * 2];
-    __shared__ float l_sh[kMaxGroup][kChunk], beta_sh[kMaxGroup][kChunk];
-    __shared__ float wtmp[4][16 * kFS];
+    __shared__ __attribute__((aligned(16))) float l2_sh[kChunk], beta_sh[kChunk];
     uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
     uint16_t* Qs = Ks + kChunk * kKS;
     float* As = reinterpret_cast<float*>(smem);
     float* Ts = As + kChunk * kFS;
 
-    const int g = blockIdx.x, hk = blockIdx.y;
+    const int r = Hv / Hk;
+    const int id = blockIdx.x, e = (id >> 3) % r;
+    const int item = (id / (8 * r)) * 8 + (id & 7);  // (chunk, key head)
+    const int g = item / Hk, hk = item % Hk, hv = hk * r + e;
     if (g >= chunk_off[N]) return;
     const ChunkPos pos = locate_chunk(chunk_off, cu, N, L_uniform, g);
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-    const int r = Hv / Hk;
+    char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
 
-    // K and Q of the chunk (rows past the run are zero).
-    for (int idx = tid; idx < kChunk * (kHD / 8); idx += 256) {
-        const int row = idx / (kHD / 8), seg = idx % (kHD / 8);
-        uint4 kv = {0, 0, 0, 0}, qv = {0, 0, 0, 0};
-        if (row < pos.len) {
-            const int64_t off = ((pos.t0 + row) * Hk + hk) * kHD + seg * 8;
-            kv = *reinterpret_cast<const uint4*>(k + off);
-            qv = *reinterpret_cast<const uint4*>(q + off);
-        }
-        *reinterpret_cast<uint4*>(Ks + row * kKS + seg * 8) = kv;
-        *reinterpret_cast<uint4*>(Qs + row * kKS + seg * 8) = qv;
+    // K and Q of the chunk: every load issued before the first LDS store
+    // (rows past the run are read clamped and stored as zero).
+    u16x8 kv[4], qv[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int row = (tid + 256 * it) >> 4, seg = tid & 15;
+        const int rc = row < pos.len ? row : pos.len - 1;
+        const int64_t off = ((pos.t0 + rc) * Hk + hk) * kHD + seg * 8;
+        kv[it] = *reinterpret_cast<const u16x8*>(k + off);
+        qv[it] = *reinterpret_cast<const u16x8*>(q + off);
     }
-    // Gates of the group's value heads: lane = token; l = inclusive prefix sum of log g.
-    for (int e = w; e < r; e += 4) {
-        const int hv = hk * r + e;
-        float lg = 0.f, beta = 0.f;
-        if (l < pos.len) {
-            const int64_t i = (pos.t0 + l) * Hv + hv;
-            if (gate_mode == 0) {
-                lg = log_forget_gate(load_any(ga, i, gb_dtype), A_log[hv], dt_bias[hv]);
-                beta = round_to(sigmoid(load_any(gb, i, gb_dtype)), gb_dtype);
-            } else {
-                const float gv = static_cast<const float*>(ga)[i];
-                lg = gv > 0.f ? logf(gv) : kLogGateFloor;
-                beta = load_any(gb, i, gb_dtype);
-            }
-            lg = fmaxf(lg, kLogGateFloor);
+    // Gates (wave 0, lane = token): l2 = inclusive prefix sum of log2 g
+    // (exp2 of differences gives the decays).
+    if (w == 0) {
+        const int lc = l < pos.len ? l : pos.len - 1;
+        const int64_t i = (pos.t0 + lc) * Hv + hv;
+        float lg, beta;
+        if (gate_mode == 0) {
+            lg = log_forget_gate(load_any(ga, i, gb_dtype), A_log[hv], dt_bias[hv]);
+            beta = round_to(sigmoid(load_any(gb, i, gb_dtype)), gb_dtype);
+        } else {
+            const float gv = static_cast<const float*>(ga)[i];
+            lg = gv > 0.f ? logf(gv) : kLogGateFloor;
+            beta = load_any(gb, i, gb_dtype);
         }
+        lg = l < pos.len ? fmaxf(lg, kLogGateFloor) * kLog2e : 0.f;
+        beta = l < pos.len ? beta : 0.f;
 #pragma unroll
         for (int off = 1; off < kChunk; off <<= 1) {
             const float y = __shfl_up(lg, off, kWave);
             if (l >= off) lg += y;
         }
-        l_sh[e][l] = lg;
-        beta_sh[e][l] = beta;
+        l2_sh[l] = lg;
+        beta_sh[l] = beta;
         const float lC = __shfl(lg, kChunk - 1, kWave);
-        char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
-        reinterpret_cast<float*>(rec + kRecEl)[l] = expf(lg);
-        reinterpret_cast<float*>(rec + kRecEd)[l] = expf(lC - lg);
+        reinterpret_cast<float*>(rec + kRecEl)[l] = exp2f(lg);
+        reinterpret_cast<float*>(rec + kRecEd)[l] = exp2f(lC - lg);
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int row = (tid + 256 * it) >> 4, seg = tid & 15;
+        const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+        *reinterpret_cast<u16x8*>(Ks + row * kKS + seg * 8) = row < pos.len ? kv[it] : z;
+        *reinterpret_cast<u16x8*>(Qs + row * kKS + seg * 8) = row < pos.len ? qv[it] : z;
     }
     __syncthreads();
 
-    // K K^T and Q K^T: wave w owns token rows 16w..16w+15, all four column tiles.
-    f32x4 kk[4], qk[4];
+    // K K^T and K Q^T: wave w owns key rows 16w..16w+15, all four column
+    // tiles; kk[jt][ii] = k_i . k_j and kq[jt][ii] = k_i . q_j for
+    // i = 16w + 4(l/16) + ii, j = 16jt + l%16.
+    f32x4 kk[4], kq[4];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) kk[jt] = qk[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int lr = l & 15, lg8 = 8 * (l >> 4);
+    for (int jt = 0; jt < 4; ++jt) kk[jt] = kq[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
         const bf16x8 ak = load8(Ks + (16 * w + lr) * kKS + 32 * s + lg8);
-        const bf16x8 aq = load8(Qs + (16 * w + lr) * kKS + 32 * s + lg8);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-            const bf16x8 bk = load8(Ks + (16 * jt + lr) * kKS + 32 * s + lg8);
-            kk[jt] = mfma16(ak, bk, kk[jt]);
-            qk[jt] = mfma16(aq, bk, qk[jt]);
+            kk[jt] = mfma16(ak, load8(Ks + (16 * jt + lr) * kKS + 32 * s + lg8), kk[jt]);
+            kq[jt] = mfma16(ak, load8(Qs + (16 * jt + lr) * kKS + 32 * s + lg8), kq[jt]);
         }
     }
     __syncthreads();  // K/Q tiles are dead from here on
 
-    const int m = l >> 2, n0 = 4 * (l & 3);
-    for (int e = 0; e < r; ++e) {
-        const int hv = hk * r + e;
-        char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
-        // P and A from the accumulators: element (i, j) with
-        // i = 16w + 4(l/16) + ii, j = 16jt + l%16. P goes through LDS (the
-        // off-diagonal scratch, free until then) to be stored as fragments.
-        float* Ps = &wtmp[0][0];
+    // A (row i, column j) into LDS and P (query j, key i) straight from the
+    // accumulators into its fragments: lane (l%16, l/16) of wave w holds keys
+    // 16w + 4(l/16) .. +3 of query 16jt + l%16, which is half of the 16-byte
+    // entry (query row l%16, keys 8g .. 8g+7) of fragment (jt, w/2), with
+    // g = 2(w%2) + (l/16)/2, half (l/16)%2. Fragments above the diagonal
+    // (jt < 2 <= w) are skipped.
+    const float4 li = *reinterpret_cast<const float4*>(l2_sh + 16 * w + 4 * lq);
+    const float4 bi = *reinterpret_cast<const float4*>(beta_sh + 16 * w + 4 * lq);
+    const float l2i[4] = {li.x, li.y, li.z, li.w}, betai[4] = {bi.x, bi.y, bi.z, bi.w};
+    uint16_t* p_hi = reinterpret_cast<uint16_t*>(rec + kRecPHi);
+    uint16_t* p_lo = reinterpret_cast<uint16_t*>(rec + kRecPLo);
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
+    for (int jt = 0; jt < 4; ++jt) {
+        const int j = 16 * jt + lr;
+        const float l2j = l2_sh[j];
+        uint16_t ph[4], pl[4];
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                const int i = 16 * w + 4 * (l >> 4) + ii, j = 16 * jt + lr;
-                const float dec = i >= j ? expf(l_sh[e][i] - l_sh[e][j]) : 0.f;
-                Ps[i * kFS + j] = qk[jt][ii] * dec;
-                As[i * kFS + j] = i > j ? beta_sh[e][i] * kk[jt][ii] * dec : 0.f;
-            }
+        for (int ii = 0; ii < 4; ++ii) {
+            const int i = 16 * w + 4 * lq + ii;
+            const float d = l2i[ii] - l2j;  // <= 0 for i >= j, >= 0 for i <= j
+            const float dki = exp2f(i > j ? d : -d);
+            As[i * kFS + j] = i > j ? betai[ii] * kk[jt][ii] * dki : 0.f;
+            split_bf16(i <= j ? kq[jt][ii] * dki : 0.f, ph[ii], pl[ii]);
         }
-        __syncthreads();
-        store_fragments(Ps, reinterpret_cast<uint16_t*>(rec + kRecPHi),
-                        reinterpret_cast<uint16_t*>(rec + kRecPLo), nullptr, tid);
-
-        // T = (I + A)^-1 by 16 x 16 blocks. Diagonal blocks by forward
-        // substitution (lane n < 16 owns column n).
-        if (l < 16) {
-            float col[16];
-#pragma unroll
-            for (int mm = 0; mm < 16; ++mm) col[mm] = mm == l ? 1.f : 0.f;
-            const float* Ab = As + (16 * w) * kFS + 16 * w;
-#pragma unroll
-            for (int mm = 1; mm < 16; ++mm) {
-                float sum = 0.f;
-#pragma unroll
-                for (int kk2 = 0; kk2 < mm; ++kk2) sum += Ab[mm * kFS + kk2] * col[kk2];
-                if (mm > l) col[mm] = -sum;
-            }
-            float* Tb = Ts + (16 * w) * kFS + 16 * w;
-#pragma unroll
-            for (int mm = 0; mm < 16; ++mm) Tb[mm * kFS + l] = col[mm];
+        if (w < 2 || jt >= 2) {
+            const int f = 2 * jt + (w >> 1), ln = 16 * (2 * (w & 1) + (lq >> 1)) + lr;
+            const int off = (64 * f + ln) * 8 + 4 * (lq & 1);
+            *reinterpret_cast<uint2*>(p_hi + off) = pack4(ph);
+            *reinterpret_cast<uint2*>(p_lo + off) = pack4(pl);
         }
-        __syncthreads();
-        // Off-diagonal blocks by block diagonals: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj.
-        for (int dist = 1; dist < 4; ++dist) {
-            const int bj = w, bi = w + dist;
-            const bool active = bi < 4;
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
-            if (active) {
-                for (int bk = bj; bk < bi; ++bk)
-                    block_mma(acc, As + (16 * bi) * kFS + 16 * bk, Ts + (16 * bk) * kFS + 16 * bj, m, n0);
-#pragma unroll
-                for (int qq = 0; qq < 4; ++qq) wtmp[w][m * kFS + n0 + qq] = acc[qq];
-            }
-            __syncthreads();
-            if (active) {
-                float out[4] = {0.f, 0.f, 0.f, 0.f};
-                block_mma(out, Ts + (16 * bi) * kFS + 16 * bi, wtmp[w], m, n0);
-#pragma unroll
-                for (int qq = 0; qq < 4; ++qq) Ts[(16 * bi + m) * kFS + 16 * bj + n0 + qq] = -out[qq];
-            }
-            __syncthreads();
-        }
-        // Tb = T diag(beta), split into bf16 hi + lo.
-        store_fragments(Ts, reinterpret_cast<uint16_t*>(rec + kRecTbHi),
-                        reinterpret_cast<uint16_t*>(rec + kRecTbLo), beta_sh[e], tid);
-        __syncthreads();  // As / Ts / Ps are reused by the next value head
     }
+    __syncthreads();
+    if (w == 0) diag_inverse(As, Ts, l);  // T's diagonal blocks
+    __syncthreads();
+    offdiag_inverse(As, Ts, w, l);
+    // Tb = T diag(beta), split into bf16 hi + lo.
+    store_fragments(Ts, reinterpret_cast<uint16_t*>(rec + kRecTbHi),
+                    reinterpret_cast<uint16_t*>(rec + kRecTbLo), beta_sh, tid, 256);
 }
 
 // ---------------------------------------------------------------------------
@@ -311,7 +355,7 @@ __global__ __launch_bounds__(256) void prefill_chunk_kernel(
 // ---------------------------------------------------------------------------
 
 constexpr int kSS = kHD + 8;     // bf16 row stride of the S operand tile
-constexpr int kKS2 = kHD + 8;    // bf16 row stride of the row-major K tile
+constexpr int kQS = kHD + 8;     // bf16 row stride of the Q tile
 constexpr int kTS = kChunk + 8;  // bf16 row stride of token-minor operand tiles
 
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -334,15 +378,14 @@ constexpr int kStateThreads = 512;
 // through registers on the way to LDS, so each load covers whole rows (full
 // cache lines): 16 lanes per 256-byte K row, 8 per 128-byte Tb row.
 struct StagedOperands {
-    bf16x8 ka[4];           // K row 16w + 4i + l/16, dk 8(l%16) .. +7
+    bf16x8 ka[4], qa[4];    // K, Q row 16w + 4i + l/16, dk 8(l%16) .. +7
     bf16x8 tbh[2], tbl[2];  // Tb fragments (2w + s) (hi, lo): row 16w + l%16, tokens 32s + 8(l/16) .. +7
-    u32x2 v;                // V (bf16) at token 16w + l%16, dv dv0 + 4(l/16) .. +3
+    u32x2 v;                // V (bf16) at token 16w + l/4, dv dv0 + 4(l%4) .. +3
     f32x4 e;                // words 32w + 4(l%8) .. +3 of the record's [exp(l) | exp(l_C - l)]
 };
 
-// Operands of output wave w itself.
+// P fragments of output wave w (used from registers).
 struct OutputOperands {
-    bf16x8 qa[4];           // Q rows 16w + l%16
     bf16x8 pah[2], pal[2];  // P rows 16w + l%16 (hi, lo)
 };
 
@@ -373,16 +416,22 @@ struct StatePassCtx {
 template <bool kUpper>
 GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int w, int l) {
     const int len = cx.len(c);
-    const uint16_t* kb = cx.k + cx.t0(c) * cx.qk_stride + cx.hk * kHD + 8 * (l & 15);
+    const int64_t qk0 = cx.t0(c) * cx.qk_stride + cx.hk * kHD + 8 * (l & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tok = 16 * w + 4 * i + (l >> 4);
         const int tok_c = tok < len ? tok : len - 1;
-        op.ka[i] = load8(kb + uint32_t(tok_c) * uint32_t(cx.qk_stride));
+        op.ka[i] = load8(cx.k + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride));
     }
-    const int tv = 16 * w + (l & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tok = 16 * w + 4 * i + (l >> 4);
+        const int tok_c = tok < len ? tok : len - 1;
+        op.qa[i] = load8(cx.q + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride));
+    }
+    const int tv = 16 * w + (l >> 2);
     const int tv_c = tv < len ? tv : len - 1;
-    const uint16_t* vb = cx.v + cx.t0(c) * cx.Hv * kHD + cx.h * kHD + cx.dv0 + 4 * (l >> 4);
+    const uint16_t* vb = cx.v + cx.t0(c) * cx.Hv * kHD + cx.h * kHD + cx.dv0 + 4 * (l & 3);
     op.v = *reinterpret_cast<const u32x2*>(vb + uint32_t(tv_c) * uint32_t(cx.Hv * kHD));
     const char* rec = cx.rec(c);
     op.e = *reinterpret_cast<const f32x4*>(rec + kRecEl + 128 * w + 16 * (l & 7));
@@ -397,14 +446,6 @@ GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int
 
 template <bool kUpper>
 GDN_DEV void fetch_output(OutputOperands& op, const StatePassCtx& cx, int c, int w, int l) {
-    const int lr = l & 15, lg8 = 8 * (l >> 4);
-    const int len = cx.len(c);
-    const int tok = 16 * w + lr;
-    const int tok_c = tok < len ? tok : len - 1;
-    const uint16_t* qb = cx.q + cx.t0(c) * cx.qk_stride + cx.hk * kHD;
-    const uint32_t qoff = uint32_t(tok_c) * uint32_t(cx.qk_stride) + uint32_t(lg8);
-#pragma unroll
-    for (int s = 0; s < kHD / 32; ++s) op.qa[s] = load8(qb + qoff + 32 * s);
     const char* rec = cx.rec(c);
     const uint16_t* p_hi = reinterpret_cast<const uint16_t*>(rec + kRecPHi);
     const uint16_t* p_lo = reinterpret_cast<const uint16_t*>(rec + kRecPLo);
@@ -415,13 +456,10 @@ GDN_DEV void fetch_output(OutputOperands& op, const StatePassCtx& cx, int c, int
     }
 }
 
-GDN_DEV uint2 pack4(const uint16_t (&x)[4]) {
-    return uint2{uint32_t(x[0]) | (uint32_t(x[1]) << 16), uint32_t(x[2]) | (uint32_t(x[3]) << 16)};
-}
-
 struct StatePassLds {
     uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];  // S[dv][dk]
-    uint16_t Kr[2][kChunk * kKS2];                                // K[token][dk], two buffers
+    uint16_t Kr[2][kChunk * kHD];                                 // K[token][dk] (swizzled), two buffers
+    uint16_t Qs[kChunk * kQS];                                   // Q[token][dk]
     uint16_t Tb_hi[kChunk * kTS], Tb_lo[kChunk * kTS];            // Tb[token][token]
     uint16_t Vs[kChunk * kSliceRows];                             // V[token][dv]
     uint16_t Rs_hi[kSliceRows * kTS], Rs_lo[kSliceRows * kTS];    // R[dv][token]
@@ -430,16 +468,33 @@ struct StatePassLds {
     float ex[2 * kChunk];                                         // exp(l), exp(l_C - l)
 };
 
+// The K tile is read three ways: whole rows (staging), 16 rows at one
+// 16-byte granule (K as an MFMA operand) and 4-row x 32-byte blocks (the
+// transposing read). Rows are unpadded and granule G of row r is stored at
+// G ^ kswz(r), which keeps all three free of LDS bank conflicts: kswz is a
+// bijection of r % 16, and its upper three bits (r%4, bit 3 of r) differ
+// across the 8 rows one transposing read pass touches.
+GDN_DEV int kswz(int r) { return (((r & 3) | ((r >> 1) & 4)) << 1) | ((r >> 2) & 1); }
+GDN_DEV int kr_off(int r, int G) { return r * kHD + ((G ^ kswz(r)) << 3); }
+
 // Output waves: staged operands into LDS, in the layouts the state waves
 // read them with.
 GDN_DEV void stage_k(const StagedOperands& op, StatePassLds& sm, int buf, int w, int l) {
-    uint16_t* kr = sm.Kr[buf] + (16 * w + (l >> 4)) * kKS2 + 8 * (l & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<bf16x8*>(kr + 4 * i * kKS2) = op.ka[i];
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<bf16x8*>(sm.Kr[buf] + kr_off(16 * w + 4 * i + (l >> 4), l & 15)) = op.ka[i];
+}
+
+// Wave w's Q rows are read only by wave w (in output_project), so the next
+// chunk's may be written as soon as this wave's projection has read them.
+GDN_DEV void stage_q(const StagedOperands& op, StatePassLds& sm, int w, int l) {
+    uint16_t* qr = sm.Qs + (16 * w + (l >> 4)) * kQS + 8 * (l & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<bf16x8*>(qr + 4 * i * kQS) = op.qa[i];
 }
 
 GDN_DEV void stage_v(const StagedOperands& op, StatePassLds& sm, int w, int l) {
-    *reinterpret_cast<u32x2*>(sm.Vs + (16 * w + (l & 15)) * kSliceRows + 4 * (l >> 4)) = op.v;
+    *reinterpret_cast<u32x2*>(sm.Vs + (16 * w + (l >> 2)) * kSliceRows + 4 * (l & 3)) = op.v;
 }
 
 // Lanes 8-63 repeat lanes 0-7 for the decay words (same words, same values):
@@ -474,11 +529,10 @@ GDN_DEV void state_stage(const f32x4 (&acc)[2], StatePassLds& sm, int w, int l) 
 GDN_DEV void state_residual(const StatePassLds& sm, StatePassLds& smw, int buf, int w, int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
     const int tok = 16 * w + lr;
-    const uint16_t* kr = sm.Kr[buf] + tok * kKS2 + lg8;
     f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xk2 = xk;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        const bf16x8 kb = load8(kr + 32 * s);
+        const bf16x8 kb = load8(sm.Kr[buf] + kr_off(tok, 4 * s + lq));
         xk = mfma16(load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), kb, xk);
         xk2 = mfma16(load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), kb, xk2);
     }
@@ -530,10 +584,10 @@ GDN_DEV void state_delta(StatePassLds& sm, int w, int l) {
 }
 
 // State waves, part 4 (after the D barrier): S^T <- exp(l_C) S^T + K^T D''.
-// The K^T operand is read from the row-major K tile with the transposing LDS
-// read: within each 16-lane group, lane i of a ds_read_b64_tr_b16 receives
-// element i%4 of source lane i/4 + 4k (k = 0..3); source lane s of group g
-// points at K[8g + 4h + s/4][dk0 + 4(s%4)] for the tokens 8g + 4h .. +3.
+// The K^T operand is read from the K tile with the transposing LDS read:
+// within each 16-lane group, lane i of a ds_read_b64_tr_b16 receives element
+// i%4 of source lane i/4 + 4k (k = 0..3); source lane s of group g points at
+// K[8g + 4h + s/4][dk0 + 4(s%4)] for the tokens 8g + 4h .. +3.
 GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds& sm, int buf, float eC, int w,
                           int l) {
     const int g = l >> 4, sl = l & 15, lr = sl, lg8 = 8 * g;
@@ -548,7 +602,8 @@ GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds& sm, int buf, floa
             v4s parts[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                const uint16_t* src = kr + (32 * s + 8 * g + 4 * hh + (sl >> 2)) * kKS2 + dk0 + 4 * (sl & 3);
+                const int r = 32 * s + 8 * g + 4 * hh + (sl >> 2);
+                const uint16_t* src = kr + kr_off(r, (dk0 >> 3) + ((sl & 3) >> 1)) + 4 * (sl & 1);
                 parts[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                     (__attribute__((address_space(3))) v4s*)(src));
             }
@@ -562,13 +617,15 @@ GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds& sm, int buf, floa
 }
 
 // Output waves, part 1 (between the staging and R barriers): exp(l) Q S^T.
-GDN_DEV f32x4 output_project(const OutputOperands& op, const StatePassLds& sm, int w, int l) {
+GDN_DEV f32x4 output_project(const StatePassLds& sm, int w, int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
+    const uint16_t* qr = sm.Qs + (16 * w + lr) * kQS + lg8;
     f32x4 xq = {0.f, 0.f, 0.f, 0.f}, xq2 = xq;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        xq = mfma16(op.qa[s], load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), xq);
-        xq2 = mfma16(op.qa[s], load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xq2);
+        const bf16x8 qa = load8(qr + 32 * s);
+        xq = mfma16(qa, load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), xq);
+        xq2 = mfma16(qa, load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xq2);
     }
     xq += xq2;
     const float4 el = *reinterpret_cast<const float4*>(sm.ex + 16 * w + 4 * lq);
@@ -604,7 +661,7 @@ GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassL
     }
 }
 
-// Chunk c: [S] B1 [R | Q S^T, K(c+1)] B2 [D | V(c+1), fetch c+2] B3
+// Chunk c: [S] B1 [R | Q S^T, Q and K(c+1)] B2 [D | V(c+1), fetch c+2] B3
 // [update | Tb(c+1), y]. Both loops are straight-line code (wave-uniform
 // roles), so the compiler's waits for loaded operands are exact and never
 // cover a later prefetch; both steps of the unrolled body are unconditional
@@ -642,7 +699,8 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
     auto step = [&](int c, int buf, const OutputOperands& oc, OutputOperands& on,
                     const StagedOperands& gn, StagedOperands& gf) {
         __syncthreads();
-        const f32x4 yacc = output_project(oc, sm, w, l);
+        const f32x4 yacc = output_project(sm, w, l);
+        stage_q(gn, sm, w, l);
         stage_k(gn, sm, buf ^ 1, w, l);
         fetch_output<kUpper>(on, cx, c + 1 < last ? c + 1 : last, w, l);
         __syncthreads();
@@ -656,6 +714,7 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
     fetch_staged<kUpper>(gb, cx, 0, w, l);
     fetch_staged<kUpper>(ga, cx, 1 < last ? 1 : last, w, l);
     fetch_output<kUpper>(oa, cx, 0, w, l);
+    stage_q(gb, sm, w, l);
     stage_k(gb, sm, 0, w, l);
     stage_v(gb, sm, w, l);
     stage_tb_e<kUpper>(gb, sm, w, l);
@@ -758,7 +817,6 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
                 "gdn_prefill_chunked: bad sizes");
     if (Dk != kHD || Dv != kHD)
         return fail(GDN_EUNSUPPORTED, "gdn_prefill_chunked: specialised for Dk=Dv=128 (got %d, %d)", Dk, Dv);
-    GDN_REQUIRE(Hv / Hk <= kMaxGroup, "gdn_prefill_chunked: more than %d value heads per key head", kMaxGroup);
     GDN_REQUIRE(gate_mode == 0 || gate_mode == 1, "gdn_prefill_chunked: gate_mode must be 0 or 1");
     GDN_REQUIRE(valid_dtype(gb_dtype) && valid_dtype(y_dtype), "gdn_prefill_chunked: bad dtype");
     GDN_REQUIRE(gate_mode == 1 || (A_log && dt_bias), "gdn_prefill_chunked: gate_mode 0 needs A_log, dt_bias");
@@ -788,7 +846,8 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(64), 0, s, cu_seqlens, N, L_uniform, chunk_off);
     if (int rc = check_launch("gdn_prefill_chunked/offsets")) return rc;
     const int64_t nchunks = chunks_bound(T_total, N);
-    hipLaunchKernelGGL(prefill_chunk_kernel, dim3(unsigned(nchunks), unsigned(Hk)), dim3(256), 0, s,
+    const int64_t items = (nchunks * Hk + 7) / 8 * 8;
+    hipLaunchKernelGGL(prefill_chunk_kernel, dim3(unsigned(items * (Hv / Hk))), dim3(256), 0, s,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), ga, gb,
                        gb_dtype, A_log, dt_bias, gate_mode, cu_seqlens, N, L_uniform, chunk_off,
                        records, Hk, Hv);

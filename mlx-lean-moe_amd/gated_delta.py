@@ -154,7 +154,7 @@ def _prefill_eligible(q, k, v, tokens_per_run: float) -> bool:
     bytes, v 8 bytes: a contiguous view may start anywhere in its storage)."""
 
     return (q.dtype == k.dtype == v.dtype == torch.bfloat16 and q.shape[-1] == 128
-            and v.shape[-1] == 128 and q.shape[-2] * 8 >= v.shape[-2]
+            and v.shape[-1] == 128
             and tokens_per_run >= PREFILL_MIN_TOKENS
             and q.data_ptr() % 16 == 0 and k.data_ptr() % 16 == 0 and v.data_ptr() % 8 == 0)
 

@@ -91,6 +91,16 @@ def test_prefill_matches_sequential_oracle(gpu, T):
     assert max_rel(s.cpu().numpy(), se) < STATE_REL
 
 
+def test_prefill_wide_gqa_group(gpu):
+    # 12 value heads on one key head (more than the production 2:1 grouping)
+    arrays = _cfg_inputs(6, 130, Hk=1, Hv=12, state_scale=0.05)
+    t = _dev(gpu, arrays)
+    y, s = _prefill(t)
+    ye, se = _oracle(arrays)
+    assert np.abs(y.cpu().numpy() - ye).max() < Y_ATOL
+    assert max_rel(s.cpu().numpy(), se) < STATE_REL
+
+
 def test_prefill_matches_gpu_sequential_scan_slow_decay(gpu):
     # the reference scan test's decay regime (g in [0.98, 1], beta in [0, 1]):
     # long memory, the hardest case for the chunked state update
