@@ -661,7 +661,7 @@ GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassL
     }
 }
 
-// Chunk c: [S] B1 [R | Q S^T, Q and K(c+1)] B2 [D | V(c+1), fetch c+2] B3
+// Chunk c: [S] B1 [R | Q S^T] B2 [D | Q, K, V(c+1), fetch c+2] B3
 // [update | Tb(c+1), y]. Both loops are straight-line code (wave-uniform
 // roles), so the compiler's waits for loaded operands are exact and never
 // cover a later prefetch; both steps of the unrolled body are unconditional
@@ -700,10 +700,10 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
                     const StagedOperands& gn, StagedOperands& gf) {
         __syncthreads();
         const f32x4 yacc = output_project(sm, w, l);
-        stage_q(gn, sm, w, l);
-        stage_k(gn, sm, buf ^ 1, w, l);
         fetch_output<kUpper>(on, cx, c + 1 < last ? c + 1 : last, w, l);
         __syncthreads();
+        stage_q(gn, sm, w, l);
+        stage_k(gn, sm, buf ^ 1, w, l);
         stage_v(gn, sm, w, l);
         fetch_staged<kUpper>(gf, cx, c + 2 < last ? c + 2 : last, w, l);
         __syncthreads();
