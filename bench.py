@@ -10,9 +10,10 @@ Infinity Cache and the bandwidth figure is HBM's, not the cache's.
 
 Also measured in the same run (reported under "also"):
   decode_large: B=256, Hv=64, fused conv roll + gated RMSNorm (1 GiB state)
-  prefill:      B=1, T=4096 chunked prefill (bf16 MFMA), when built
+  prefill:      B=1, T=4096 chunked prefill (bf16 MFMA)
+  prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
 
-python bench.py [--steps K] [--warmup W] [--workload decode|decode_large|prefill|copy]
+python bench.py [--steps K] [--warmup W] [--workload decode|decode_large|prefill|prefill_varlen|copy]
 """
 
 from __future__ import annotations
@@ -156,14 +157,23 @@ def prefill_flops(T, Hv, d=128, chunk=64):
 
 
 class PrefillWorkload:
-    """Synthetic chunked-prefill inputs resident in HBM: N runs of L tokens,
-    bf16 q/k/v (q, k L2-normalised), bf16 a/b, zero initial state; y in bf16."""
+    """Synthetic chunked-prefill inputs resident in HBM: N runs of L tokens
+    (or packed runs of the given lengths, through cu_seqlens), bf16 q/k/v
+    (q, k L2-normalised), bf16 a/b, initial state zero (or ~N(0, 0.05) with
+    packed runs); y in bf16."""
 
-    def __init__(self, dev, N, L, Hk, Hv, seed=0):
+    def __init__(self, dev, N, L, Hk, Hv, seed=0, lens=None):
         d = 128
         g = torch.Generator(device=dev).manual_seed(seed)
         bf = torch.bfloat16
-        T = N * L
+        if lens is not None:
+            N = len(lens)
+            cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+            self.cu = torch.tensor(cu, device=dev)
+            T = int(cu[-1])
+        else:
+            self.cu = None
+            T = N * L
         randn = lambda *s: torch.randn(*s, generator=g, device=dev)
         q = randn(T, Hk, d)
         k = randn(T, Hk, d)
@@ -175,6 +185,7 @@ class PrefillWorkload:
         self.A_log = torch.rand(Hv, generator=g, device=dev) * float(np.log(16))
         self.dt_bias = torch.rand(Hv, generator=g, device=dev) * 2 - 1
         self.state_out = torch.empty(N, Hv, d, d, device=dev)
+        self.state_in = (randn(N, Hv, d, d) * 0.05 if lens is not None else None)
         self.y = torch.empty(T, Hv, d, dtype=bf, device=dev)
         nbytes = gated_delta.prefill_workspace_bytes(N, T, Hk, Hv, d, d)
         self.ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -184,8 +195,10 @@ class PrefillWorkload:
         self._fn = _lib.load().gdn_prefill_chunked
         self._args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.a.data_ptr(),
                       self.b.data_ptr(), _lib.GDN_BF16, self.A_log.data_ptr(),
-                      self.dt_bias.data_ptr(), 0, None, self.state_out.data_ptr(),
-                      self.y.data_ptr(), _lib.GDN_BF16, None, N, T, Hk, Hv, d, d,
+                      self.dt_bias.data_ptr(), 0,
+                      None if self.state_in is None else self.state_in.data_ptr(),
+                      self.state_out.data_ptr(), self.y.data_ptr(), _lib.GDN_BF16,
+                      None if self.cu is None else self.cu.data_ptr(), N, T, Hk, Hv, d, d,
                       self.ws.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)
 
     def step(self, s):
@@ -194,8 +207,11 @@ class PrefillWorkload:
             raise RuntimeError(f"gdn_prefill_chunked failed with {rc}")
 
 
-def bench_prefill(dev, N, L, Hk, Hv, steps, warmup):
-    w = PrefillWorkload(dev, N, L, Hk, Hv)
+VARLEN_LENS = np.random.default_rng(0).integers(128, 8193, 16)  # 16 runs, 67,128 tokens
+
+
+def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None):
+    w = PrefillWorkload(dev, N, L, Hk, Hv, lens=lens)
     total_ms, launch_ms = time_steps(w.step, steps, warmup)
     tflops = w.flops / (launch_ms * 1e-3) / 1e12
     return {
@@ -294,7 +310,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "prefill", "copy"])
+                    choices=["decode", "decode_large", "prefill", "prefill_varlen", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary workloads")
     args = ap.parse_args(argv)
@@ -361,6 +377,7 @@ def main(argv=None):
         if not args.no_also and not big:
             lg = bench_decode(dev, 256, 16, 64, True, steps=64, warmup=8)
             pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
+            pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
             line["also"] = {
                 "decode_large": {
                     "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
@@ -370,24 +387,34 @@ def main(argv=None):
                     "workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64, bf16 MFMA",
                     "tokens_per_s": pf["tokens_per_s"], "call_us": pf["call_us"],
                     "tflops": pf["tflops"], "mfma_frac": pf["mfma_frac"],
-                    "flops_per_call": pf["flops_per_call"]}}
+                    "flops_per_call": pf["flops_per_call"]},
+                "prefill_varlen": {
+                    "workload": "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 "
+                                "Hv=32, nonzero initial states",
+                    "tokens_per_s": pv["tokens_per_s"], "call_us": pv["call_us"],
+                    "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"]}}
         print(json.dumps(line))
         return 0
 
-    if args.workload == "prefill":
-        r = bench_prefill(dev, 1, 4096, 16, 32, args.steps, args.warmup)
+    if args.workload in ("prefill", "prefill_varlen"):
+        varlen = args.workload == "prefill_varlen"
+        r = bench_prefill(dev, 1, 4096, 16, 32, args.steps, args.warmup,
+                          lens=VARLEN_LENS if varlen else None)
         print(json.dumps({"metric": METRIC, "value": r["tokens_per_s"], "unit": "tokens/s",
                           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": r["ms_per_step"], "higher_is_better": True,
                           "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                           "data": "synthetic",
-                          "config": {"workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64"},
+                          "config": {"workload": (
+                              "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 Hv=32 "
+                              "d=128 chunk 64" if varlen else
+                              "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64")},
                           "roofline": {"bound": "mfma", "achieved": r["tflops"],
                                        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                        "frac": r["mfma_frac"], "traffic": None,
                                        "kernel": "gdn_prefill_chunked (3 launches)",
                                        "call_us": r["call_us"]},
-                          **({} if args.no_cpu_baseline else
+                          **({} if args.no_cpu_baseline or varlen else
                              {"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)})}))
         return 0
 

@@ -84,18 +84,34 @@ GDN_DEV bf16x8 zero8() {
 // run / chunk bookkeeping
 // ---------------------------------------------------------------------------
 
-// chunk_off[i] = index of run i's first chunk; chunk_off[N] = chunk count.
-__global__ void chunk_offsets_kernel(const int32_t* __restrict__ cu, int N, int64_t L_uniform,
+// Packed runs: chunk_off[i] = index of run i's first chunk; chunk_off[N] =
+// chunk count.
+__global__ void chunk_offsets_kernel(const int32_t* __restrict__ cu, int N,
                                      int32_t* __restrict__ chunk_off) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     int32_t off = 0;
     for (int i = 0; i < N; ++i) {
         chunk_off[i] = off;
-        const int64_t len = cu ? int64_t(cu[i + 1]) - cu[i] : L_uniform;
-        off += int32_t((len + kChunk - 1) / kChunk);
+        off += int32_t((int64_t(cu[i + 1]) - cu[i] + kChunk - 1) / kChunk);
     }
     chunk_off[N] = off;
 }
+
+// Where the runs and their chunks lie: packed runs (cu) with the chunk
+// offsets chunk_offsets_kernel wrote, or N runs of L_uniform tokens, cpr
+// chunks each (no offsets needed, and no launch for them).
+struct RunLayout {
+    const int32_t* cu;
+    const int32_t* chunk_off;  // null for uniform runs
+    int64_t L_uniform;
+    int N, cpr;
+
+    GDN_DEV int total() const { return chunk_off ? chunk_off[N] : N * cpr; }
+    GDN_DEV int first(int run) const { return chunk_off ? chunk_off[run] : run * cpr; }
+    GDN_DEV int run_of(int g) const { return chunk_off ? find_run(chunk_off, N, g) : g / cpr; }
+    GDN_DEV int64_t start(int run) const { return cu ? cu[run] : run * L_uniform; }
+    GDN_DEV int64_t end(int run) const { return cu ? cu[run + 1] : (run + 1) * L_uniform; }
+};
 
 struct ChunkPos {
     int run;
@@ -103,15 +119,11 @@ struct ChunkPos {
     int len;     // tokens in the chunk (1..64)
 };
 
-GDN_DEV ChunkPos locate_chunk(const int32_t* chunk_off, const int32_t* cu, int N, int64_t L_uniform,
-                              int g) {
-    const int run = find_run(chunk_off, N, g);
-    const int c = g - chunk_off[run];
-    const int64_t rs = cu ? cu[run] : run * L_uniform;
-    const int64_t re = cu ? cu[run + 1] : rs + L_uniform;
-    const int64_t t0 = rs + int64_t(c) * kChunk;
-    const int64_t len = re - t0 < kChunk ? re - t0 : kChunk;
-    return {run, t0, int(len)};
+GDN_DEV ChunkPos locate_chunk(const RunLayout& rl, int g) {
+    const int run = rl.run_of(g);
+    const int64_t t0 = rl.start(run) + int64_t(g - rl.first(run)) * kChunk;
+    const int64_t rest = rl.end(run) - t0;
+    return {run, t0, int(rest < kChunk ? rest : kChunk)};
 }
 
 // ---------------------------------------------------------------------------
@@ -224,9 +236,8 @@ GDN_DEV void offdiag_inverse(float* As, float* Ts, int w, int l) {
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_chunk_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const void* __restrict__ ga,
     const void* __restrict__ gb, int gb_dtype, const float* __restrict__ A_log,
-    const float* __restrict__ dt_bias, int gate_mode, const int32_t* __restrict__ cu, int N,
-    int64_t L_uniform, const int32_t* __restrict__ chunk_off, char* __restrict__ records, int Hk,
-    int Hv) {
+    const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
+    int Hk, int Hv) {
     // K/Q tiles first; once K K^T and K Q^T are in registers the same bytes
     // hold the A and T matrices.
     __shared__ __attribute__((aligned(16))) char smem[2 * kChunk * kKS * 2];
@@ -240,8 +251,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     const int id = blockIdx.x, e = (id >> 3) % r;
     const int item = (id / (8 * r)) * 8 + (id & 7);  // (chunk, key head)
     const int g = item / Hk, hk = item % Hk, hv = hk * r + e;
-    if (g >= chunk_off[N]) return;
-    const ChunkPos pos = locate_chunk(chunk_off, cu, N, L_uniform, g);
+    if (g >= rl.total()) return;
+    const ChunkPos pos = locate_chunk(rl, g);
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
     char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
 
@@ -730,14 +741,14 @@ template <class Y>
 __global__ __launch_bounds__(kStateThreads) void prefill_state_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const float* __restrict__ state_in, float* __restrict__ state_out,
-    typename Y::storage* __restrict__ y, const int32_t* __restrict__ cu, int N, int64_t L_uniform,
-    const int32_t* __restrict__ chunk_off, const char* __restrict__ records, int Hk, int Hv) {
+    typename Y::storage* __restrict__ y, RunLayout rl, const char* __restrict__ records, int Hk,
+    int Hv) {
     __shared__ __attribute__((aligned(16))) StatePassLds sm;
 
     // Work mapping: the 8 slices of one (run, head) share its K/Q and chunk
     // records, so they are placed on one XCD (workgroups go round-robin over
     // the 8 XCDs) when the head count allows it.
-    const int R = N * Hv;
+    const int R = rl.N * Hv;
     const int id = blockIdx.x;
     int hr, slice;
     if (R % 8 == 0) {
@@ -760,15 +771,15 @@ __global__ __launch_bounds__(kStateThreads) void prefill_state_kernel(
     cx.k = k;
     cx.v = v;
     cx.records = records;
-    cx.rs = cu ? cu[run] : run * L_uniform;
-    cx.re = cu ? cu[run + 1] : cx.rs + L_uniform;
+    cx.rs = rl.start(run);
+    cx.re = rl.end(run);
     cx.qk_stride = int64_t(Hk) * kHD;
-    cx.c0 = chunk_off[run];
+    cx.c0 = rl.first(run);
     cx.h = h;
     cx.hk = h / (Hv / Hk);
     cx.Hv = Hv;
     cx.dv0 = slice * kSliceRows;
-    const int nch = chunk_off[run + 1] - cx.c0;
+    const int nch = rl.first(run + 1) - cx.c0;
 
     if (state_wave) {
         // S^T in accumulators: acc[t][i] = S^T[dk = 32w + 16t + 4(l/16) + i][dv = dv0 + l%16].
@@ -840,25 +851,31 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     GDN_REQUIRE(state_in != state_out, "gdn_prefill_chunked: state_out must not alias state_in");
 
     hipStream_t s = as_stream(stream);
-    const int64_t L_uniform = cu_seqlens ? 0 : T_total / N;
-    int32_t* chunk_off = static_cast<int32_t*>(workspace);
+    RunLayout rl;
+    rl.cu = cu_seqlens;
+    rl.N = N;
+    rl.L_uniform = cu_seqlens ? 0 : T_total / N;
+    rl.cpr = int((rl.L_uniform + kChunk - 1) / kChunk);
+    rl.chunk_off = nullptr;
     char* records = static_cast<char*>(workspace) + records_offset(N);
-    hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(64), 0, s, cu_seqlens, N, L_uniform, chunk_off);
-    if (int rc = check_launch("gdn_prefill_chunked/offsets")) return rc;
+    if (cu_seqlens) {  // packed runs: chunk offsets from the run lengths
+        int32_t* chunk_off = static_cast<int32_t*>(workspace);
+        hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(64), 0, s, cu_seqlens, N, chunk_off);
+        if (int rc = check_launch("gdn_prefill_chunked/offsets")) return rc;
+        rl.chunk_off = chunk_off;
+    }
     const int64_t nchunks = chunks_bound(T_total, N);
     const int64_t items = (nchunks * Hk + 7) / 8 * 8;
     hipLaunchKernelGGL(prefill_chunk_kernel, dim3(unsigned(items * (Hv / Hk))), dim3(256), 0, s,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), ga, gb,
-                       gb_dtype, A_log, dt_bias, gate_mode, cu_seqlens, N, L_uniform, chunk_off,
-                       records, Hk, Hv);
+                       gb_dtype, A_log, dt_bias, gate_mode, rl, records, Hk, Hv);
     if (int rc = check_launch("gdn_prefill_chunked/chunk")) return rc;
     const dim3 sgrid(unsigned(int64_t(N) * Hv * kSlices));
 #define GDN_STATE_LAUNCH(YT)                                                                      \
     hipLaunchKernelGGL(prefill_state_kernel<YT>, sgrid, dim3(kStateThreads), 0, s,                          \
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),           \
                        static_cast<const uint16_t*>(v), state_in, state_out,                       \
-                       static_cast<YT::storage*>(y), cu_seqlens, N, L_uniform, chunk_off, records, \
-                       Hk, Hv)
+                       static_cast<YT::storage*>(y), rl, records, Hk, Hv)
     if (y_dtype == GDN_F32) GDN_STATE_LAUNCH(ActF32);
     else if (y_dtype == GDN_BF16) GDN_STATE_LAUNCH(ActBF16);
     else GDN_STATE_LAUNCH(ActF16);
