@@ -108,8 +108,10 @@ class DecodeWorkload:
 
 
 def time_steps(step, steps, warmup):
-    """Total time of `steps` back-to-back steps (events on the launch stream)
-    and the mean duration of one launch (event pair around each launch)."""
+    """Total time of `steps` back-to-back steps (one event pair on the launch
+    stream around the timed region) and, as a cross-check, the mean time of
+    one step timed alone (an event pair around each step, which adds the
+    events' own overhead of ~2 us per step)."""
 
     stream = torch.cuda.current_stream()
     for s in range(warmup):
@@ -135,13 +137,14 @@ def time_steps(step, steps, warmup):
 
 def bench_decode(dev, B, Hk, Hv, with_z, steps, warmup):
     w = DecodeWorkload(dev, B, Hk, Hv, with_z)
-    total_ms, launch_ms = time_steps(w.step, steps, warmup)
-    ms = total_ms / steps
-    achieved = w.bytes_per_step / (launch_ms * 1e-3) / 1e9
+    total_ms, isolated_ms = time_steps(w.step, steps, warmup)
+    ms = total_ms / steps  # one launch per step
+    achieved = w.bytes_per_step / (ms * 1e-3) / 1e9
     return {
         "tokens_per_s": B * steps / (total_ms * 1e-3),
         "ms_per_step": ms,
-        "kernel_us": launch_ms * 1e3,
+        "kernel_us": ms * 1e3,
+        "isolated_launch_us": isolated_ms * 1e3,
         "bytes_per_step": w.bytes_per_step,
         "hbm_gbs": achieved,
         "hbm_frac": achieved / HBM_PEAK_GBS,
@@ -212,12 +215,14 @@ VARLEN_LENS = np.random.default_rng(0).integers(128, 8193, 16)  # 16 runs, 67,12
 
 def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None):
     w = PrefillWorkload(dev, N, L, Hk, Hv, lens=lens)
-    total_ms, launch_ms = time_steps(w.step, steps, warmup)
-    tflops = w.flops / (launch_ms * 1e-3) / 1e12
+    total_ms, isolated_ms = time_steps(w.step, steps, warmup)
+    call_ms = total_ms / steps  # one gdn_prefill_chunked call per step
+    tflops = w.flops / (call_ms * 1e-3) / 1e12
     return {
         "tokens_per_s": w.T * steps / (total_ms * 1e-3),
-        "ms_per_step": total_ms / steps,
-        "call_us": launch_ms * 1e3,
+        "ms_per_step": call_ms,
+        "call_us": call_ms * 1e3,
+        "isolated_call_us": isolated_ms * 1e3,
         "flops_per_call": w.flops,
         "tflops": tflops,
         "mfma_frac": tflops / BF16_PEAK_TFLOPS,
@@ -328,12 +333,13 @@ def main(argv=None):
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev).normal_()
         dst = torch.empty_like(src)
         n = max(args.steps, 1)
-        total_ms, launch_ms = time_steps(lambda s: dst.copy_(src), n, max(args.warmup, 1))
+        total_ms, _ = time_steps(lambda s: dst.copy_(src), n, max(args.warmup, 1))
+        copy_ms = total_ms / n
         nbytes = 2 * src.numel() * 4
         print(json.dumps({"workload": "copy 1 GiB float32 (torch copy_)", "bytes_read": nbytes // 2,
                           "bytes_written": nbytes // 2, "launches": n,
-                          "copy_us": launch_ms * 1e3,
-                          "gbs": nbytes / (launch_ms * 1e-3) / 1e9}))
+                          "copy_us": copy_ms * 1e3,
+                          "gbs": nbytes / (copy_ms * 1e-3) / 1e9}))
         return 0
 
     if args.workload in ("decode", "decode_large"):
@@ -369,6 +375,7 @@ def main(argv=None):
                 "traffic": load_traffic(f"{kernel}_{'b256_hv64' if big else 'b64_hv32'}_traffic.json"),
                 "kernel": kernel,
                 "kernel_us": r["kernel_us"],
+                "isolated_launch_us": r["isolated_launch_us"],
                 "algorithmic_bytes_per_launch": r["bytes_per_step"],
             },
         }

@@ -101,6 +101,43 @@ def test_prefill_wide_gqa_group(gpu):
     assert max_rel(s.cpu().numpy(), se) < STATE_REL
 
 
+def test_prefill_exact_zero_and_unit_gates(gpu):
+    """Gates of exactly 0 (a state reset: log-gate clamped at -80) and exactly
+    1 (no decay) mid-sequence, through gated_delta_scan's chunked path (fp32
+    g and beta, bf16 q/k/v), against the float64 recurrence."""
+
+    T, Hk, Hv, D = 200, 2, 4, 128
+    q, k, v, g, beta, s0 = R.metal_test_inputs(T, key_dim=D, value_dim=D, key_heads=Hk,
+                                               value_heads=Hv)
+    q, k, v = (R.bf16_round(x) for x in (q, k, v))
+    g = g.copy()
+    g[70, 1] = 0.0
+    g[130:140, :] = 0.0
+    g[10:40, 2] = 1.0
+    g[150:, 3] = 1.0
+    dev = lambda x, dt=torch.float32: torch.tensor(x, device=gpu).to(dt)
+    y, s = gdn.gated_delta_scan(dev(q, torch.bfloat16), dev(k, torch.bfloat16),
+                                dev(v, torch.bfloat16), dev(g), dev(beta), dev(s0))
+    ye, se = R.gated_delta_scan(q, k, v, g, beta, s0)
+    assert np.abs(y.cpu().numpy() - ye).max() < Y_ATOL
+    assert max_rel(y.cpu().numpy(), ye) < 1e-3
+    assert max_rel(s.cpu().numpy(), se) < STATE_REL
+
+
+def test_prefill_many_short_runs(gpu):
+    # 64 packed runs of 1..100 tokens: chunk bookkeeping across many runs
+    lens = np.random.default_rng(11).integers(1, 101, 64)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    arrays = _cfg_inputs(12, T, Hk=2, Hv=4, state_scale=0.05, N=len(lens))
+    t = _dev(gpu, arrays)
+    y, s = _prefill(t, cu=cu)
+    ye, se = _oracle(arrays, cu=cu)
+    assert np.abs(y.cpu().numpy() - ye).max() < Y_ATOL
+    for i in range(len(lens)):
+        assert max_rel(s[i].cpu().numpy(), se[i]) < STATE_REL, i
+
+
 def test_prefill_matches_gpu_sequential_scan_slow_decay(gpu):
     # the reference scan test's decay regime (g in [0.98, 1], beta in [0, 1]):
     # long memory, the hardest case for the chunked state update
