@@ -13,7 +13,7 @@ Also measured in the same run (reported under "also"):
   prefill:      B=1, T=4096 chunked prefill (bf16 MFMA)
   prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
 
-python bench.py [--steps K] [--warmup W] [--workload decode|decode_large|prefill|prefill_varlen|copy]
+python bench.py [--steps K] [--warmup W] [--workload decode|decode_large|prefill|prefill_varlen|qlinear|copy]
 """
 
 from __future__ import annotations
@@ -210,6 +210,48 @@ class PrefillWorkload:
             raise RuntimeError(f"gdn_prefill_chunked failed with {rc}")
 
 
+class QLinearWorkload:
+    """The layer's stacked input projection (qkv | z | a | b: 2048 -> 12352)
+    as a 4-bit affine (group 64, bf16 scales/biases) quantized matmul of M
+    bf16 rows; random codes, scales ~U(0.001, 0.01), biases ~U(-0.05, 0.05)."""
+
+    def __init__(self, dev, M, N=12352, K=2048, bits=4, group_size=64, seed=0):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        self.w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K * bits // 32), generator=g,
+                               device=dev, dtype=torch.int32)
+        self.scales = (torch.rand(N, K // group_size, generator=g, device=dev) * 0.009
+                       + 0.001).to(torch.bfloat16)
+        self.biases = ((torch.rand(N, K // group_size, generator=g, device=dev) - 0.5)
+                       * 0.1).to(torch.bfloat16)
+        self.y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        self.M, self.N, self.K = M, N, K
+        self.flops = 2 * M * N * K
+        self.bytes = (N * K * bits // 8 + 2 * N * (K // group_size) * 2 + M * K * 2 + M * N * 2)
+        from mlx_lean_moe_amd import _lib
+
+        self._fn = _lib.load().gdn_quantized_matmul
+        self._args = (self.x.data_ptr(), _lib.GDN_BF16, self.w.data_ptr(),
+                      self.scales.data_ptr(), self.biases.data_ptr(), _lib.GDN_BF16,
+                      self.y.data_ptr(), _lib.GDN_BF16, M, N, K, bits, group_size,
+                      torch.cuda.current_stream().cuda_stream)
+
+    def step(self, s):
+        rc = self._fn(*self._args)
+        if rc != 0:
+            raise RuntimeError(f"gdn_quantized_matmul failed with {rc}")
+
+
+def bench_qlinear(dev, M, steps, warmup):
+    w = QLinearWorkload(dev, M)
+    total_ms, isolated_ms = time_steps(w.step, steps, warmup)
+    ms = total_ms / steps
+    return {"kernel_us": ms * 1e3, "isolated_launch_us": isolated_ms * 1e3,
+            "hbm_gbs": w.bytes / (ms * 1e-3) / 1e9, "tflops": w.flops / (ms * 1e-3) / 1e12,
+            "bytes_per_launch": w.bytes, "flops_per_launch": w.flops,
+            "tokens_per_s": M / (ms * 1e-3)}
+
+
 VARLEN_LENS = np.random.default_rng(0).integers(128, 8193, 16)  # 16 runs, 67,128 tokens
 
 
@@ -315,7 +357,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "prefill", "prefill_varlen", "copy"])
+                    choices=["decode", "decode_large", "prefill", "prefill_varlen", "qlinear",
+                             "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary workloads")
     args = ap.parse_args(argv)
@@ -401,6 +444,27 @@ def main(argv=None):
                     "tokens_per_s": pv["tokens_per_s"], "call_us": pv["call_us"],
                     "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"]}}
         print(json.dumps(line))
+        return 0
+
+    if args.workload == "qlinear":
+        dec = bench_qlinear(dev, 64, args.steps, args.warmup)
+        pre = bench_qlinear(dev, 4096, max(args.steps // 4, 5), args.warmup)
+        print(json.dumps({
+            "metric": "4-bit affine quantized input projection (hidden 2048 -> qkv|z|a|b 12352)",
+            "value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": dec["kernel_us"] * 1e-3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic",
+            "config": {"workload": "gdn_quantized_matmul M=64 (decode) N=12352 K=2048, "
+                                   "4-bit group 64, bf16 scales/biases"},
+            "roofline": {"bound": "hbm", "achieved": dec["hbm_gbs"], "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": dec["hbm_gbs"] / HBM_PEAK_GBS, "traffic": None,
+                         "kernel": "gdn_quantized_matmul", "kernel_us": dec["kernel_us"],
+                         "algorithmic_bytes_per_launch": dec["bytes_per_launch"]},
+            "also": {"prefill_m4096": {
+                "kernel_us": pre["kernel_us"], "tflops": pre["tflops"],
+                "mfma_frac": pre["tflops"] / BF16_PEAK_TFLOPS,
+                "flops_per_launch": pre["flops_per_launch"]}}}))
         return 0
 
     if args.workload in ("prefill", "prefill_varlen"):

@@ -44,7 +44,8 @@ typedef enum {
 #define GDN_EINVAL (-1)
 #define GDN_EUNSUPPORTED (-2)
 
-/* Library ABI version (bumped on any signature change). */
+/* Library ABI version (bumped on any signature change or addition; 2 adds the
+ * quantized matmul and dequantize entry points). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -171,6 +172,35 @@ int gdn_prefill_chunked(const void *q, const void *k, const void *v, const void 
  */
 int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, const float *w,
                       float eps, void *out, int out_dtype, int64_t rows, int D, void *stream);
+
+/*
+ * gdn_quantized_matmul - y = x W^T for an affine-quantized W in MLX's packing,
+ * on bf16 MFMA with float32 accumulation.
+ *   x: (M, K) bfloat16 (other dtypes: GDN_EUNSUPPORTED, see gdn_dequantize)
+ *   w: (N, K * bits / 32) uint32, element k of row n at bits [bits * (k % (32 / bits)), +bits)
+ *      of word k / (32 / bits), least significant first; 16-byte aligned
+ *   scales, biases: (N, K / group_size) sb_dtype; w[n][k] = scales[n][g] * q + biases[n][g]
+ *   y: (M, N) y_dtype
+ *   bits 4 or 8 (others: GDN_EUNSUPPORTED); group_size 32, 64 or 128; K a
+ *   multiple of 64 and of group_size
+ * The weights enter the MFMAs as bf16(scale * q + bias) (the product is exact
+ * in float32; one rounding), i.e. x times the weights mx.dequantize yields.
+ * Replaces mx.quantized_matmul(..., mode="affine") in quantized_linear
+ * (model/moe_block.py:44-55), used for the layer's projections
+ * (model/qwen3_5/linear_attention.py:96-101,125).
+ */
+int gdn_quantized_matmul(const void *x, int x_dtype, const void *w, const void *scales,
+                         const void *biases, int sb_dtype, void *y, int y_dtype, int M, int N,
+                         int K, int bits, int group_size, void *stream);
+
+/*
+ * gdn_dequantize - the dense weights of gdn_quantized_matmul's layout:
+ * out[n][k] = scales[n][g] * q + biases[n][g] (float32 product, one rounding
+ * to out_dtype). out: (N, K) out_dtype. Counterpart of mx.dequantize, which
+ * the reference's tests use to build dense weights (tests/test_qwen3_5_linear_attention.py:59-70).
+ */
+int gdn_dequantize(const void *w, const void *scales, const void *biases, int sb_dtype, void *out,
+                   int out_dtype, int N, int K, int bits, int group_size, void *stream);
 
 #ifdef __cplusplus
 }

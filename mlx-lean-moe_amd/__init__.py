@@ -12,20 +12,25 @@ from .gated_delta import (beta_gate, forget_gate, gated_delta_scan, gated_delta_
                           gated_delta_update)
 from .linear_attention import (Qwen3_5LinearAttention, conv_frontend, fused_decode_step,
                                gated_rms_norm)
+from .quant import LinearWeights, QuantScheme, dequantize, quantized_linear
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
 
 __all__ = [
     "LinearAttentionDims",
+    "LinearWeights",
+    "QuantScheme",
     "QWEN3_5_LINEAR",
     "Qwen3_5LinearAttention",
     "RecurrentCache",
     "RecurrentStatePool",
     "beta_gate",
     "conv_frontend",
+    "dequantize",
     "forget_gate",
     "fused_decode_step",
     "gated_delta_scan",
     "gated_delta_step",
     "gated_delta_update",
     "gated_rms_norm",
+    "quantized_linear",
 ]

@@ -4,8 +4,12 @@ Mirrors ``Qwen3_5LinearAttention`` and ``_gated_rms_norm``
 (``src/mlx_lean_moe/model/qwen3_5/linear_attention.py:22-127``): four input
 projections, the causal depthwise conv with SiLU and conv-state roll, q/k
 scaling, the gates, the gated-delta recurrence, the gated RMSNorm and
-out_proj. Projections are dense ``x @ W.T`` products (moe_block.py:44-46) on
-the vendor BLAS; everything between them runs in this library's kernels:
+out_proj. Projections go through :func:`quant.quantized_linear`
+(moe_block.py:27-55): affine-quantized weights (the reference's
+``other_quant``, e.g. 4-bit groups of 64) on this library's quantized matmul
+kernel — the four input projections stacked into one launch when they share a
+scheme — and dense weights as ``x @ W.T`` on the vendor BLAS; everything
+between them runs in this library's kernels:
 
 * one decode token (1-D ``x``) with Dk = Dv = 128 and K = 4: the fused decode
   kernel (front-end, recurrence and gated norm in one launch);
@@ -23,6 +27,7 @@ import torch
 from . import _lib
 from .config import LinearAttentionDims
 from .gated_delta import _c, _require_device, _stream, gated_delta_update
+from .quant import LinearWeights, QuantScheme, concat_quantized, quantized_linear
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
 
 
@@ -144,14 +149,21 @@ class Qwen3_5LinearAttention:
 
     def __init__(self, dims: LinearAttentionDims, in_proj_qkv, in_proj_z, in_proj_a, in_proj_b,
                  conv1d_weight, A_log, dt_bias, norm_weight, out_proj,
-                 rms_norm_eps: float = 1e-6) -> None:
+                 rms_norm_eps: float = 1e-6, quant: QuantScheme | None = None) -> None:
+        """Projections are dense ``(N, K)`` tensors, quantized dicts
+        ``{"weight", "scales", "biases"}`` (scheme ``quant``, the reference's
+        ``config.other_quant``) or :class:`LinearWeights` carrying their own
+        scheme (linear_attention.py:95-101)."""
+
         self.linear = dims
         self.rms_norm_eps = rms_norm_eps
+        self.quant = quant
         self.in_proj_qkv = in_proj_qkv
         self.in_proj_z = in_proj_z
         self.in_proj_a = in_proj_a
         self.in_proj_b = in_proj_b
         self.out_proj = out_proj
+        self._in_stacked = self._stack_inputs()
         C, K = dims.conv_dim, dims.conv_kernel_dim
         self.conv1d_weight = conv1d_weight.float().reshape(C, K).contiguous()
         self.A_log = A_log.float().contiguous()
@@ -163,15 +175,42 @@ class Qwen3_5LinearAttention:
         return RecurrentCache(d.conv_kernel_dim, d.conv_dim, d.num_value_heads, d.value_head_dim,
                               d.key_head_dim, dtype=dtype, device=self.A_log.device)
 
-    @staticmethod
-    def _proj(rows: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        if weight.dtype != rows.dtype:
-            weight = weight.to(rows.dtype)
-        return rows @ weight.T
+    def _scheme_of(self, weights):
+        if isinstance(weights, LinearWeights):
+            return weights.tensors, weights.quant
+        if isinstance(weights, torch.Tensor):
+            return weights, None
+        return weights, self.quant
+
+    def _stack_inputs(self):
+        """One quantized projection for qkv|z|a|b when all four are quantized
+        with one scheme and one scales dtype (one launch instead of four)."""
+
+        parts = [self._scheme_of(w) for w in (self.in_proj_qkv, self.in_proj_z,
+                                             self.in_proj_a, self.in_proj_b)]
+        schemes = {q for _, q in parts}
+        if len(schemes) != 1 or None in schemes:
+            return None
+        tensors = [t for t, _ in parts]
+        if len({t["scales"].dtype for t in tensors}) != 1:
+            return None
+        return LinearWeights(concat_quantized(tensors), schemes.pop())
+
+    def _proj(self, rows: torch.Tensor, weights) -> torch.Tensor:
+        tensors, quant = self._scheme_of(weights)
+        if quant is None and tensors.dtype != rows.dtype:
+            tensors = tensors.to(rows.dtype)
+        return quantized_linear(rows, tensors, quant)
 
     def _project(self, rows: torch.Tensor):
         d = self.linear
         L = rows.shape[0]
+        if self._in_stacked is not None:
+            out = quantized_linear(rows, self._in_stacked)
+            qkv, z, a, b = torch.split(out, [d.conv_dim, d.value_dim, d.num_value_heads,
+                                             d.num_value_heads], dim=-1)
+            return (qkv.contiguous(), z.reshape(L, d.num_value_heads, d.value_head_dim),
+                    a.contiguous(), b.contiguous())
         qkv = self._proj(rows, self.in_proj_qkv)
         z = self._proj(rows, self.in_proj_z).reshape(L, d.num_value_heads, d.value_head_dim)
         a = self._proj(rows, self.in_proj_a)

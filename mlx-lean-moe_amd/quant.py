@@ -1,0 +1,141 @@
+"""Affine-quantized linear projections (MLX's packing) for the layer's input
+and output projections.
+
+Mirrors ``mlx_lean_moe.config.QuantScheme`` (``config.py:10-33``) and
+``mlx_lean_moe.model.moe_block.{LinearWeights, quantized_linear}``
+(``model/moe_block.py:13-55``): a projection is either a dense ``(N, K)``
+matrix or a dict ``{"weight", "scales", "biases"}`` with ``weight`` uint32
+``(N, K * bits / 32)`` (MLX's packing, least significant element first) and
+``scales``/``biases`` ``(N, K / group_size)``; ``w = scales * q + biases``.
+Quantized projections of bf16 activations run on ``gdn_quantized_matmul``;
+other activation dtypes dequantize on the GPU (``gdn_dequantize``) and
+multiply on the vendor BLAS. Dense projections are ``x @ W.T``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_SUPPORTED = {
+    "affine": ({2, 3, 4, 5, 6, 8}, {32, 64, 128}),
+    "mxfp4": ({4}, {32}),
+    "mxfp8": ({8}, {32}),
+    "nvfp4": ({4}, {16}),
+}
+# what the kernels implement (valid schemes outside it raise NotImplementedError)
+_KERNEL_BITS = {4, 8}
+
+
+@dataclass(frozen=True)
+class QuantScheme:
+    """One MLX quantization scheme, including its packing mode (the
+    reference's validation: config.py:17-33)."""
+
+    bits: int
+    group_size: int
+    mode: str = "affine"
+
+    def __post_init__(self) -> None:
+        if self.mode not in _SUPPORTED:
+            raise ValueError(f"unsupported quantization mode {self.mode!r}")
+        bits, groups = _SUPPORTED[self.mode]
+        if self.bits not in bits or self.group_size not in groups:
+            raise ValueError(f"unsupported {self.mode} quantization with bits={self.bits}, "
+                             f"group_size={self.group_size}")
+
+
+@dataclass(frozen=True)
+class LinearWeights:
+    """A loaded linear projection with its own storage scheme; ``quant`` is
+    ``None`` for an ordinary floating-point matrix (moe_block.py:13-20)."""
+
+    tensors: object
+    quant: QuantScheme | None
+
+
+def _kernel_scheme(quant: QuantScheme) -> None:
+    if quant.mode != "affine" or quant.bits not in _KERNEL_BITS:
+        raise NotImplementedError(
+            f"{quant.mode} {quant.bits}-bit weights: this build runs affine 4- and 8-bit")
+
+
+def _check_quantized(tensors: dict, quant: QuantScheme, K: int | None):
+    w, scales = tensors["weight"], tensors["scales"]
+    biases = tensors.get("biases")
+    if biases is None:
+        raise ValueError("affine quantized weights need biases")
+    if w.dtype not in (torch.int32, torch.uint32) or w.dim() != 2:
+        raise ValueError("quantized weight must be a 2-D 32-bit integer tensor")
+    N, words = w.shape
+    k = words * 32 // quant.bits
+    if K is not None and K != k:
+        raise ValueError(f"input width {K} does not match the weight's {k}")
+    if tuple(scales.shape) != (N, k // quant.group_size) or scales.shape != biases.shape:
+        raise ValueError(f"scales and biases must have shape {(N, k // quant.group_size)}")
+    if scales.dtype != biases.dtype:
+        raise ValueError("scales and biases must share a dtype")
+    return w, scales, biases, N, k
+
+
+def _c(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def dequantize(tensors: dict, quant: QuantScheme, dtype: torch.dtype | None = None):
+    """Dense ``(N, K)`` weights of a quantized projection, in ``dtype``
+    (default: the scales' dtype), computed on the GPU (mx.dequantize's
+    counterpart)."""
+
+    _kernel_scheme(quant)
+    w, scales, biases, N, K = _check_quantized(tensors, quant, None)
+    if w.device.type != "cuda":
+        raise RuntimeError(f"quantized weights must be on a ROCm device, got {w.device}")
+    out = torch.empty((N, K), dtype=dtype or scales.dtype, device=w.device)
+    w, scales, biases = _c(w), _c(scales), _c(biases)
+    _lib.call("gdn_dequantize", _lib.ptr(w), _lib.ptr(scales), _lib.ptr(biases),
+              _lib.dtype_code(scales.dtype), _lib.ptr(out), _lib.dtype_code(out.dtype), N, K,
+              quant.bits, quant.group_size, _lib.stream_ptr(w.device))
+    return out
+
+
+def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None) -> torch.Tensor:
+    """Linear projection for self-describing, legacy quantized, or dense
+    weights (moe_block.py:27-55): ``x @ W.T`` over the last axis of ``x``,
+    in ``x``'s dtype."""
+
+    if isinstance(tensors, LinearWeights):
+        quant = tensors.quant
+        tensors = tensors.tensors
+    if isinstance(tensors, torch.Tensor):
+        return x @ tensors.T
+    if quant is None:
+        raise ValueError("quantized linear weights require a quantization scheme")
+    _kernel_scheme(quant)
+    w, scales, biases, N, K = _check_quantized(tensors, quant, x.shape[-1])
+    if x.device.type != "cuda":
+        raise RuntimeError(f"quantized projections run on ROCm devices only; got {x.device}")
+    lead = x.shape[:-1]
+    if x.dtype != torch.bfloat16:
+        return x @ dequantize(tensors, quant, x.dtype).T
+    x2 = _c(x.reshape(-1, K))
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    w, scales, biases = _c(w), _c(scales), _c(biases)
+    _lib.call("gdn_quantized_matmul", _lib.ptr(x2), _lib.GDN_BF16, _lib.ptr(w), _lib.ptr(scales),
+              _lib.ptr(biases), _lib.dtype_code(scales.dtype), _lib.ptr(y),
+              _lib.dtype_code(y.dtype), M, N, K, quant.bits, quant.group_size,
+              _lib.stream_ptr(x.device))
+    return y.reshape(*lead, N)
+
+
+def concat_quantized(parts: list[dict]) -> dict:
+    """Stacks quantized projections that share an input (same K, scheme and
+    scales dtype) along N, so that one launch computes all of them."""
+
+    return {key: torch.cat([p[key] for p in parts], dim=0) for key in ("weight", "scales", "biases")}

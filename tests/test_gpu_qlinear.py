@@ -1,0 +1,129 @@
+"""GPU parity of the affine-quantized projections against the oracle's
+restatement of MLX's format: y = x @ dequantize(W).T (the reference test's
+dense comparison, tests/test_qwen3_5_linear_attention.py:59-86)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mlx_lean_moe_amd as gdn
+from mlx_lean_moe_amd import _lib
+from oracle import quant_ref as Q
+from oracle import gated_delta_ref as R
+from tests.helpers import assert_bf16_out_close, layer_inputs, layer_params
+
+pytestmark = pytest.mark.gpu
+
+_TORCH = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _weights(rng, N, K, bits, gs, sb):
+    words, s, b = Q.quantize(rng.standard_normal((N, K)) * 0.05, bits, gs, sb=sb)
+    return words, s, b
+
+
+def _dev_weights(gpu, words, s, b, sb):
+    return {"weight": torch.tensor(words.view(np.int32), device=gpu),
+            "scales": torch.tensor(s, dtype=torch.float32, device=gpu).to(_TORCH[sb]),
+            "biases": torch.tensor(b, dtype=torch.float32, device=gpu).to(_TORCH[sb])}
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,sb", [
+    (1, 40, 128, 4, 64, "bf16"),
+    (7, 96, 256, 4, 32, "f16"),
+    (64, 12352, 2048, 4, 64, "bf16"),   # the layer's stacked input projection at decode
+    (33, 2048, 4096, 4, 64, "bf16"),    # out_proj at decode (value_dim 4096 -> hidden)
+    (5, 70, 1024, 8, 32, "f16"),
+    (200, 130, 512, 8, 128, "f32"),
+    (300, 2048, 1024, 4, 64, "bf16"),   # large-M tiles, partial edge tiles
+    (2, 78, 256, 4, 64, "bf16"),        # decode kernel: 4 groups per column, last block partial
+    (3, 77, 256, 4, 64, "bf16"),        # scales span not whole 16-byte pieces: tiled kernel
+    (16, 200, 1024, 4, 32, "f32"),      # decode kernel with float32 scales
+    (64, 100, 4096, 8, 32, "f32"),      # scales exceed the decode kernel's LDS: tiled kernel
+    (9, 64, 4096, 8, 128, "bf16"),      # decode kernel, 16 K steps, 8-bit
+])
+def test_quantized_matmul_matches_oracle(gpu, M, N, K, bits, gs, sb):
+    rng = np.random.default_rng(M + N + K)
+    words, s, b = _weights(rng, N, K, bits, gs, sb)
+    x = R.bf16_round(rng.standard_normal((M, K)))
+    # bf16 activations: the weights enter the MFMAs dequantized to bf16
+    # whatever the scales' dtype (gdn_quantized_matmul's contract)
+    ref = Q.quantized_matmul(x, words, s, b, bits, gs, w_round="bf16")
+    scheme = gdn.QuantScheme(bits, gs)
+    W = _dev_weights(gpu, words, s, b, sb)
+    xt = torch.tensor(x, dtype=torch.float32, device=gpu).to(torch.bfloat16)
+    y = gdn.quantized_linear(xt, W, scheme)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (M, N)
+    assert_bf16_out_close(y.float().cpu().numpy(), ref)
+    # float32 output: the accumulation alone (no output rounding)
+    y32 = torch.empty(M, N, device=gpu)
+    _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.GDN_BF16, _lib.ptr(W["weight"]),
+              _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
+              _lib.ptr(y32), _lib.GDN_F32, M, N, K, bits, gs, _lib.stream_ptr(xt.device))
+    err = np.abs(y32.cpu().numpy() - ref).max()
+    assert err <= 1e-5 * np.abs(ref).max() + 1e-6, err
+
+
+@pytest.mark.parametrize("bits,gs,sb,out", [(4, 64, "bf16", "bf16"), (8, 32, "f16", "f32"),
+                                             (4, 128, "f32", "f32")])
+def test_dequantize_is_bit_exact(gpu, bits, gs, sb, out):
+    rng = np.random.default_rng(bits * gs)
+    words, s, b = _weights(rng, 33, 256, bits, gs, sb)
+    W = _dev_weights(gpu, words, s, b, sb)
+    dense = gdn.dequantize(W, gdn.QuantScheme(bits, gs), _TORCH[out])
+    np.testing.assert_array_equal(dense.float().cpu().numpy(),
+                                  Q.dequantize(words, s, b, bits, gs, out=out))
+
+
+def test_non_bf16_activations_use_dense_weights(gpu):
+    rng = np.random.default_rng(4)
+    words, s, b = _weights(rng, 48, 128, 4, 64, "bf16")
+    W = _dev_weights(gpu, words, s, b, "bf16")
+    x = rng.standard_normal((5, 128)).astype(np.float32)
+    y = gdn.quantized_linear(torch.tensor(x, device=gpu), W, gdn.QuantScheme(4, 64))
+    assert y.dtype == torch.float32
+    ref = x.astype(np.float64) @ Q.dequantize(words, s, b, 4, 64, out="f32").T
+    assert np.abs(y.cpu().numpy() - ref).max() < 1e-4
+
+
+def test_layer_with_quantized_projections_matches_dense_weights(gpu):
+    """The reference's layer test setup: quantized projections against the
+    same layer on the dequantized dense weights, decode and prefill."""
+
+    dims = gdn.LinearAttentionDims(2, 4, 128, 128, 4)
+    dt = (2, 4, 128, 128)
+    H = 256
+    rng = np.random.default_rng(21)
+    conv_w, A_log, dt_bias, norm_w = layer_params(rng, dt)
+    scheme = gdn.QuantScheme(4, 64)
+    shapes = {"qkv": dims.conv_dim, "z": dims.value_dim, "a": 4, "b": 4}
+    quant, dense = {}, {}
+    for name, n in shapes.items():
+        words, s, b = _weights(rng, n, H, 4, 64, "bf16")
+        quant[name] = _dev_weights(gpu, words, s, b, "bf16")
+        dense[name] = torch.tensor(Q.dequantize(words, s, b, 4, 64), dtype=torch.float32,
+                                   device=gpu).to(torch.bfloat16)
+    words, s, b = _weights(rng, H, dims.value_dim, 4, 64, "bf16")
+    quant["out"] = _dev_weights(gpu, words, s, b, "bf16")
+    dense["out"] = torch.tensor(Q.dequantize(words, s, b, 4, 64), dtype=torch.float32,
+                                device=gpu).to(torch.bfloat16)
+    f32 = lambda x: torch.tensor(np.asarray(x, np.float32), device=gpu)
+    common = (f32(conv_w)[:, :, None], f32(A_log), f32(dt_bias), f32(norm_w))
+
+    def make(w, q):
+        return gdn.Qwen3_5LinearAttention(dims, w["qkv"], w["z"], w["a"], w["b"], common[0],
+                                          common[1], common[2], common[3], w["out"], quant=q)
+
+    lq, ld = make(quant, scheme), make(dense, None)
+    assert lq._in_stacked is not None  # one launch for the four input projections
+    x = torch.tensor(R.bf16_round(rng.standard_normal((70, H))), dtype=torch.float32,
+                     device=gpu).to(torch.bfloat16)
+    cq, cd = lq.new_cache(torch.bfloat16), ld.new_cache(torch.bfloat16)
+    oq, od = lq(x, cq), ld(x, cd)
+    assert_bf16_out_close(oq.float().cpu().numpy(), od.float().cpu().numpy().astype(np.float64))
+    for t in range(3):
+        xt = x[t]
+        oq, od = lq(xt, cq), ld(xt, cd)
+        assert_bf16_out_close(oq.float().cpu().numpy(), od.float().cpu().numpy().astype(np.float64))
