@@ -162,145 +162,373 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
         }
 }
 
-// Small M (decode, M <= 64): weight-stationary. One 1024-thread workgroup
-// per 64 output columns over the whole K: each thread requests its share of
-// the packed weights for every K step (16 consecutive k of one column per
-// step) at the start, and the workgroup's scales and biases go to LDS with
-// 16-byte loads, so the HBM stream is issued at once; x then streams from L2
-// in steps of 256 k through double-buffered LDS, where each step's weights
-// are also dequantized. Wave w computes the 16 x 16 output tile (w / 4,
-// w % 4) of the 64 x 64 block. kSteps = K / 256; the 64 columns' K /
-// group_size scales (and as many biases) must fit kSmallSBBytes each.
-constexpr int kSmallBK = 256;
-constexpr int kSmallTS = kSmallBK + 8;
-constexpr int kSmallSBBytes = 14336;  // LDS bytes for scales (and again for biases)
+// Decode-sized M (<= 64): one 512-thread workgroup per kCols (32 or 64)
+// output columns over the whole K. The MFMAs take the integer codes, not dequantized
+// weights: a wave's k slice of a step (kSlice = 32 or 64 k) lies in one
+// quantization group g, so with P = sum_{k in slice} x[m][k] q[n][k] and
+// X = sum_{k in slice} x[m][k],
+//     y[m][n] = sum over slices of s[n][g] P + b[n][g] X,
+// accumulated in float (MLX's matrix-vector kernels apply scale and bias to
+// per-group float partial sums in the same way). 4-bit B fragments are the
+// bf16 values 1 + q / 16, written straight into bf16 bits two codes per
+// bit-and (exact; pairs codes i and i + 4 of a word, so the x tile is staged
+// with the matching order of each 8-element chunk), giving
+// P' = X + P / 16 and y += 16 s P' + (b - 16 s) X; 8-bit codes convert to
+// bf16 exactly (P' = P). X comes from one MFMA against ones.
+//
+// Every thread first requests its pieces of the workgroup's scales and
+// biases, the first step of x and its share of the packed weights for ALL
+// steps (16-byte runs of one column), so the HBM stream is in flight at
+// once. Each step stages x (16 kMT rows, clamped to M) and the step's
+// packed words in LDS; wave w takes k slice [kSlice w, kSlice (w + 1)) of
+// the step for the whole 16 kMT x kCols block. The 8 waves' float partial
+// blocks are summed in LDS in a fixed order at the end. Needs K a multiple
+// of 8 kSlice (kSteps steps), K / group_size <= kDecGroups and a multiple of
+// the 16-byte piece's entry count, and 16-byte aligned operands.
+constexpr int kDecGroups = 64;  // scale groups per column the LDS holds
 
-template <int kBits, int kSteps, class SB, class Y>
-__global__ __launch_bounds__(1024) void qlinear_small_m_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
-    const typename SB::storage* __restrict__ scales, const typename SB::storage* __restrict__ biases,
-    typename Y::storage* __restrict__ y, int M, int N, int K, int group_size) {
-    typedef uint32_t wword_t __attribute__((ext_vector_type(kBits / 2)));  // 16 codes
-    using sb_t = typename SB::storage;
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][64 * kSmallTS];
-    __shared__ __attribute__((aligned(16))) uint16_t ws[2][64 * kSmallTS];
-    __shared__ __attribute__((aligned(16))) sb_t sbs[2][kSmallSBBytes / sizeof(sb_t)];  // [column][group]
+// The two constants of the 4-bit code fragment, held in registers so that
+// each dword is a shift and one v_and_or_b32 (gfx9 VOP3 takes no literals).
+struct CodeConsts {
+    uint32_t mask, one;
+};
 
-    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, lr = l & 15, lq = l >> 4;
-    const int n0 = blockIdx.x * 64;
-    // weight share: column n0 + tid / 16, k = 256 s + 16 (tid % 16) .. +15
-    const int wc = tid >> 4, wk = 16 * (tid & 15);
-    const int64_t wrow = n0 + wc < N ? n0 + wc : N - 1;
-    const int64_t wpr = int64_t(K) / Packing<kBits>::per_word;
-    const int gpr = K / group_size;
+GDN_DEV CodeConsts code_consts() {
+    CodeConsts k;
+    asm volatile("s_mov_b32 %0, 0x780078" : "=s"(k.mask));
+    asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(k.one));
+    return k;
+}
 
-    // x share per step: row tid / 16 (clamped to M - 1), k 8 (tid % 16) + {0, 128} .. +7
-    const int xr = tid >> 4, xk = 8 * (tid & 15);
-    const int64_t xrow = xr < M ? xr : M - 1;
-    u16x8 xv[2][2];
-    auto fetch_x = [&](int s, u16x8 (&v)[2]) {
-        const uint16_t* src = x + xrow * K + kSmallBK * s + xk;
-        v[0] = *reinterpret_cast<const u16x8*>(src);
-        v[1] = *reinterpret_cast<const u16x8*>(src + 128);
-    };
-    auto stage_x = [&](int buf, const u16x8 (&v)[2]) {
-        *reinterpret_cast<u16x8*>(&xs[buf][xr * kSmallTS + xk]) = v[0];
-        *reinterpret_cast<u16x8*>(&xs[buf][xr * kSmallTS + xk + 128]) = v[1];
-    };
-
-    // Scales and biases of the 64 columns are one contiguous span of 64
-    // gpr entries each, loaded in 16-byte pieces, at most two per thread
-    // (2 kSmallSBBytes / 16 <= 2048). They are requested first so that
-    // waiting for them does not wait for the weight stream. Pieces past the
-    // end of the arrays (columns >= N, whose outputs are not stored) read
-    // the last piece instead; threads past the last piece repeat it.
-    constexpr int per_piece = 16 / int(sizeof(sb_t));
-    const int span_pieces = 64 * gpr / per_piece;
-    const int64_t base_piece = int64_t(n0) * gpr / per_piece, last_piece = int64_t(N) * gpr / per_piece - 1;
-    int pdst[2];
-    uint4 pv[2];
+template <int kBits>
+GDN_DEV bf16x8 code_fragment(const uint32_t* words, CodeConsts k) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 d;
+    if constexpr (kBits == 4) {
+        // dword i = (1 + q_i / 16, 1 + q_{i+4} / 16): code bits to bf16 mantissa bits 3..6
+        const uint32_t q = words[0];
+        d[0] = ((q << 3) & k.mask) | k.one;
+        d[1] = ((q >> 1) & k.mask) | k.one;
+        d[2] = ((q >> 5) & k.mask) | k.one;
+        d[3] = ((q >> 9) & k.mask) | k.one;
+        return __builtin_bit_cast(bf16x8, d);
+    } else {
+        bf16x8 b;
+        const uint32_t q0 = words[0], q1 = words[1];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        int p = tid + 1024 * i;
-        p = p < 2 * span_pieces ? p : 2 * span_pieces - 1;
-        const int which = p >= span_pieces, o = p - which * span_pieces;
-        const int64_t gp = base_piece + o < last_piece ? base_piece + o : last_piece;
-        pv[i] = *reinterpret_cast<const uint4*>((which ? biases : scales) + gp * per_piece);
-        pdst[i] = which * (kSmallSBBytes / 16) + o;
-    }
-    fetch_x(0, xv[0]);
-    if (kSteps > 1) fetch_x(1, xv[1]);
-    wword_t wq[kSteps];
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s)
-        wq[s] = *reinterpret_cast<const wword_t*>(w + wrow * wpr + (kSmallBK * s + wk) / Packing<kBits>::per_word);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) reinterpret_cast<uint4*>(&sbs[0][0])[pdst[i]] = pv[i];
-    __syncthreads();
-    auto stage_w = [&](int buf, int s) {
-        const int g = (kSmallBK * s + wk) / group_size;
-        const float sf = SB::load(&sbs[0][wc * gpr + g], 0), bf = SB::load(&sbs[1][wc * gpr + g], 0);
-        const uint32_t* words = reinterpret_cast<const uint32_t*>(&wq[s]);
-        u16x8 dq[2];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t q = (words[j / Packing<kBits>::per_word] >> (kBits * (j % Packing<kBits>::per_word))) &
-                               Packing<kBits>::mask;
-            dq[j / 8][j % 8] = f32_to_bf16_bits(__builtin_fmaf(sf, float(q), bf));
-        }
-        *reinterpret_cast<u16x8*>(&ws[buf][wc * kSmallTS + wk]) = dq[0];
-        *reinterpret_cast<u16x8*>(&ws[buf][wc * kSmallTS + wk + 8]) = dq[1];
-    };
-
-    const int tm = wv >> 2, tn = wv & 3;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    stage_x(0, xv[0]);
-    stage_w(0, 0);
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-        const int buf = s & 1;
-        if (s + 2 < kSteps) fetch_x(s + 2, xv[s & 1]);
-#pragma unroll
-        for (int kb = 0; kb < kSmallBK / 32; ++kb) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&xs[buf][(16 * tm + lr) * kSmallTS + 32 * kb + 8 * lq]);
-            const bf16x8 b = *reinterpret_cast<const bf16x8*>(&ws[buf][(16 * tn + lr) * kSmallTS + 32 * kb + 8 * lq]);
-            acc = mfma_bf16(a, b, acc);
-        }
-        if (s + 1 < kSteps) {
-            stage_x(buf ^ 1, xv[(s + 1) & 1]);
-            stage_w(buf ^ 1, s + 1);
-        }
-        __syncthreads();
-    }
-    const int n = n0 + 16 * tn + lr;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 16 * tm + 4 * lq + i;
-        if (m < M && n < N) Y::store(y, int64_t(m) * N + n, acc[i]);
+        for (int j = 0; j < 8; ++j) b[j] = static_cast<__bf16>(float(((j < 4 ? q0 : q1) >> (8 * (j & 3))) & 255u));
+        return b;
     }
 }
 
-template <int kBits, class SB, class Y>
-int launch_small_m(const void* x, const uint32_t* w, const void* scales, const void* biases, void* y,
-                   int M, int N, int K, int group_size, hipStream_t s) {
-    const dim3 grid(unsigned((N + 63) / 64));
-#define GDN_SMALL(STEPS)                                                                            \
-    hipLaunchKernelGGL((qlinear_small_m_kernel<kBits, STEPS, SB, Y>), grid, dim3(1024), 0, s,          \
-                       static_cast<const uint16_t*>(x), w,                                          \
-                       static_cast<const typename SB::storage*>(scales),                            \
-                       static_cast<const typename SB::storage*>(biases),                            \
-                       static_cast<typename Y::storage*>(y), M, N, K, group_size)
-    switch (K / kSmallBK) {
-        case 1: GDN_SMALL(1); break;
-        case 2: GDN_SMALL(2); break;
-        case 4: GDN_SMALL(4); break;
-        case 8: GDN_SMALL(8); break;
-        case 16: GDN_SMALL(16); break;
+template <int kBits, int kSteps, int kMT, int kSlice, int kCols>
+__global__ __launch_bounds__(512) void qlinear_decode_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w, const void* __restrict__ scales,
+    const void* __restrict__ biases, int sb_dtype, void* __restrict__ y, int y_dtype, int M, int N, int K,
+    int group_size) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int kStep = 8 * kSlice;            // k per step
+    constexpr int kKB = kSlice / 32;             // MFMA k blocks per wave per step
+    constexpr int kRows = 16 * kMT;
+    constexpr int kTN = kCols / 16;              // 16-column tiles
+    constexpr int kXS = kStep + 8;               // bf16 row stride of the x tile
+    constexpr int kWPC = kStep * kBits / 32;     // packed words of one column per step
+    constexpr int kWS = kWPC + 4;                // word row stride of the weight tile
+    constexpr int kXLoads = kRows * kStep / 8 / 512;   // 16-byte x chunks per thread per step
+    constexpr int kWLoads = kCols * kWPC / 4 / 512;    // 16-byte weight pieces per thread per step
+    constexpr int kXBytes = kRows * kXS * 2;
+    constexpr int kWBytes = kCols * kWS * 4;
+    constexpr int kPBytes = 4 * kMT * kTN * 64 * 16;  // 4 partial blocks of kMT x kTN tiles of float4 per lane
+    constexpr int kSBRow = kCols * (kDecGroups + 1);
+    constexpr int kSBBytes = 2 * kSBRow * 4;
+    // double-buffered tiles (one barrier per step) where the LDS holds them,
+    // for two workgroups per CU with 32 columns
+    constexpr int kBudget = kCols == 32 ? 80 * 1024 : 160 * 1024;
+    constexpr int kBufs = 2 * (kXBytes + kWBytes) + kSBBytes <= kBudget ? 2 : 1;
+    constexpr int kMain = kBufs * (kXBytes + kWBytes) > kPBytes ? kBufs * (kXBytes + kWBytes) : kPBytes;
+    static_assert(kXLoads >= 1 && kWLoads >= 1, "step too small for 512 threads");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kMain];
+    __shared__ float sbs[2 * kSBRow];
+    auto xs = [&](int buf) { return reinterpret_cast<uint16_t*>(lds + buf * kXBytes); };              // [kRows][kXS]
+    auto ws = [&](int buf) { return reinterpret_cast<uint32_t*>(lds + kBufs * kXBytes + buf * kWBytes); };  // [kCols][kWS]
+    f32x4* part = reinterpret_cast<f32x4*>(lds);  // [4][kMT][kTN][64] after the steps
+
+    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, lr = l & 15, lq = l >> 4;
+    const int n0 = blockIdx.x * kCols;
+    const int gpr = K / group_size;
+    const int64_t wpr = int64_t(K) * kBits / 32;
+
+    // Scales and biases of the kCols columns: one contiguous span of kCols gpr
+    // entries each, in 16-byte pieces (a piece holds groups of one column),
+    // at most 4 per thread. Pieces past the arrays' end (columns >= N, whose
+    // outputs are not stored) read the last piece; threads past the last
+    // piece repeat it.
+    const int esz = sb_dtype == GDN_F32 ? 4 : 2, per_piece = 16 / esz;
+    const int span_pieces = kCols * gpr / per_piece;
+    const int64_t base_piece = int64_t(n0) * gpr / per_piece, last_piece = int64_t(N) * gpr / per_piece - 1;
+    u32x4 pv[4];
+    int pdst[4];
+    const int sb_rounds = (2 * span_pieces + 511) / 512;  // pieces per thread, at most 4
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int p = tid + 512 * i;
+        p = p < 2 * span_pieces ? p : 2 * span_pieces - 1;
+        const int which = p >= span_pieces, o = p - which * span_pieces;
+        const int64_t gp = base_piece + o < last_piece ? base_piece + o : last_piece;
+        pv[i] = reinterpret_cast<const u32x4*>(which ? biases : scales)[gp];
+        const int e = o * per_piece, c = e / gpr;
+        pdst[i] = which * kSBRow + c * (gpr + 1) + (e - c * gpr);
+    }
+
+    // x chunk p = tid + 512 i of a step: row p / (kStep / 8) (clamped to
+    // M - 1), k 8 (p % (kStep / 8)) .. +7
+    u16x8 xv[kXLoads];
+    auto fetch_x = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+            const int p = tid + 512 * i, r = p / (kStep / 8), ch = p % (kStep / 8);
+            const int row = r < M ? r : M - 1;
+            xv[i] = *reinterpret_cast<const u16x8*>(x + int64_t(row) * K + kStep * s + 8 * ch);
+        }
+    };
+    auto stage_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+            const int p = tid + 512 * i, r = p / (kStep / 8), ch = p % (kStep / 8);
+            u16x8 o = xv[i];
+            if constexpr (kBits == 4) o = __builtin_shufflevector(xv[i], xv[i], 0, 4, 1, 5, 2, 6, 3, 7);
+            *reinterpret_cast<u16x8*>(&xs(buf)[r * kXS + 8 * ch]) = o;
+        }
+    };
+    fetch_x(0);
+
+    // packed weights of every step: piece p = tid + 512 i of a step's
+    // kCols x kWPC words is 16-byte piece p % (kWPC / 4) of column p / (kWPC / 4)
+    u32x4 wq[kSteps][kWLoads];
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s)
+#pragma unroll
+        for (int i = 0; i < kWLoads; ++i) {
+            const int p = tid + 512 * i, c = p / (kWPC / 4), pc = p % (kWPC / 4);
+            const int64_t col = n0 + c < N ? n0 + c : N - 1;
+            wq[s][i] = *reinterpret_cast<const u32x4*>(w + col * wpr + kWPC * s + 4 * pc);
+        }
+    auto stage_w = [&](int buf, int s) {
+#pragma unroll
+        for (int i = 0; i < kWLoads; ++i) {
+            const int p = tid + 512 * i, c = p / (kWPC / 4), pc = p % (kWPC / 4);
+            *reinterpret_cast<u32x4*>(&ws(buf)[c * kWS + 4 * pc]) = wq[s][i];
+        }
+    };
+
+    // scales and biases to float, [which][column][group] with rows of gpr + 1;
+    // only threads holding a piece store it (the repeats would pile onto
+    // one LDS address)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (i >= sb_rounds || tid + 512 * i >= 2 * span_pieces) break;
+        float* d = sbs + pdst[i];
+        if (sb_dtype == GDN_F32) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) d[j] = __uint_as_float(pv[i][j]);
+        } else if (sb_dtype == GDN_BF16) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) d[j] = __uint_as_float((j & 1) ? pv[i][j >> 1] & 0xFFFF0000u : pv[i][j >> 1] << 16);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) d[j] = f16_bits_to_f32(uint16_t(pv[i][j >> 1] >> (16 * (j & 1))));
+        }
+    }
+
+    f32x4 acc[kMT][kTN];
+#pragma unroll
+    for (int tm = 0; tm < kMT; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < kTN; ++tn) acc[tm][tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    bf16x8 ones;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = static_cast<__bf16>(1.0f);
+    constexpr float kQScale = kBits == 4 ? 16.f : 1.f;  // P = kQScale (P' - X) for 4-bit codes
+    const CodeConsts kc = code_consts();
+
+    // wave wv's slice of step s from tile buffer buf
+    auto compute = [&](int buf, int s) {
+        const uint16_t* xb = xs(buf);
+        const uint32_t* wb = ws(buf);
+        const int g = (kStep * s + kSlice * wv) / group_size;
+        bf16x8 a[kMT][kKB];
+        f32x4 X[kMT];
+#pragma unroll
+        for (int tm = 0; tm < kMT; ++tm) {
+#pragma unroll
+            for (int kb = 0; kb < kKB; ++kb)
+                a[tm][kb] = *reinterpret_cast<const bf16x8*>(&xb[(16 * tm + lr) * kXS + kSlice * wv + 32 * kb + 8 * lq]);
+            X[tm] = mfma_bf16(a[tm][0], ones, zero);
+            if constexpr (kKB == 2) X[tm] = mfma_bf16(a[tm][1], ones, X[tm]);
+        }
+#pragma unroll
+        for (int tn = 0; tn < kTN; ++tn) {
+            const int c = 16 * tn + lr;
+            const float sc = sbs[c * (gpr + 1) + g], bi = sbs[kSBRow + c * (gpr + 1) + g];
+            const float sp = kQScale * sc, cb = kBits == 4 ? __builtin_fmaf(-kQScale, sc, bi) : bi;
+            bf16x8 bq[kKB];
+#pragma unroll
+            for (int kb = 0; kb < kKB; ++kb)
+                bq[kb] = code_fragment<kBits>(&wb[c * kWS + (kSlice * wv + 32 * kb + 8 * lq) * kBits / 32], kc);
+#pragma unroll
+            for (int tm = 0; tm < kMT; ++tm) {
+                f32x4 P = mfma_bf16(a[tm][0], bq[0], zero);
+                if constexpr (kKB == 2) P = mfma_bf16(a[tm][1], bq[1], P);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[tm][tn][i] = __builtin_fmaf(cb, X[tm][i], __builtin_fmaf(sp, P[i], acc[tm][tn][i]));
+            }
+        }
+    };
+
+    if constexpr (kBufs == 2) {
+        stage_x(0);
+        stage_w(0, 0);
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const int buf = s & 1;
+            if (s + 1 < kSteps) fetch_x(s + 1);
+            compute(buf, s);
+            if (s + 1 < kSteps) {
+                stage_x(buf ^ 1);
+                stage_w(buf ^ 1, s + 1);
+            }
+            __syncthreads();
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            if (s > 0) __syncthreads();  // the previous step's reads of the tiles are done
+            stage_x(0);
+            stage_w(0, s);
+            __syncthreads();
+            if (s + 1 < kSteps) fetch_x(s + 1);
+            compute(0, s);
+        }
+        __syncthreads();
+    }
+
+    // Sum of the 8 waves' blocks: waves 4-7 hand theirs to waves 0-3, which
+    // add them in place; every thread then adds the 4 sums for its outputs.
+    // A block holds each lane's kMT x kTN tiles as float4 at
+    // [(blk kMT + tm) kTN + tn][lane].
+    f32x4* mine = part + (wv & 3) * kMT * kTN * 64 + l;
+    if (wv >= 4) {
+#pragma unroll
+        for (int tm = 0; tm < kMT; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < kTN; ++tn) mine[(tm * kTN + tn) * 64] = acc[tm][tn];
+    }
+    __syncthreads();
+    if (wv < 4) {
+#pragma unroll
+        for (int tm = 0; tm < kMT; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < kTN; ++tn)
+                mine[(tm * kTN + tn) * 64] = acc[tm][tn] + mine[(tm * kTN + tn) * 64];
+    }
+    __syncthreads();
+    // float4 f = tid + 512 j of a block: tile f / 64 = tm kTN + tn, lane f % 64,
+    // rows 16 tm + 4 (lane / 16) + i, column 16 tn + lane % 16
+    constexpr int kF = kMT * kTN * 64;
+    auto store = [&](auto put) {
+#pragma unroll
+        for (int j = 0; j < (kF + 511) / 512; ++j) {
+            const int f = tid + 512 * j;
+            if (f < kF) {
+                const f32x4 v = (part[f] + part[kF + f]) + (part[2 * kF + f] + part[3 * kF + f]);
+                const int t = f >> 6, ln = f & 63, tm = t / kTN, tn = t % kTN;
+                const int n = n0 + 16 * tn + (ln & 15), m0 = 16 * tm + 4 * (ln >> 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (m0 + i < M && n < N) put(int64_t(m0 + i) * N + n, v[i]);
+            }
+        }
+    };
+    if (y_dtype == GDN_BF16)
+        store([&](int64_t i, float v) { static_cast<uint16_t*>(y)[i] = f32_to_bf16_bits(v); });
+    else if (y_dtype == GDN_F16)
+        store([&](int64_t i, float v) { static_cast<uint16_t*>(y)[i] = f32_to_f16_bits(v); });
+    else
+        store([&](int64_t i, float v) { static_cast<float*>(y)[i] = v; });
+}
+
+template <int kBits, int kMT, int kSlice, int kCols>
+int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
+                     void* y, int y_dtype, int M, int N, int K, int group_size, hipStream_t s) {
+    const dim3 grid(unsigned((N + kCols - 1) / kCols));
+#define GDN_DEC(STEPS)                                                                              \
+    hipLaunchKernelGGL((qlinear_decode_kernel<kBits, STEPS, kMT, kSlice, kCols>), grid, dim3(512), 0, s, \
+                       static_cast<const uint16_t*>(x), w, scales, biases, sb_dtype, y, y_dtype, M, N,   \
+                       K, group_size)
+    switch (K / (8 * kSlice)) {
+        case 1: GDN_DEC(1); break;
+        case 2: GDN_DEC(2); break;
+        case 4: GDN_DEC(4); break;
+        case 8:
+            if constexpr (kBits == 4 || kSlice == 32) {
+                GDN_DEC(8);
+                break;
+            }
+            return -1;
+        case 16:
+            if constexpr (kBits == 4 && kSlice == 32) {
+                GDN_DEC(16);
+                break;
+            }
+            return -1;
         default: return -1;
     }
-#undef GDN_SMALL
+#undef GDN_DEC
     return check_launch("gdn_quantized_matmul");
+}
+
+// The k slice a wave takes per step: one whole group of 32, else 64 k.
+int decode_slice(int group_size) { return group_size == 32 ? 32 : 64; }
+
+// Whether the decode kernel takes this call (M <= 64 checked by the caller):
+// the step counts launch_decode_mt instantiates, the scale rows the LDS
+// holds, scales in whole 16-byte pieces of one column, aligned operands.
+bool decode_kernel_fits(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
+                        int N, int K, int bits, int group_size) {
+    const int slice = decode_slice(group_size), step = 8 * slice;
+    const int ks = K / step, gpr = K / group_size, per_piece = sb_dtype == GDN_F32 ? 4 : 8;
+    const int words_per_thread = ks * step * bits / 32 / 8;  // packed weight words each thread holds
+    const bool steps_ok = K % step == 0 && (ks == 1 || ks == 2 || ks == 4 || ks == 8 || ks == 16) &&
+                          words_per_thread <= 64;
+    const auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    return steps_ok && gpr <= kDecGroups && gpr % per_piece == 0 && al(x) && al(w) && al(scales) && al(biases);
+}
+
+// Up to 32 rows, workgroups of 32 columns where every thread still gets a
+// weight piece (64-k slices or 8-bit codes): two fit on a CU, which doubles
+// the waves that hide the LDS and MFMA latencies and spreads the columns
+// over all CUs. 33-64 rows keep 64 columns (the LDS holds one workgroup).
+int launch_decode(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
+                  void* y, int y_dtype, int M, int N, int K, int bits, int group_size, hipStream_t s) {
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+#define GDN_ARGS x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s
+#define GDN_MT(BITS, SLICE, NARROW)                                                \
+    do {                                                                           \
+        if (mt == 1) return launch_decode_mt<BITS, 1, SLICE, NARROW>(GDN_ARGS);    \
+        if (mt == 2) return launch_decode_mt<BITS, 2, SLICE, NARROW>(GDN_ARGS);    \
+        return launch_decode_mt<BITS, 4, SLICE, 64>(GDN_ARGS);                     \
+    } while (0)
+    if (bits == 4) {
+        if (decode_slice(group_size) == 32) GDN_MT(4, 32, 64);
+        GDN_MT(4, 64, 32);
+    }
+    if (decode_slice(group_size) == 32) GDN_MT(8, 32, 32);
+    GDN_MT(8, 64, 32);
+#undef GDN_MT
+#undef GDN_ARGS
 }
 
 template <int kBits, class SB, class O>
@@ -333,21 +561,13 @@ int launch_qlinear(const void* x, const uint32_t* w, const void* scales, const v
     return check_launch("gdn_quantized_matmul");
 }
 
-// Kernel choice: M <= 64 (decode) takes the weight-stationary kernel when
-// K / 256 is 1, 2, 4, 8 or 16 (hidden sizes up to 4096), else 64 x 32 tiles;
-// larger M takes 128 x 128 tiles.
+// Kernel choice for the tiled kernels: 64 x 32 tiles for M <= 64, 128 x 128
+// tiles for larger M. (Decode-sized calls the decode kernel takes never get
+// here.)
 template <int kBits, class SB, class Y>
 int dispatch_qlinear(const void* x, const uint32_t* w, const void* scales, const void* biases,
                      void* y, int M, int N, int K, int group_size, hipStream_t s) {
-    if (M <= 64) {
-        const int ks = K / kSmallBK;
-        if (K % kSmallBK == 0 && (ks == 1 || ks == 2 || ks == 4 || ks == 8 || ks == 16) &&
-            64 * (K / group_size) * int(sizeof(typename SB::storage)) <= kSmallSBBytes &&
-            int64_t(N) * (K / group_size) * int(sizeof(typename SB::storage)) % 16 == 0 &&
-            reinterpret_cast<uintptr_t>(scales) % 16 == 0 && reinterpret_cast<uintptr_t>(biases) % 16 == 0)
-            return launch_small_m<kBits, SB, Y>(x, w, scales, biases, y, M, N, K, group_size, s);
-        return launch_qlinear<64, 32, kBits, SB, Y>(x, w, scales, biases, y, M, N, K, group_size, s);
-    }
+    if (M <= 64) return launch_qlinear<64, 32, kBits, SB, Y>(x, w, scales, biases, y, M, N, K, group_size, s);
     return launch_qlinear<128, 128, kBits, SB, Y>(x, w, scales, biases, y, M, N, K, group_size, s);
 }
 
@@ -430,6 +650,8 @@ extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, c
                 "gdn_quantized_matmul: y overlaps x");
     hipStream_t s = as_stream(stream);
     const auto* wp = static_cast<const uint32_t*>(w);
+    if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, N, K, bits, group_size))
+        return launch_decode(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size, s);
     if (bits == 4) return dispatch_sb<4>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);
     return dispatch_sb<8>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);
 }

@@ -30,6 +30,18 @@ def _dev_weights(gpu, words, s, b, sb):
             "biases": torch.tensor(b, dtype=torch.float32, device=gpu).to(_TORCH[sb])}
 
 
+def _decode_kernel_takes(M, K, bits, gs, sb):
+    """Mirror of gdn_quantized_matmul's kernel choice (decode_kernel_fits in
+    gdn_qlinear.hip): the decode kernel multiplies by the exact weights
+    s * q + b in float, the tiled kernels by the weights rounded to bf16."""
+    if M > 64:
+        return False
+    step = 8 * (32 if gs == 32 else 64)
+    ks, gpr = K // step, K // gs
+    return (K % step == 0 and ks in (1, 2, 4, 8, 16) and ks * step * bits // 256 <= 64
+            and gpr <= 64 and gpr % (4 if sb == "f32" else 8) == 0)
+
+
 @pytest.mark.parametrize("M,N,K,bits,gs,sb", [
     (1, 40, 128, 4, 64, "bf16"),
     (7, 96, 256, 4, 32, "f16"),
@@ -42,15 +54,21 @@ def _dev_weights(gpu, words, s, b, sb):
     (3, 77, 256, 4, 64, "bf16"),        # scales span not whole 16-byte pieces: tiled kernel
     (16, 200, 1024, 4, 32, "f32"),      # decode kernel with float32 scales
     (64, 100, 4096, 8, 32, "f32"),      # scales exceed the decode kernel's LDS: tiled kernel
-    (9, 64, 4096, 8, 128, "bf16"),      # decode kernel, 16 K steps, 8-bit
+    (9, 64, 4096, 8, 128, "bf16"),      # 8-bit codes past the decode kernel's registers: tiled
+    (1, 4096, 2048, 4, 64, "bf16"),     # decode kernel, one row
+    (2, 78, 512, 4, 64, "bf16"),        # decode kernel, one step, last block partial
+    (17, 130, 2048, 8, 64, "f16"),      # decode kernel, 8-bit codes, 64-k slices
+    (48, 96, 1024, 4, 128, "f32"),      # decode kernel, two slices per group
 ])
 def test_quantized_matmul_matches_oracle(gpu, M, N, K, bits, gs, sb):
     rng = np.random.default_rng(M + N + K)
     words, s, b = _weights(rng, N, K, bits, gs, sb)
     x = R.bf16_round(rng.standard_normal((M, K)))
-    # bf16 activations: the weights enter the MFMAs dequantized to bf16
-    # whatever the scales' dtype (gdn_quantized_matmul's contract)
-    ref = Q.quantized_matmul(x, words, s, b, bits, gs, w_round="bf16")
+    # bf16 activations: the decode kernel applies scales and biases to float
+    # partial sums (exact weights); the tiled kernels dequantize the weights
+    # to bf16 whatever the scales' dtype (gdn_quantized_matmul's contract)
+    exact = _decode_kernel_takes(M, K, bits, gs, sb)
+    ref = Q.quantized_matmul(x, words, s, b, bits, gs, w_round="f32" if exact else "bf16")
     scheme = gdn.QuantScheme(bits, gs)
     W = _dev_weights(gpu, words, s, b, sb)
     xt = torch.tensor(x, dtype=torch.float32, device=gpu).to(torch.bfloat16)
