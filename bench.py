@@ -213,37 +213,46 @@ class PrefillWorkload:
 class QLinearWorkload:
     """The layer's stacked input projection (qkv | z | a | b: 2048 -> 12352)
     as a 4-bit affine (group 64, bf16 scales/biases) quantized matmul of M
-    bf16 rows; random codes, scales ~U(0.001, 0.01), biases ~U(-0.05, 0.05)."""
+    bf16 rows; random codes, scales ~U(0.001, 0.01), biases ~U(-0.05, 0.05).
+    With `rotate` the packed weights, scales and biases cycle through enough
+    copies (over 320 MB) that every launch reads them from HBM rather than
+    the 256 MB Infinity Cache, as a decode step does after the other layers'
+    weights have passed through it."""
 
-    def __init__(self, dev, M, N=12352, K=2048, bits=4, group_size=64, seed=0):
+    def __init__(self, dev, M, N=12352, K=2048, bits=4, group_size=64, seed=0, rotate=True):
         g = torch.Generator(device=dev).manual_seed(seed)
         self.x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
-        self.w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K * bits // 32), generator=g,
-                               device=dev, dtype=torch.int32)
-        self.scales = (torch.rand(N, K // group_size, generator=g, device=dev) * 0.009
-                       + 0.001).to(torch.bfloat16)
-        self.biases = ((torch.rand(N, K // group_size, generator=g, device=dev) - 0.5)
-                       * 0.1).to(torch.bfloat16)
+        wbytes = N * K * bits // 8 + 2 * N * (K // group_size) * 2
+        self.copies = -(-320_000_000 // wbytes) if rotate else 1
+        self.weights = []
+        for _ in range(self.copies):
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K * bits // 32), generator=g,
+                              device=dev, dtype=torch.int32)
+            sc = (torch.rand(N, K // group_size, generator=g, device=dev) * 0.009
+                  + 0.001).to(torch.bfloat16)
+            bi = ((torch.rand(N, K // group_size, generator=g, device=dev) - 0.5)
+                  * 0.1).to(torch.bfloat16)
+            self.weights.append((w, sc, bi))
         self.y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
         self.M, self.N, self.K = M, N, K
         self.flops = 2 * M * N * K
-        self.bytes = (N * K * bits // 8 + 2 * N * (K // group_size) * 2 + M * K * 2 + M * N * 2)
+        self.bytes = wbytes + M * K * 2 + M * N * 2
         from mlx_lean_moe_amd import _lib
 
         self._fn = _lib.load().gdn_quantized_matmul
-        self._args = (self.x.data_ptr(), _lib.GDN_BF16, self.w.data_ptr(),
-                      self.scales.data_ptr(), self.biases.data_ptr(), _lib.GDN_BF16,
-                      self.y.data_ptr(), _lib.GDN_BF16, M, N, K, bits, group_size,
-                      torch.cuda.current_stream().cuda_stream)
+        stream = torch.cuda.current_stream().cuda_stream
+        self._args = [(self.x.data_ptr(), _lib.GDN_BF16, w.data_ptr(), sc.data_ptr(),
+                       bi.data_ptr(), _lib.GDN_BF16, self.y.data_ptr(), _lib.GDN_BF16, M, N, K,
+                       bits, group_size, stream) for w, sc, bi in self.weights]
 
     def step(self, s):
-        rc = self._fn(*self._args)
+        rc = self._fn(*self._args[s % self.copies])
         if rc != 0:
             raise RuntimeError(f"gdn_quantized_matmul failed with {rc}")
 
 
-def bench_qlinear(dev, M, steps, warmup):
-    w = QLinearWorkload(dev, M)
+def bench_qlinear(dev, M, steps, warmup, rotate=True):
+    w = QLinearWorkload(dev, M, rotate=rotate)
     total_ms, isolated_ms = time_steps(w.step, steps, warmup)
     ms = total_ms / steps
     return {"kernel_us": ms * 1e3, "isolated_launch_us": isolated_ms * 1e3,
@@ -337,6 +346,36 @@ def cpu_baseline_decode(B, Hk, Hv, budget_s=10.0):
         "kind": "port",
         "sample": f"{steps} fused decode steps of the B={B}, Hv={Hv} workload "
                   f"({B * steps} tokens, {dt:.1f} s), float32 C/OpenMP restatement",
+    }
+
+
+def cpu_baseline_qlinear(M=64, N=12352, K=2048, bits=4, group_size=64, budget_s=10.0):
+    """The oracle's restatement of the quantized projection (dequantize the
+    MLX-packed codes, then x @ W.T; what mx.quantized_matmul computes on the
+    reference's CPU path, model/moe_block.py:44-55) timed on the host over a
+    bounded number of calls of the same M=64 workload."""
+
+    from oracle import quant_ref as Q
+
+    rng = np.random.default_rng(0)
+    words = rng.integers(0, 2 ** 32, (N, K * bits // 32), dtype=np.uint64).astype(np.uint32)
+    scales = rng.uniform(0.001, 0.01, (N, K // group_size))
+    biases = rng.uniform(-0.05, 0.05, (N, K // group_size))
+    x = rng.standard_normal((M, K))
+    Q.quantized_matmul(x, words, scales, biases, bits, group_size, w_round="f32")
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        Q.quantized_matmul(x, words, scales, biases, bits, group_size, w_round="f32")
+        calls += 1
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    return {
+        "value": M * calls / dt,
+        "unit": "tokens/s",
+        "cores": min(threads, len(os.sched_getaffinity(0))),
+        "kind": "port",
+        "sample": f"{calls} calls of the M={M} N={N} K={K} 4-bit projection ({M * calls} tokens, "
+                  f"{dt:.1f} s), NumPy float64 dequantize + BLAS matmul",
     }
 
 
@@ -448,7 +487,8 @@ def main(argv=None):
 
     if args.workload == "qlinear":
         dec = bench_qlinear(dev, 64, args.steps, args.warmup)
-        pre = bench_qlinear(dev, 4096, max(args.steps // 4, 5), args.warmup)
+        pre = (None if args.no_also else
+               bench_qlinear(dev, 4096, max(args.steps // 4, 5), args.warmup, rotate=False))
         print(json.dumps({
             "metric": "4-bit affine quantized input projection (hidden 2048 -> qkv|z|a|b 12352)",
             "value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -458,10 +498,13 @@ def main(argv=None):
             "config": {"workload": "gdn_quantized_matmul M=64 (decode) N=12352 K=2048, "
                                    "4-bit group 64, bf16 scales/biases"},
             "roofline": {"bound": "hbm", "achieved": dec["hbm_gbs"], "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": dec["hbm_gbs"] / HBM_PEAK_GBS, "traffic": None,
+                         "unit": "GB/s", "frac": dec["hbm_gbs"] / HBM_PEAK_GBS,
+                         "traffic": load_traffic("gdn_quantized_matmul_m64_n12352_k2048_traffic.json"),
                          "kernel": "gdn_quantized_matmul", "kernel_us": dec["kernel_us"],
+                         "isolated_launch_us": dec["isolated_launch_us"],
                          "algorithmic_bytes_per_launch": dec["bytes_per_launch"]},
-            "also": {"prefill_m4096": {
+            **({} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_qlinear()}),
+            "also": {} if pre is None else {"prefill_m4096": {
                 "kernel_us": pre["kernel_us"], "tflops": pre["tflops"],
                 "mfma_frac": pre["tflops"] / BF16_PEAK_TFLOPS,
                 "flops_per_launch": pre["flops_per_launch"]}}}))

@@ -183,8 +183,15 @@ int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, co
  *   y: (M, N) y_dtype
  *   bits 4 or 8 (others: GDN_EUNSUPPORTED); group_size 32, 64 or 128; K a
  *   multiple of 64 and of group_size
- * The weights enter the MFMAs as bf16(scale * q + bias) (the product is exact
- * in float32; one rounding), i.e. x times the weights mx.dequantize yields.
+ * Up to 64 rows, on the shapes the decode kernel takes (decode_kernel_fits in
+ * gdn_qlinear.hip: K in whole steps of 8 quantization slices, K / group_size
+ * <= 64, 16-byte aligned operands; the layer's projections at hidden 2048 and
+ * value dim 4096 all qualify): products against the exact weights
+ * scale * q + bias, with scale
+ * and bias applied per group to float partial sums (as MLX's matrix-vector
+ * kernels do). Otherwise the weights enter the MFMAs as bf16(scale * q + bias)
+ * (the product is exact in float32; one rounding), i.e. x times the weights
+ * mx.dequantize yields (as MLX's matrix-matrix kernels do).
  * Replaces mx.quantized_matmul(..., mode="affine") in quantized_linear
  * (model/moe_block.py:44-55), used for the layer's projections
  * (model/qwen3_5/linear_attention.py:96-101,125).
