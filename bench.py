@@ -12,8 +12,10 @@ Also measured in the same run (reported under "also"):
   decode_large: B=256, Hv=64, fused conv roll + gated RMSNorm (1 GiB state)
   prefill:      B=1, T=4096 chunked prefill (bf16 MFMA)
   prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
+  decode_slots: B=64 active sequences at random slots of a 256-sequence pool
 
-python bench.py [--steps K] [--warmup W] [--workload decode|decode_large|prefill|prefill_varlen|qlinear|copy]
+python bench.py [--steps K] [--warmup W]
+                [--workload decode|decode_large|decode_slots|prefill|prefill_varlen|qlinear|copy]
 """
 
 from __future__ import annotations
@@ -97,7 +99,7 @@ class DecodeWorkload:
                 self.z[s % n_i].data_ptr() if self.with_z else None,
                 self.norm_w.data_ptr() if self.with_z else None, 1e-6, self.out.data_ptr(),
                 _lib.GDN_BF16, self.B, d.num_key_heads, d.num_value_heads, 128, 128, 4,
-                _lib.GDN_BF16, stream))
+                _lib.GDN_BF16, None, 0, stream))
         self._fn = lib.gdn_decode_step
         return phases
 
@@ -133,6 +135,78 @@ def time_steps(step, steps, warmup):
     torch.cuda.synchronize()
     launch_ms = float(np.mean([e0.elapsed_time(e1) for e0, e1 in pairs]))
     return total_ms, launch_ms
+
+
+class SlotDecodeWorkload:
+    """B active sequences decoding out of a device pool of P = 4 B state
+    slots (the pool with slot indices): step s takes the next of four
+    disjoint random slot sets, so the 512 MB of state the steps touch exceed
+    the Infinity Cache. A step is the fused kernel on those slots (state
+    tiles updated in place at the slots) plus the copy of the B rolled conv
+    rows back to their slots."""
+
+    def __init__(self, dev, B, Hk, Hv, seed=0, n_inputs=8):
+        d, K = 128, 4
+        self.dims = gdn.LinearAttentionDims(Hk, Hv, d, d, K)
+        C = self.dims.conv_dim
+        P = 4 * B
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        randn = lambda *s: torch.randn(*s, generator=g, device=dev)
+        self.qkv = [randn(B, C).to(bf) for _ in range(n_inputs)]
+        self.a = [randn(B, Hv).to(bf) for _ in range(n_inputs)]
+        self.b = [randn(B, Hv).to(bf) for _ in range(n_inputs)]
+        self.state = randn(P, Hv, d, d) * 0.05
+        self.conv = randn(P, K - 1, C).to(bf)
+        self.conv_out = torch.empty(B, K - 1, C, dtype=bf, device=dev)
+        self.conv_w = randn(C, K) * 0.2
+        self.A_log = torch.rand(Hv, generator=g, device=dev) * float(np.log(16))
+        self.dt_bias = torch.rand(Hv, generator=g, device=dev) * 2 - 1
+        self.out = torch.empty(B, Hv, d, dtype=bf, device=dev)
+        perm = torch.randperm(P, generator=torch.Generator().manual_seed(seed))
+        self.slots = [perm[i * B:(i + 1) * B].to(dev) for i in range(4)]
+        self.slots32 = [s_.to(torch.int32) for s_ in self.slots]
+        self.B, self.P = B, P
+        _, _, kernel_bytes = decode_bytes(B, Hk, Hv, d, K, False)
+        self.kernel_bytes = kernel_bytes
+        self.bytes_per_step = kernel_bytes + 2 * B * (K - 1) * C * 2  # + the conv rows' copy
+        from mlx_lean_moe_amd import _lib
+
+        self._fn = _lib.load().gdn_decode_step
+        stream = torch.cuda.current_stream().cuda_stream
+        self.args = [(self.qkv[s_ % n_inputs].data_ptr(), self.conv.data_ptr(),
+                      self.conv_out.data_ptr(), self.conv_w.data_ptr(),
+                      self.a[s_ % n_inputs].data_ptr(), self.b[s_ % n_inputs].data_ptr(),
+                      self.A_log.data_ptr(), self.dt_bias.data_ptr(), self.state.data_ptr(),
+                      self.state.data_ptr(), None, None, 1e-6, self.out.data_ptr(),
+                      _lib.GDN_BF16, B, Hk, Hv, d, d, K, _lib.GDN_BF16,
+                      self.slots32[s_ % 4].data_ptr(), P, stream) for s_ in range(n_inputs)]
+
+    def kernel_step(self, s):
+        rc = self._fn(*self.args[s % len(self.args)])
+        if rc != 0:
+            raise RuntimeError(f"gdn_decode_step failed with {rc}")
+
+    def step(self, s):
+        self.kernel_step(s)
+        self.conv.index_copy_(0, self.slots[s % len(self.args) % 4], self.conv_out)
+
+
+def bench_decode_slots(dev, B, Hk, Hv, steps, warmup):
+    w = SlotDecodeWorkload(dev, B, Hk, Hv)
+    kernel_ms, _ = time_steps(w.kernel_step, steps, warmup)
+    total_ms, _ = time_steps(w.step, steps, warmup)
+    k_ms, ms = kernel_ms / steps, total_ms / steps
+    return {
+        "workload": f"decode of B={B} active sequences at random slots of a pool of {w.P} "
+                    f"(Hk={Hk} Hv={Hv} d=128), four rotating slot sets",
+        "tokens_per_s": B * steps / (total_ms * 1e-3),
+        "step_us": ms * 1e3,
+        "kernel_us": k_ms * 1e3,
+        "kernel_hbm_gbs": w.kernel_bytes / (k_ms * 1e-3) / 1e9,
+        "kernel_hbm_frac": w.kernel_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "step_hbm_gbs": w.bytes_per_step / (ms * 1e-3) / 1e9,
+    }
 
 
 def bench_decode(dev, B, Hk, Hv, with_z, steps, warmup):
@@ -396,8 +470,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "prefill", "prefill_varlen", "qlinear",
-                             "copy"])
+                    choices=["decode", "decode_large", "decode_slots", "prefill",
+                             "prefill_varlen", "qlinear", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary workloads")
     args = ap.parse_args(argv)
@@ -467,7 +541,9 @@ def main(argv=None):
             lg = bench_decode(dev, 256, 16, 64, True, steps=64, warmup=8)
             pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
             pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
+            sl = bench_decode_slots(dev, 64, 16, 32, steps=64, warmup=8)
             line["also"] = {
+                "decode_slots": sl,
                 "decode_large": {
                     "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
                     "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],
@@ -483,6 +559,20 @@ def main(argv=None):
                     "tokens_per_s": pv["tokens_per_s"], "call_us": pv["call_us"],
                     "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"]}}
         print(json.dumps(line))
+        return 0
+
+    if args.workload == "decode_slots":
+        r = bench_decode_slots(dev, 64, 16, 32, args.steps, args.warmup)
+        print(json.dumps({"metric": METRIC, "value": r["tokens_per_s"], "unit": "tokens/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["step_us"] * 1e-3, "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic", "config": {"workload": r["workload"]},
+                          "roofline": {"bound": "hbm", "achieved": r["kernel_hbm_gbs"],
+                                       "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                       "frac": r["kernel_hbm_frac"], "traffic": None,
+                                       "kernel": "gdn_decode_step (slots)",
+                                       "kernel_us": r["kernel_us"], "step_us": r["step_us"]}}))
         return 0
 
     if args.workload == "qlinear":

@@ -113,7 +113,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const typename Act::storage* __restrict__ a_in, const typename Act::storage* __restrict__ b_in,
     const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* S_in,
     float* S_out, const typename Act::storage* __restrict__ z, const float* __restrict__ norm_w,
-    float eps, void* __restrict__ out, int y_dtype, int Hk, int Hv) {
+    float eps, void* __restrict__ out, int y_dtype, int Hk, int Hv,
+    const int32_t* __restrict__ slots, int pool) {
     __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
     __shared__ float gate_g, gate_beta, norm_r;
 
@@ -123,11 +124,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const int r = Hv / Hk, hk = h / r;
     const int tid = threadIdx.x;
     const int w = tid >> 6, l = tid & 63, half = l >> 5, l32 = l & 31;
+    // the state slot of batch row b: its conv state is read and its state
+    // tile read and written there; everything else is indexed by row
+    const int sl = slots ? slots[b] : b;
+    if (unsigned(sl) >= unsigned(pool)) {  // a slot outside the pool: touch no state
+        if (tid < kD) store_any(out, size_t(bh) * kD + tid, kNorm ? Act::code : y_dtype, __builtin_nanf(""));
+        return;
+    }
+    const size_t sh = size_t(sl) * Hv + h;  // the state tile's index
 
     // A. the front-end's few inputs first, then the 16 float4 state loads:
     // waiting for the former does not wait for the latter.
     const typename Act::storage* x = qkv + size_t(b) * C;
-    const typename Act::storage* cs = cs_in + size_t(b) * (kTaps - 1) * C;
+    const typename Act::storage* cs = cs_in + size_t(sl) * (kTaps - 1) * C;
     typename Act::storage* cso = cs_out + size_t(b) * (kTaps - 1) * C;
     const float4* w4 = reinterpret_cast<const float4*>(conv_w);
     const int e = tid & (kD - 1);
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const float av = Act::load(a_in, bh), bv = Act::load(b_in, bh);
     const float alog = A_log[h], dtb = dt_bias[h];
 
-    const float4* Sb = reinterpret_cast<const float4*>(S_in + size_t(bh) * kD * kD);
+    const float4* Sb = reinterpret_cast<const float4*>(S_in + sh * kD * kD);
     float4 s[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = load_state(&Sb[(8 * i + 2 * w + half) * (kD / 4) + l32]);
@@ -199,7 +208,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     __syncthreads();
 
     // H. update and store the tile.
-    float4* So = reinterpret_cast<float4*>(S_out + size_t(bh) * kD * kD);
+    float4* So = reinterpret_cast<float4*>(S_out + sh * kD * kD);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int row = 8 * i + 2 * w + half;
@@ -241,7 +250,8 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                                const float* A_log, const float* dt_bias, const float* state_in,
                                float* state_out, const void* z, const float* norm_weight,
                                float norm_eps, void* out, int y_dtype, int B, int Hk, int Hv,
-                               int Dk, int Dv, int K, int act_dtype, void* stream) {
+                               int Dk, int Dv, int K, int act_dtype, const int32_t* slots,
+                               int pool, void* stream) {
     GDN_REQUIRE(B >= 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, "gdn_decode_step: bad head counts");
     GDN_REQUIRE(act_dtype == GDN_F32 || act_dtype == GDN_BF16,
                 "gdn_decode_step: activations must be float32 or bfloat16");
@@ -254,11 +264,13 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                     dt_bias && state_in && state_out && out,
                 "gdn_decode_step: null pointer");
     GDN_REQUIRE(!z || norm_weight, "gdn_decode_step: z without norm_weight");
+    if (!slots) pool = B;
+    GDN_REQUIRE(pool >= 1, "gdn_decode_step: bad pool size %d", pool);
     const int64_t C = 2LL * Hk * kD + int64_t(Hv) * kD;
-    const int64_t conv_bytes = int64_t(B) * (kTaps - 1) * C * dtype_size(act_dtype);
-    GDN_REQUIRE(!overlaps(conv_state_in, conv_bytes, conv_state_out, conv_bytes),
+    const int64_t row_bytes = (kTaps - 1) * C * dtype_size(act_dtype);
+    GDN_REQUIRE(!overlaps(conv_state_in, int64_t(pool) * row_bytes, conv_state_out, int64_t(B) * row_bytes),
                 "gdn_decode_step: conv_state_out overlaps conv_state_in");
-    const int64_t state_bytes = int64_t(B) * Hv * kD * kD * 4;
+    const int64_t state_bytes = int64_t(pool) * Hv * kD * kD * 4;
     GDN_REQUIRE(state_in == state_out || !overlaps(state_in, state_bytes, state_out, state_bytes),
                 "gdn_decode_step: state_out partially overlaps state_in");
     GDN_REQUIRE((reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out) |
@@ -273,7 +285,7 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                        static_cast<ACT::storage*>(conv_state_out), conv_weight,               \
                        static_cast<const ACT::storage*>(a), static_cast<const ACT::storage*>(b), \
                        A_log, dt_bias, state_in, state_out, static_cast<const ACT::storage*>(z), \
-                       norm_weight, norm_eps, out, y_dtype, Hk, Hv)
+                       norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool)
     if (act_dtype == GDN_BF16) {
         if (z) GDN_DECODE_LAUNCH(ActBF16, true); else GDN_DECODE_LAUNCH(ActBF16, false);
     } else {

@@ -89,9 +89,29 @@ def _fused_decode_ok(dims: LinearAttentionDims, act: torch.dtype) -> bool:
             and act in (torch.float32, torch.bfloat16))
 
 
+def check_slots(slots, batch: int, pool: int) -> list[int]:
+    """Host-side check of decode slot indices: ``batch`` distinct integers in
+    ``[0, pool)`` (two rows on one slot would race on its state)."""
+
+    if isinstance(slots, torch.Tensor):
+        if slots.ndim != 1:
+            raise ValueError("slots must be one-dimensional")
+        if slots.dtype not in (torch.int32, torch.int64):
+            raise ValueError("slots must be integers")
+        slots = slots.tolist()
+    slots = [int(v) for v in slots]
+    if len(slots) != batch:
+        raise ValueError(f"expected {batch} slots, got {len(slots)}")
+    if any(v < 0 or v >= pool for v in slots):
+        raise ValueError(f"slots must lie in [0, {pool})")
+    if len(set(slots)) != len(slots):
+        raise ValueError("slots must be distinct")
+    return slots
+
+
 def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias,
                       norm_weight, eps, dims: LinearAttentionDims, *, conv_out=None,
-                      state_out=None, y_dtype=None):
+                      state_out=None, y_dtype=None, slots=None):
     """One decode token for ``B`` sequences in a single kernel launch: conv +
     SiLU + roll, q/k scaling, gates, recurrence and gated RMSNorm
     (linear_attention.py:103-124 at L = 1).
@@ -102,6 +122,13 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     (in-place update); ``conv_out`` must be a different buffer. With ``z`` the
     result is the gated-norm output in the activation dtype; without, the
     recurrence output ``y`` in ``y_dtype`` (float32 by default).
+
+    With ``slots`` (``B`` distinct indices into a pool of ``P`` sequences),
+    ``conv_state`` is the pool's ``(P, K-1, C)`` and ``ssm_state`` its
+    ``(P, Hv, Dv, Dk)``: row ``b`` reads its conv state at ``slots[b]`` and
+    updates the state tiles of ``slots[b]`` in place (``state_out`` must be
+    ``ssm_state`` or None); ``conv_out`` is ``(B, K-1, C)`` with the rolled
+    rows in batch order, for the caller to put back at the slots.
     Returns ``(out (B, Hv, Dv), conv_out, state_out)``."""
 
     device = _require_device(qkv, z, a, b, conv_state, ssm_state)
@@ -110,10 +137,17 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     if not _fused_decode_ok(dims, act):
         raise ValueError("the fused decode kernel needs Dk = Dv = 128, K = 4 and float32 or "
                          "bfloat16 activations")
+    P = B
+    if slots is not None:
+        P = ssm_state.shape[0]
+        slot_list = check_slots(slots, B, P)
+        if state_out is not None and state_out is not ssm_state:
+            raise ValueError("with slots the state is updated in place (state_out=ssm_state)")
+        state_out = ssm_state
     if (tuple(qkv.shape) != (B, dims.conv_dim) or tuple(a.shape) != (B, dims.num_value_heads)
             or b.shape != a.shape
-            or tuple(conv_state.shape) != (B, dims.conv_kernel_dim - 1, dims.conv_dim)
-            or tuple(ssm_state.shape) != (B, dims.num_value_heads, dims.value_head_dim,
+            or tuple(conv_state.shape) != (P, dims.conv_kernel_dim - 1, dims.conv_dim)
+            or tuple(ssm_state.shape) != (P, dims.num_value_heads, dims.value_head_dim,
                                            dims.key_head_dim)
             or (z is not None and tuple(z.shape) != (B, dims.num_value_heads, dims.value_head_dim))):
         raise ValueError("fused_decode_step: inconsistent shapes")
@@ -127,9 +161,13 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     A_log, dt_bias = _c(A_log.float()), _c(dt_bias.float())
     norm_weight = _c(norm_weight.float()) if z is not None else None
     if conv_out is None:
-        conv_out = torch.empty_like(conv_state)
+        conv_out = torch.empty((B,) + tuple(conv_state.shape[1:]), dtype=act, device=device)
+    elif tuple(conv_out.shape) != (B, dims.conv_kernel_dim - 1, dims.conv_dim) or conv_out.dtype != act:
+        raise ValueError("conv_out must be (B, K-1, C) in the activation dtype")
     if state_out is None:
         state_out = torch.empty_like(ssm_state)
+    slot_t = (torch.tensor(slot_list, dtype=torch.int32, device=device)
+              if slots is not None else None)
     out_dtype = act if z is not None else (y_dtype or torch.float32)
     out = torch.empty((B, dims.num_value_heads, dims.value_head_dim), dtype=out_dtype,
                       device=device)
@@ -138,7 +176,7 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
               _lib.ptr(dt_bias), _lib.ptr(ssm_state), _lib.ptr(state_out), _lib.ptr(z),
               _lib.ptr(norm_weight), float(eps), _lib.ptr(out), _lib.dtype_code(out_dtype), B,
               dims.num_key_heads, dims.num_value_heads, dims.key_head_dim, dims.value_head_dim,
-              dims.conv_kernel_dim, _lib.dtype_code(act), _stream(device))
+              dims.conv_kernel_dim, _lib.dtype_code(act), _lib.ptr(slot_t), P, _stream(device))
     return out, conv_out, state_out
 
 
@@ -270,20 +308,34 @@ class Qwen3_5LinearAttention:
                                  self.linear, conv_out=conv_out,
                                  state_out=ssm_state if in_place else None)
 
-    def decode_batch(self, x: torch.Tensor, pool: RecurrentStatePool) -> torch.Tensor:
-        """One decode token for each of the pool's ``B`` sequences: ``x (B, hidden)``
-        -> ``(B, hidden)``. The ssm slots are updated in place; the conv state
-        is double-buffered."""
+    def decode_batch(self, x: torch.Tensor, pool: RecurrentStatePool, slots=None) -> torch.Tensor:
+        """One decode token for each of the pool's sequences: ``x (pool.batch,
+        hidden)`` -> ``(pool.batch, hidden)``; or, with ``slots`` (distinct
+        pool indices, e.g. the sequences a scheduler has active this step),
+        ``x (len(slots), hidden)`` for those slots only. The ssm slots are
+        updated in place by the kernel; the conv state is double-buffered
+        without slots and copied back to the slots with them."""
 
-        if x.ndim != 2 or x.shape[0] != pool.batch:
-            raise ValueError("decode_batch expects x of shape (pool.batch, hidden)")
         d = self.linear
+        rows = pool.batch if slots is None else len(slots)
+        if x.ndim != 2 or x.shape[0] != rows:
+            raise ValueError("decode_batch expects x of shape (pool.batch, hidden), or "
+                             "(len(slots), hidden) with slots")
         qkv, z, a, b = self._project(x)
         if not _fused_decode_ok(d, qkv.dtype) or pool.conv_state.dtype != qkv.dtype:
             raise ValueError("decode_batch needs Dk = Dv = 128, K = 4 and a pool in the "
                              "activation dtype (float32 or bfloat16)")
-        out, _, _ = self._decode_fused(qkv, z, a, b, pool.conv_state, pool.ssm_state,
-                                       in_place=True, conv_out=pool.conv_spare)
-        pool.swap_conv()
-        pool.size += 1
-        return self._proj(out.reshape(pool.batch, d.value_dim), self.out_proj)
+        if slots is None:
+            out, _, _ = self._decode_fused(qkv, z, a, b, pool.conv_state, pool.ssm_state,
+                                           in_place=True, conv_out=pool.conv_spare)
+            pool.swap_conv()
+            pool.size += 1
+        else:
+            slot_list = check_slots(slots, rows, pool.batch)
+            out, conv_out, _ = fused_decode_step(
+                qkv, z, a, b, pool.conv_state, pool.ssm_state, self.conv1d_weight, self.A_log,
+                self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_list)
+            index = torch.tensor(slot_list, dtype=torch.int64, device=pool.conv_state.device)
+            pool.conv_state.index_copy_(0, index, conv_out)
+            pool.size[torch.tensor(slot_list, dtype=torch.int64)] += 1
+        return self._proj(out.reshape(rows, d.value_dim), self.out_proj)

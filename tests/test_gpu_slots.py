@@ -1,0 +1,111 @@
+"""Decode of active sequences at arbitrary slots of a device state pool
+(the pool with slot indices): the fused kernel on slots equals the same
+kernel on the gathered sequences, leaves every other slot untouched, and the
+layer's pooled decode after a chunked prefill (the transformer's prefill
+loop, transformer.py:283-304, at layer level) equals per-sequence calls."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mlx_lean_moe_amd as gdn
+from mlx_lean_moe_amd import _lib
+from tests.helpers import layer_inputs, layer_params
+from tests.test_gpu_layer import HIDDEN, _build
+
+pytestmark = pytest.mark.gpu
+
+DIMS = gdn.LinearAttentionDims(2, 4, 128, 128, 4)
+
+
+def _pool_case(seed, P, B, adt, dev):
+    rng = np.random.default_rng(seed)
+    dt = (DIMS.num_key_heads, DIMS.num_value_heads, 128, 128)
+    conv_w, A_log, dt_bias, norm_w = layer_params(rng, dt)
+    qkv, z, a, b = layer_inputs(rng, dt, L=1, act_bf16=adt == torch.bfloat16, B=B)
+    t = lambda x, dtype=torch.float32: torch.tensor(np.asarray(x, np.float32), device=dev).to(dtype)
+    conv = t(rng.standard_normal((P, 3, DIMS.conv_dim)), adt)
+    state = t(rng.standard_normal((P, DIMS.num_value_heads, 128, 128)) * 0.05)
+    return dict(qkv=t(qkv[:, 0], adt), z=t(z[:, 0], adt), a=t(a[:, 0], adt), b=t(b[:, 0], adt),
+                conv=conv, state=state, conv_w=t(conv_w), A_log=t(A_log), dt_bias=t(dt_bias),
+                norm_w=t(norm_w))
+
+
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+@pytest.mark.parametrize("with_z", [False, True])
+def test_slot_decode_equals_decode_of_gathered_sequences(gpu, act, with_z):
+    adt = torch.bfloat16 if act == "bf16" else torch.float32
+    P, slots = 7, [5, 0, 3]
+    c = _pool_case(11, P, len(slots), adt, gpu)
+    z = c["z"] if with_z else None
+    idx = torch.tensor(slots, device=gpu)
+    conv_g, state_g = c["conv"][idx].clone(), c["state"][idx].clone()
+    ref_out, ref_conv, ref_state = gdn.fused_decode_step(
+        c["qkv"], z, c["a"], c["b"], conv_g, state_g, c["conv_w"], c["A_log"], c["dt_bias"],
+        c["norm_w"], 1e-6, DIMS, state_out=state_g)
+    before = c["state"].clone()
+    conv_before = c["conv"].clone()
+    out, conv_out, state_out = gdn.fused_decode_step(
+        c["qkv"], z, c["a"], c["b"], c["conv"], c["state"], c["conv_w"], c["A_log"],
+        c["dt_bias"], c["norm_w"], 1e-6, DIMS, slots=slots)
+    assert state_out is c["state"]
+    assert torch.equal(out, ref_out)
+    assert torch.equal(conv_out, ref_conv)
+    assert torch.equal(c["state"][idx], ref_state)
+    others = torch.tensor([i for i in range(P) if i not in slots], device=gpu)
+    assert torch.equal(c["state"][others], before[others])
+    assert torch.equal(c["conv"], conv_before)  # the pool's conv rows are the caller's to update
+
+
+def test_slot_outside_pool_touches_no_state(gpu):
+    """The C ABI's own guard (the Python layer rejects such slots first): a
+    row whose slot lies outside the pool writes NaN and leaves the state."""
+
+    P, B = 4, 2
+    c = _pool_case(12, P, B, torch.bfloat16, gpu)
+    before = c["state"].clone()
+    slots = torch.tensor([P, 1], dtype=torch.int32, device=gpu)
+    conv_out = torch.empty(B, 3, DIMS.conv_dim, dtype=torch.bfloat16, device=gpu)
+    out = torch.empty(B, DIMS.num_value_heads, 128, dtype=torch.float32, device=gpu)
+    _lib.call("gdn_decode_step", _lib.ptr(c["qkv"]), _lib.ptr(c["conv"]), _lib.ptr(conv_out),
+              _lib.ptr(c["conv_w"].reshape(DIMS.conv_dim, 4).contiguous()), _lib.ptr(c["a"]),
+              _lib.ptr(c["b"]), _lib.ptr(c["A_log"]), _lib.ptr(c["dt_bias"]), _lib.ptr(c["state"]),
+              _lib.ptr(c["state"]), None, None, 1e-6, _lib.ptr(out), _lib.GDN_F32, B, 2, 4, 128,
+              128, 4, _lib.GDN_BF16, _lib.ptr(slots), P, _lib.stream_ptr(gpu))
+    torch.cuda.synchronize()
+    assert torch.isnan(out[0]).all() and torch.isfinite(out[1]).all()
+    assert torch.equal(c["state"][0], before[0]) and torch.equal(c["state"][2:], before[2:])
+    assert not torch.equal(c["state"][1], before[1])
+
+
+def test_pooled_decode_after_chunked_prefill_matches_per_sequence_calls(gpu):
+    layer, _ = _build(6, DIMS, gpu, dtype=torch.bfloat16)
+    rng = np.random.default_rng(106)
+    P = 6
+    pool = gdn.RecurrentStatePool(P, 4, DIMS.conv_dim, DIMS.num_value_heads, 128, 128,
+                                  dtype=torch.bfloat16, device=gpu)
+    slots = [4, 1, 2]
+    prompts = [torch.tensor(rng.standard_normal((n, HIDDEN)), dtype=torch.bfloat16, device=gpu)
+               for n in (9, 5, 1)]
+    caches = [layer.new_cache(torch.bfloat16) for _ in slots]
+    for slot, p, cache in zip(slots, prompts, caches):
+        # prefill in chunks of 4 tokens, carrying the cache, then copy it into
+        # the pool; the cache itself goes on as the per-sequence reference
+        for start in range(0, p.shape[0], 4):
+            layer(p[start:start + 4], cache)
+        pool.load(slot, cache)
+    for step in range(3):
+        active = slots if step != 1 else [2, 4]  # a step where one sequence sits out
+        x = torch.tensor(rng.standard_normal((len(active), HIDDEN)), dtype=torch.bfloat16,
+                         device=gpu)
+        out = layer.decode_batch(x, pool, slots=active)
+        ref = torch.stack([layer(x[i], caches[slots.index(s)]) for i, s in enumerate(active)])
+        torch.testing.assert_close(out.float(), ref.float(), rtol=0, atol=0)
+    for slot, cache in zip(slots, caches):
+        torch.testing.assert_close(pool.ssm_state[slot], cache.ssm_state, rtol=0, atol=0)
+        torch.testing.assert_close(pool.conv_state[slot], cache.conv_state, rtol=0, atol=0)
+        assert int(pool.size[slot]) == cache.size
+    for free in (0, 3, 5):
+        assert not pool.ssm_state[free].any() and not pool.conv_state[free].any()

@@ -92,3 +92,18 @@ def test_promotion_matches_reference_ops_dtypes():
     assert gated_delta._promote(t(bf16), t(bf16), t(f16)) == f32
     assert gated_delta._promote(t(bf16), t(bf16)) == bf16
     assert gated_delta._promote(t(bf16), t(f32)) == f32
+
+
+def test_decode_slots_are_checked_on_the_host():
+    from mlx_lean_moe_amd.linear_attention import check_slots
+
+    assert check_slots([3, 0, 2], 3, 4) == [3, 0, 2]
+    assert check_slots(torch.tensor([1, 0], dtype=torch.int32), 2, 2) == [1, 0]
+    for bad, msg in (([0, 0], "distinct"), ([0, 4], r"\[0, 4\)"), ([-1, 0], r"\[0, 4\)"),
+                     ([0], "expected 2")):
+        with pytest.raises(ValueError, match=msg):
+            check_slots(bad, 2, 4)
+    with pytest.raises(ValueError, match="one-dimensional"):
+        check_slots(torch.zeros(2, 1, dtype=torch.int64), 2, 4)
+    with pytest.raises(ValueError, match="integers"):
+        check_slots(torch.zeros(2), 2, 4)
