@@ -104,14 +104,17 @@ def dequantize(tensors: dict, quant: QuantScheme, dtype: torch.dtype | None = No
 
 def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None) -> torch.Tensor:
     """Linear projection for self-describing, legacy quantized, or dense
-    weights (moe_block.py:27-55): ``x @ W.T`` over the last axis of ``x``,
-    in ``x``'s dtype."""
+    weights (moe_block.py:27-55): ``x @ W.T`` over the last axis of ``x``.
+    Quantized weights give ``x``'s dtype; dense ones the promotion of ``x``'s
+    and ``W``'s dtypes, as MLX's matmul does (a checkpoint's bf16 dense
+    weights are read widened to float32)."""
 
     if isinstance(tensors, LinearWeights):
         quant = tensors.quant
         tensors = tensors.tensors
     if isinstance(tensors, torch.Tensor):
-        return x @ tensors.T
+        dt = torch.promote_types(x.dtype, tensors.dtype)
+        return x.to(dt) @ tensors.to(dt).T
     if quant is None:
         raise ValueError("quantized linear weights require a quantization scheme")
     _kernel_scheme(quant)
