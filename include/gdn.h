@@ -46,7 +46,7 @@ typedef enum {
 
 /* Library ABI version (bumped on any signature change or addition; 2 adds the
  * quantized matmul and dequantize entry points, 3 the decode step's state
- * slots). */
+ * slots, 4 its conv rows). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -129,13 +129,21 @@ int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dt
  *   out:            (B, Hv, Dv): act_dtype (gated-norm output) when z != NULL,
  *                   else the recurrence output y in y_dtype
  *   slots:          NULL (row b is state slot b), or (B) int32 distinct slot
- *                   indices into a pool of `pool` sequences: conv_state_in is
- *                   then (pool, K-1, C) and read at slots[b], state_in/state_out
+ *                   indices into a pool of `pool` sequences: state_in/state_out
  *                   are (pool, Hv, Dv, Dk) and the tile of slots[b] is read and
- *                   written (pass state_out == state_in); conv_state_out stays
- *                   (B, K-1, C), row b (the caller copies it back to slots[b]).
- *                   A slot outside [0, pool) writes NaN to its output rows and
- *                   touches no state. pool is ignored when slots is NULL.
+ *                   written (pass state_out == state_in); without conv_rows,
+ *                   conv_state_in is (pool, K-1, C) read at slots[b] and
+ *                   conv_state_out (B, K-1, C) written at row b (the caller
+ *                   copies it back). pool is ignored when slots is NULL.
+ *   conv_rows:      NULL, or (B, 2) int32 (in row, out row) per batch row into
+ *                   conv arrays of conv_pool rows each (needs slots): row b
+ *                   reads its conv state at conv_rows[2b] of conv_state_in and
+ *                   writes the rolled state at conv_rows[2b+1] of
+ *                   conv_state_out. The two arrays may be one (a pool's two
+ *                   halves); out rows must be distinct and no out row may be
+ *                   an in row of the launch.
+ *   A row whose slot or conv rows fall outside the pools writes NaN to its
+ *   output and touches no state.
  * Specialised for Dk = Dv = 128, K = 4; act_dtype in {F32, BF16}.
  * Replaces one decode call of Qwen3_5LinearAttention.__call__ between the
  * projections (linear_attention.py:103-124) with the Metal scan at T=1.
@@ -145,7 +153,8 @@ int gdn_decode_step(const void *qkv, const void *conv_state_in, void *conv_state
                     const float *A_log, const float *dt_bias, const float *state_in,
                     float *state_out, const void *z, const float *norm_weight, float norm_eps,
                     void *out, int y_dtype, int B, int Hk, int Hv, int Dk, int Dv, int K,
-                    int act_dtype, const int32_t *slots, int pool, void *stream);
+                    int act_dtype, const int32_t *slots, int pool, const int32_t *conv_rows,
+                    int conv_pool, void *stream);
 
 /*
  * gdn_prefill_chunked - chunked (WY/UT, 64-token chunks) prefill on bf16

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* S_in,
     float* S_out, const typename Act::storage* __restrict__ z, const float* __restrict__ norm_w,
     float eps, void* __restrict__ out, int y_dtype, int Hk, int Hv,
-    const int32_t* __restrict__ slots, int pool) {
+    const int32_t* __restrict__ slots, int pool, const int32_t* __restrict__ conv_rows, int conv_pool) {
     __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
     __shared__ float gate_g, gate_beta, norm_r;
 
@@ -124,10 +124,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const int r = Hv / Hk, hk = h / r;
     const int tid = threadIdx.x;
     const int w = tid >> 6, l = tid & 63, half = l >> 5, l32 = l & 31;
-    // the state slot of batch row b: its conv state is read and its state
-    // tile read and written there; everything else is indexed by row
+    // the state slot of batch row b (its state tile is read and written
+    // there) and its conv state rows (read at ci, rolled into co); everything
+    // else is indexed by row
     const int sl = slots ? slots[b] : b;
-    if (unsigned(sl) >= unsigned(pool)) {  // a slot outside the pool: touch no state
+    const int ci = conv_rows ? conv_rows[2 * b] : sl, co = conv_rows ? conv_rows[2 * b + 1] : b;
+    if (unsigned(sl) >= unsigned(pool) || unsigned(ci) >= unsigned(conv_pool) ||
+        unsigned(co) >= unsigned(conv_pool)) {  // outside the pools: touch no state
         if (tid < kD) store_any(out, size_t(bh) * kD + tid, kNorm ? Act::code : y_dtype, __builtin_nanf(""));
         return;
     }
@@ -136,8 +139,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     // A. the front-end's few inputs first, then the 16 float4 state loads:
     // waiting for the former does not wait for the latter.
     const typename Act::storage* x = qkv + size_t(b) * C;
-    const typename Act::storage* cs = cs_in + size_t(sl) * (kTaps - 1) * C;
-    typename Act::storage* cso = cs_out + size_t(b) * (kTaps - 1) * C;
+    const typename Act::storage* cs = cs_in + size_t(ci) * (kTaps - 1) * C;
+    typename Act::storage* cso = cs_out + size_t(co) * (kTaps - 1) * C;
     const float4* w4 = reinterpret_cast<const float4*>(conv_w);
     const int e = tid & (kD - 1);
     // pass 1: q channel (tid < 128) or k channel (tid >= 128) of key head hk;
@@ -251,7 +254,7 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                                float* state_out, const void* z, const float* norm_weight,
                                float norm_eps, void* out, int y_dtype, int B, int Hk, int Hv,
                                int Dk, int Dv, int K, int act_dtype, const int32_t* slots,
-                               int pool, void* stream) {
+                               int pool, const int32_t* conv_rows, int conv_pool, void* stream) {
     GDN_REQUIRE(B >= 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, "gdn_decode_step: bad head counts");
     GDN_REQUIRE(act_dtype == GDN_F32 || act_dtype == GDN_BF16,
                 "gdn_decode_step: activations must be float32 or bfloat16");
@@ -266,10 +269,16 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
     GDN_REQUIRE(!z || norm_weight, "gdn_decode_step: z without norm_weight");
     if (!slots) pool = B;
     GDN_REQUIRE(pool >= 1, "gdn_decode_step: bad pool size %d", pool);
+    GDN_REQUIRE(!conv_rows || slots, "gdn_decode_step: conv_rows needs slots");
+    GDN_REQUIRE(!conv_rows || conv_pool >= 1, "gdn_decode_step: bad conv row count %d", conv_pool);
     const int64_t C = 2LL * Hk * kD + int64_t(Hv) * kD;
     const int64_t row_bytes = (kTaps - 1) * C * dtype_size(act_dtype);
-    GDN_REQUIRE(!overlaps(conv_state_in, int64_t(pool) * row_bytes, conv_state_out, int64_t(B) * row_bytes),
-                "gdn_decode_step: conv_state_out overlaps conv_state_in");
+    // with conv_rows the in and out rows may share one array (the caller
+    // keeps them disjoint); otherwise the two arrays must not overlap
+    if (!conv_rows)
+        GDN_REQUIRE(!overlaps(conv_state_in, int64_t(pool) * row_bytes, conv_state_out, int64_t(B) * row_bytes),
+                    "gdn_decode_step: conv_state_out overlaps conv_state_in");
+    const int rows_bound = conv_rows ? conv_pool : (pool > B ? pool : B);
     const int64_t state_bytes = int64_t(pool) * Hv * kD * kD * 4;
     GDN_REQUIRE(state_in == state_out || !overlaps(state_in, state_bytes, state_out, state_bytes),
                 "gdn_decode_step: state_out partially overlaps state_in");
@@ -285,7 +294,7 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                        static_cast<ACT::storage*>(conv_state_out), conv_weight,               \
                        static_cast<const ACT::storage*>(a), static_cast<const ACT::storage*>(b), \
                        A_log, dt_bias, state_in, state_out, static_cast<const ACT::storage*>(z), \
-                       norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool)
+                       norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool, conv_rows, rows_bound)
     if (act_dtype == GDN_BF16) {
         if (z) GDN_DECODE_LAUNCH(ActBF16, true); else GDN_DECODE_LAUNCH(ActBF16, false);
     } else {

@@ -109,9 +109,25 @@ def check_slots(slots, batch: int, pool: int) -> list[int]:
     return slots
 
 
+def check_conv_rows(conv_rows, batch: int, rows: int) -> list[int]:
+    """Host-side check of per-row (in, out) conv rows: ``2 batch`` integers
+    in ``[0, rows)``, the out rows distinct and none of them an in row (a
+    row read by one batch row must not be overwritten by another)."""
+
+    conv_rows = [int(v) for v in conv_rows]
+    if len(conv_rows) != 2 * batch:
+        raise ValueError(f"expected {2 * batch} conv rows, got {len(conv_rows)}")
+    if any(v < 0 or v >= rows for v in conv_rows):
+        raise ValueError(f"conv rows must lie in [0, {rows})")
+    ins, outs = conv_rows[0::2], conv_rows[1::2]
+    if len(set(outs)) != len(outs) or set(outs) & set(ins):
+        raise ValueError("conv out rows must be distinct and disjoint from the in rows")
+    return conv_rows
+
+
 def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias,
                       norm_weight, eps, dims: LinearAttentionDims, *, conv_out=None,
-                      state_out=None, y_dtype=None, slots=None):
+                      state_out=None, y_dtype=None, slots=None, conv_rows=None):
     """One decode token for ``B`` sequences in a single kernel launch: conv +
     SiLU + roll, q/k scaling, gates, recurrence and gated RMSNorm
     (linear_attention.py:103-124 at L = 1).
@@ -128,7 +144,10 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     ``(P, Hv, Dv, Dk)``: row ``b`` reads its conv state at ``slots[b]`` and
     updates the state tiles of ``slots[b]`` in place (``state_out`` must be
     ``ssm_state`` or None); ``conv_out`` is ``(B, K-1, C)`` with the rolled
-    rows in batch order, for the caller to put back at the slots.
+    rows in batch order, for the caller to put back at the slots. With
+    ``conv_rows`` as well (``2 B`` row indices: where row ``b`` reads its conv
+    state in ``conv_state`` and writes the rolled one in ``conv_out``, which
+    may be the same ``(R, K-1, C)`` array), nothing is left to copy back.
     Returns ``(out (B, Hv, Dv), conv_out, state_out)``."""
 
     device = _require_device(qkv, z, a, b, conv_state, ssm_state)
@@ -144,9 +163,17 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
         if state_out is not None and state_out is not ssm_state:
             raise ValueError("with slots the state is updated in place (state_out=ssm_state)")
         state_out = ssm_state
+    conv_in_rows = P
+    if conv_rows is not None:
+        if slots is None or conv_out is None:
+            raise ValueError("conv_rows needs slots and an explicit conv_out")
+        conv_in_rows = conv_state.shape[0]
+        if conv_out.shape[0] != conv_in_rows:
+            raise ValueError("conv_state and conv_out must have the same number of rows")
+        row_list = check_conv_rows(conv_rows, B, conv_in_rows)
     if (tuple(qkv.shape) != (B, dims.conv_dim) or tuple(a.shape) != (B, dims.num_value_heads)
             or b.shape != a.shape
-            or tuple(conv_state.shape) != (P, dims.conv_kernel_dim - 1, dims.conv_dim)
+            or tuple(conv_state.shape) != (conv_in_rows, dims.conv_kernel_dim - 1, dims.conv_dim)
             or tuple(ssm_state.shape) != (P, dims.num_value_heads, dims.value_head_dim,
                                            dims.key_head_dim)
             or (z is not None and tuple(z.shape) != (B, dims.num_value_heads, dims.value_head_dim))):
@@ -162,12 +189,17 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     norm_weight = _c(norm_weight.float()) if z is not None else None
     if conv_out is None:
         conv_out = torch.empty((B,) + tuple(conv_state.shape[1:]), dtype=act, device=device)
-    elif tuple(conv_out.shape) != (B, dims.conv_kernel_dim - 1, dims.conv_dim) or conv_out.dtype != act:
-        raise ValueError("conv_out must be (B, K-1, C) in the activation dtype")
+    elif (tuple(conv_out.shape[1:]) != (dims.conv_kernel_dim - 1, dims.conv_dim) or conv_out.dtype != act
+          or not conv_out.is_contiguous()
+          or (conv_rows is None and conv_out.shape[0] != B)):
+        raise ValueError("conv_out must be contiguous (B, K-1, C) in the activation dtype "
+                         "(or conv_state's rows with conv_rows)")
     if state_out is None:
         state_out = torch.empty_like(ssm_state)
     slot_t = (torch.tensor(slot_list, dtype=torch.int32, device=device)
               if slots is not None else None)
+    rows_t = (torch.tensor(row_list, dtype=torch.int32, device=device)
+              if conv_rows is not None else None)
     out_dtype = act if z is not None else (y_dtype or torch.float32)
     out = torch.empty((B, dims.num_value_heads, dims.value_head_dim), dtype=out_dtype,
                       device=device)
@@ -176,7 +208,8 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
               _lib.ptr(dt_bias), _lib.ptr(ssm_state), _lib.ptr(state_out), _lib.ptr(z),
               _lib.ptr(norm_weight), float(eps), _lib.ptr(out), _lib.dtype_code(out_dtype), B,
               dims.num_key_heads, dims.num_value_heads, dims.key_head_dim, dims.value_head_dim,
-              dims.conv_kernel_dim, _lib.dtype_code(act), _lib.ptr(slot_t), P, _stream(device))
+              dims.conv_kernel_dim, _lib.dtype_code(act), _lib.ptr(slot_t), P, _lib.ptr(rows_t),
+              conv_in_rows, _stream(device))
     return out, conv_out, state_out
 
 
@@ -312,9 +345,9 @@ class Qwen3_5LinearAttention:
         """One decode token for each of the pool's sequences: ``x (pool.batch,
         hidden)`` -> ``(pool.batch, hidden)``; or, with ``slots`` (distinct
         pool indices, e.g. the sequences a scheduler has active this step),
-        ``x (len(slots), hidden)`` for those slots only. The ssm slots are
-        updated in place by the kernel; the conv state is double-buffered
-        without slots and copied back to the slots with them."""
+        ``x (len(slots), hidden)`` for those slots only. One kernel launch
+        updates the slots' ssm tiles in place and rolls their conv state into
+        the other half of the pool's conv buffer."""
 
         d = self.linear
         rows = pool.batch if slots is None else len(slots)
@@ -322,20 +355,13 @@ class Qwen3_5LinearAttention:
             raise ValueError("decode_batch expects x of shape (pool.batch, hidden), or "
                              "(len(slots), hidden) with slots")
         qkv, z, a, b = self._project(x)
-        if not _fused_decode_ok(d, qkv.dtype) or pool.conv_state.dtype != qkv.dtype:
+        if not _fused_decode_ok(d, qkv.dtype) or pool.conv_buf.dtype != qkv.dtype:
             raise ValueError("decode_batch needs Dk = Dv = 128, K = 4 and a pool in the "
                              "activation dtype (float32 or bfloat16)")
-        if slots is None:
-            out, _, _ = self._decode_fused(qkv, z, a, b, pool.conv_state, pool.ssm_state,
-                                           in_place=True, conv_out=pool.conv_spare)
-            pool.swap_conv()
-            pool.size += 1
-        else:
-            slot_list = check_slots(slots, rows, pool.batch)
-            out, conv_out, _ = fused_decode_step(
-                qkv, z, a, b, pool.conv_state, pool.ssm_state, self.conv1d_weight, self.A_log,
-                self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_list)
-            index = torch.tensor(slot_list, dtype=torch.int64, device=pool.conv_state.device)
-            pool.conv_state.index_copy_(0, index, conv_out)
-            pool.size[torch.tensor(slot_list, dtype=torch.int64)] += 1
+        slot_list = list(range(rows)) if slots is None else check_slots(slots, rows, pool.batch)
+        out, _, _ = fused_decode_step(
+            qkv, z, a, b, pool.conv_buf, pool.ssm_state, self.conv1d_weight, self.A_log,
+            self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_list,
+            conv_rows=pool.conv_rows(slot_list), conv_out=pool.conv_buf)
+        pool.advance(slot_list)
         return self._proj(out.reshape(rows, d.value_dim), self.out_proj)

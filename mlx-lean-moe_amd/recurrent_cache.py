@@ -37,19 +37,22 @@ class RecurrentCache:
 
 
 class RecurrentStatePool:
-    """``B`` sequences' states for batched decode: conv ``(B, K-1, C)`` in the
-    activation dtype and ssm ``(B, Hv, Dv, Dk)`` float32.
+    """``B`` sequences' states for batched decode: ssm ``(B, Hv, Dv, Dk)``
+    float32 and conv ``(K-1, C)`` per slot in the activation dtype.
 
-    The decode kernel reads the ssm slots and writes them back in place; the
-    conv state is double-buffered (``conv_state`` / ``conv_spare``) because a
-    key head's conv channels are read by several workgroups."""
+    The decode kernel updates a slot's ssm tiles in place. A key head's conv
+    channels are read by several workgroups, so a slot's conv state cannot
+    be rolled in place: ``conv_buf`` holds two ``(B, K-1, C)`` halves and
+    slot ``s`` currently lives in row ``s + B * conv_half[s]``; a decode reads
+    that row and writes the rolled state into the slot's other half, then
+    the slot's half flips (no copy, and slots decode independently)."""
 
     def __init__(self, batch: int, conv_kernel_dim: int, conv_dim: int, num_value_heads: int,
                  value_head_dim: int, key_head_dim: int, dtype: torch.dtype = torch.bfloat16,
                  device: torch.device | str = "cuda") -> None:
-        shape = (batch, conv_kernel_dim - 1, conv_dim)
-        self.conv_state = torch.zeros(shape, dtype=dtype, device=device)
-        self.conv_spare = torch.zeros(shape, dtype=dtype, device=device)
+        self.conv_buf = torch.zeros((2 * batch, conv_kernel_dim - 1, conv_dim), dtype=dtype,
+                                    device=device)
+        self.conv_half = torch.zeros(batch, dtype=torch.int64)
         self.ssm_state = torch.zeros((batch, num_value_heads, value_head_dim, key_head_dim),
                                      dtype=torch.float32, device=device)
         self.size = torch.zeros(batch, dtype=torch.int64)
@@ -58,16 +61,35 @@ class RecurrentStatePool:
     def batch(self) -> int:
         return self.ssm_state.shape[0]
 
+    def _current_rows(self) -> torch.Tensor:
+        return torch.arange(self.batch) + self.batch * self.conv_half
+
+    @property
+    def conv_state(self) -> torch.Tensor:
+        """Every slot's current conv state ``(B, K-1, C)`` (a gathered copy)."""
+        return self.conv_buf[self._current_rows().to(self.conv_buf.device)]
+
     def state(self) -> tuple[torch.Tensor, torch.Tensor]:
         return self.conv_state, self.ssm_state
 
-    def swap_conv(self) -> None:
-        """Make the freshly written spare conv buffer current."""
-        self.conv_state, self.conv_spare = self.conv_spare, self.conv_state
+    def conv_rows(self, slots: list[int]) -> list[int]:
+        """(current row, other row) of each slot's conv state, flattened."""
+        rows = []
+        for s in slots:
+            h = int(self.conv_half[s])
+            rows += [s + self.batch * h, s + self.batch * (1 - h)]
+        return rows
+
+    def advance(self, slots: list[int]) -> None:
+        """After a decode of ``slots``: their conv state now lives in the
+        other half, and each holds one more token."""
+        idx = torch.tensor(slots, dtype=torch.int64)
+        self.conv_half[idx] ^= 1
+        self.size[idx] += 1
 
     def load(self, slot: int, cache: RecurrentCache) -> None:
         """Copy one sequence's state (e.g. after its prefill) into ``slot``."""
         conv, ssm = cache.state()
-        self.conv_state[slot].copy_(conv)
+        self.conv_buf[slot + self.batch * int(self.conv_half[slot])].copy_(conv)
         self.ssm_state[slot].copy_(ssm)
         self.size[slot] = cache.size

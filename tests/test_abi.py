@@ -53,7 +53,8 @@ def test_invalid_arguments_return_einval_without_launching():
                                 ctypes.c_void_p(16), 0, None, 0, None, 3, 4, 1, 1, 32, 8, None)
     assert rc == _lib.GDN_EINVAL and "divisible" in _err(lib)
     # the fused decode kernel is specialised for Dk = Dv = 128
-    rc = lib.gdn_decode_step(*([None] * 12), 1e-6, None, 0, 1, 2, 4, 64, 64, 4, 1, None, 0, None)
+    rc = lib.gdn_decode_step(*([None] * 12), 1e-6, None, 0, 1, 2, 4, 64, 64, 4, 1, None, 0, None, 0,
+                             None)
     assert rc == _lib.GDN_EUNSUPPORTED
     # overlapping conv state buffers are rejected
     p = ctypes.c_void_p(4096)

@@ -59,6 +59,41 @@ def test_slot_decode_equals_decode_of_gathered_sequences(gpu, act, with_z):
     assert torch.equal(c["conv"], conv_before)  # the pool's conv rows are the caller's to update
 
 
+def test_conv_rows_roll_into_the_other_half_without_a_copy(gpu):
+    """Conv state in the two halves of one array: each row reads its slot's
+    current row and writes the other; untouched rows keep their bytes."""
+
+    P, slots = 6, [4, 1]
+    c = _pool_case(13, P, len(slots), torch.bfloat16, gpu)
+    buf = torch.cat([c["conv"], torch.zeros_like(c["conv"])])  # slot s in row s (half 0)
+    buf[P + 1] = c["conv"][1]  # slot 1 currently in half 1: row 7 (row 1 is stale)
+    buf[1].fill_(3.0)
+    half = {4: 0, 1: 1}
+    rows = []
+    for s_ in slots:
+        rows += [s_ + P * half[s_], s_ + P * (1 - half[s_])]
+    idx = torch.tensor(slots, device=gpu)
+    ref_out, ref_conv, ref_state = gdn.fused_decode_step(
+        c["qkv"], c["z"], c["a"], c["b"], c["conv"][idx].clone(), c["state"][idx].clone(),
+        c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS)
+    before = buf.clone()
+    out, _, _ = gdn.fused_decode_step(
+        c["qkv"], c["z"], c["a"], c["b"], buf, c["state"], c["conv_w"], c["A_log"], c["dt_bias"],
+        c["norm_w"], 1e-6, DIMS, slots=slots, conv_rows=rows, conv_out=buf)
+    assert torch.equal(out, ref_out)
+    assert torch.equal(buf[rows[1]], ref_conv[0]) and torch.equal(buf[rows[3]], ref_conv[1])
+    assert torch.equal(c["state"][idx], ref_state)
+    written = {rows[1], rows[3]}
+    for r in range(2 * P):
+        if r not in written:
+            assert torch.equal(buf[r], before[r]), r
+    for bad in ([4, 4, 7, 1], [4, 10, 7, 4], [4, 12, 7, 1]):  # out rows shared, out = an in row, range
+        with pytest.raises(ValueError):
+            gdn.fused_decode_step(c["qkv"], c["z"], c["a"], c["b"], buf, c["state"], c["conv_w"],
+                                  c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS, slots=slots,
+                                  conv_rows=bad, conv_out=buf)
+
+
 def test_slot_outside_pool_touches_no_state(gpu):
     """The C ABI's own guard (the Python layer rejects such slots first): a
     row whose slot lies outside the pool writes NaN and leaves the state."""
@@ -73,7 +108,7 @@ def test_slot_outside_pool_touches_no_state(gpu):
               _lib.ptr(c["conv_w"].reshape(DIMS.conv_dim, 4).contiguous()), _lib.ptr(c["a"]),
               _lib.ptr(c["b"]), _lib.ptr(c["A_log"]), _lib.ptr(c["dt_bias"]), _lib.ptr(c["state"]),
               _lib.ptr(c["state"]), None, None, 1e-6, _lib.ptr(out), _lib.GDN_F32, B, 2, 4, 128,
-              128, 4, _lib.GDN_BF16, _lib.ptr(slots), P, _lib.stream_ptr(gpu))
+              128, 4, _lib.GDN_BF16, _lib.ptr(slots), P, None, 0, _lib.stream_ptr(gpu))
     torch.cuda.synchronize()
     assert torch.isnan(out[0]).all() and torch.isfinite(out[1]).all()
     assert torch.equal(c["state"][0], before[0]) and torch.equal(c["state"][2:], before[2:])

@@ -111,16 +111,17 @@ def test_layer_varlen_prefill_then_fused_decode(gpu):
         ssm_ref.append(ns)
 
     pool = gdn.RecurrentStatePool(N, 4, C, 4, 128, 128, dtype=torch.bfloat16, device=gpu)
-    pool.conv_state.copy_(conv)
+    pool.conv_buf[:N].copy_(conv)  # every slot starts in the first half
     pool.ssm_state.copy_(ssm)
+    slots = list(range(N))
     for _ in range(8):
         x_qkv, x_z, x_a, x_b = layer_inputs(rng, dt, L=1, act_bf16=True, B=N)
         o_dev, _, _ = gdn.fused_decode_step(bf(x_qkv[:, 0]), bf(x_z[:, 0]), bf(x_a[:, 0]),
-                                            bf(x_b[:, 0]), pool.conv_state, pool.ssm_state,
+                                            bf(x_b[:, 0]), pool.conv_buf, pool.ssm_state,
                                             layer.conv1d_weight, layer.A_log, layer.dt_bias,
-                                            layer.norm_weight, 1e-6, dims,
-                                            conv_out=pool.conv_spare, state_out=pool.ssm_state)
-        pool.swap_conv()
+                                            layer.norm_weight, 1e-6, dims, slots=slots,
+                                            conv_rows=pool.conv_rows(slots), conv_out=pool.conv_buf)
+        pool.advance(slots)
         for i in range(N):
             o, conv_ref[i], ssm_ref[i] = R.linear_attention_core(
                 x_qkv[i], x_z[i], x_a[i], x_b[i], conv_ref[i], ssm_ref[i], conv_w, A_log,
