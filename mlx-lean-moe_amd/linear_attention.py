@@ -125,6 +125,17 @@ def check_conv_rows(conv_rows, batch: int, rows: int) -> list[int]:
     return conv_rows
 
 
+def _index_array(values, n: int, device, check, name: str) -> torch.Tensor:
+    """A kernel index array: an int32 device tensor of ``n`` entries is used
+    as given; anything else is checked on the host and copied."""
+
+    if isinstance(values, torch.Tensor) and values.device.type == "cuda":
+        if values.dtype != torch.int32 or values.shape != (n,) or not values.is_contiguous():
+            raise ValueError(f"{name} on the device must be a contiguous int32 tensor of {n} entries")
+        return values
+    return torch.tensor(check(values), dtype=torch.int32, device=device)
+
+
 def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias,
                       norm_weight, eps, dims: LinearAttentionDims, *, conv_out=None,
                       state_out=None, y_dtype=None, slots=None, conv_rows=None):
@@ -148,6 +159,10 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     ``conv_rows`` as well (``2 B`` row indices: where row ``b`` reads its conv
     state in ``conv_state`` and writes the rolled one in ``conv_out``, which
     may be the same ``(R, K-1, C)`` array), nothing is left to copy back.
+    ``slots`` and ``conv_rows`` given as host sequences are checked on the
+    host; given as int32 device tensors they are used as they are (no host
+    round trip), and the caller guarantees they are distinct and disjoint as
+    required — the kernel itself still refuses indices outside the arrays.
     Returns ``(out (B, Hv, Dv), conv_out, state_out)``."""
 
     device = _require_device(qkv, z, a, b, conv_state, ssm_state)
@@ -157,9 +172,10 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
         raise ValueError("the fused decode kernel needs Dk = Dv = 128, K = 4 and float32 or "
                          "bfloat16 activations")
     P = B
+    slot_t = rows_t = None
     if slots is not None:
         P = ssm_state.shape[0]
-        slot_list = check_slots(slots, B, P)
+        slot_t = _index_array(slots, B, device, lambda v: check_slots(v, B, P), "slots")
         if state_out is not None and state_out is not ssm_state:
             raise ValueError("with slots the state is updated in place (state_out=ssm_state)")
         state_out = ssm_state
@@ -170,7 +186,8 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
         conv_in_rows = conv_state.shape[0]
         if conv_out.shape[0] != conv_in_rows:
             raise ValueError("conv_state and conv_out must have the same number of rows")
-        row_list = check_conv_rows(conv_rows, B, conv_in_rows)
+        rows_t = _index_array(conv_rows, 2 * B, device,
+                              lambda v: check_conv_rows(v, B, conv_in_rows), "conv_rows")
     if (tuple(qkv.shape) != (B, dims.conv_dim) or tuple(a.shape) != (B, dims.num_value_heads)
             or b.shape != a.shape
             or tuple(conv_state.shape) != (conv_in_rows, dims.conv_kernel_dim - 1, dims.conv_dim)
@@ -196,10 +213,6 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
                          "(or conv_state's rows with conv_rows)")
     if state_out is None:
         state_out = torch.empty_like(ssm_state)
-    slot_t = (torch.tensor(slot_list, dtype=torch.int32, device=device)
-              if slots is not None else None)
-    rows_t = (torch.tensor(row_list, dtype=torch.int32, device=device)
-              if conv_rows is not None else None)
     out_dtype = act if z is not None else (y_dtype or torch.float32)
     out = torch.empty((B, dims.num_value_heads, dims.value_head_dim), dtype=out_dtype,
                       device=device)
@@ -359,9 +372,10 @@ class Qwen3_5LinearAttention:
             raise ValueError("decode_batch needs Dk = Dv = 128, K = 4 and a pool in the "
                              "activation dtype (float32 or bfloat16)")
         slot_list = list(range(rows)) if slots is None else check_slots(slots, rows, pool.batch)
+        slot_t = pool.device_slots(slot_list)
         out, _, _ = fused_decode_step(
             qkv, z, a, b, pool.conv_buf, pool.ssm_state, self.conv1d_weight, self.A_log,
-            self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_list,
-            conv_rows=pool.conv_rows(slot_list), conv_out=pool.conv_buf)
-        pool.advance(slot_list)
+            self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_t,
+            conv_rows=pool.device_conv_rows(slot_t), conv_out=pool.conv_buf)
+        pool.advance(slot_list, slot_t)
         return self._proj(out.reshape(rows, d.value_dim), self.out_proj)

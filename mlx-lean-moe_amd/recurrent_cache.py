@@ -53,6 +53,10 @@ class RecurrentStatePool:
         self.conv_buf = torch.zeros((2 * batch, conv_kernel_dim - 1, conv_dim), dtype=dtype,
                                     device=device)
         self.conv_half = torch.zeros(batch, dtype=torch.int64)
+        # the same bits on the device, so a decode step's conv rows are
+        # computed without a host round trip
+        self._half_dev = torch.zeros(batch, dtype=torch.int32, device=device)
+        self._slot_sets: dict[tuple[int, ...], torch.Tensor] = {}
         self.ssm_state = torch.zeros((batch, num_value_heads, value_head_dim, key_head_dim),
                                      dtype=torch.float32, device=device)
         self.size = torch.zeros(batch, dtype=torch.int64)
@@ -80,12 +84,31 @@ class RecurrentStatePool:
             rows += [s + self.batch * h, s + self.batch * (1 - h)]
         return rows
 
-    def advance(self, slots: list[int]) -> None:
+    def device_slots(self, slots: list[int]) -> torch.Tensor:
+        """``slots`` as an int32 device array, kept per active set (a serving
+        loop decodes the same set for many steps), copied without blocking."""
+        key = tuple(slots)
+        t = self._slot_sets.get(key)
+        if t is None:
+            if len(self._slot_sets) >= 64:
+                self._slot_sets.clear()
+            host = torch.tensor(key, dtype=torch.int32).pin_memory()
+            t = self._slot_sets[key] = host.to(self.ssm_state.device, non_blocking=True)
+        return t
+
+    def device_conv_rows(self, slot_t: torch.Tensor) -> torch.Tensor:
+        """conv_rows for an int32 device array of slots, on the device."""
+        h = self._half_dev[slot_t.long()]
+        return torch.stack([slot_t + self.batch * h, slot_t + self.batch * (1 - h)], 1).reshape(-1)
+
+    def advance(self, slots: list[int], slot_t: torch.Tensor | None = None) -> None:
         """After a decode of ``slots``: their conv state now lives in the
         other half, and each holds one more token."""
         idx = torch.tensor(slots, dtype=torch.int64)
         self.conv_half[idx] ^= 1
         self.size[idx] += 1
+        dev_idx = slot_t.long() if slot_t is not None else idx.to(self._half_dev.device)
+        self._half_dev[dev_idx] ^= 1
 
     def load(self, slot: int, cache: RecurrentCache) -> None:
         """Copy one sequence's state (e.g. after its prefill) into ``slot``."""
