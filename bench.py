@@ -324,14 +324,23 @@ class QLinearWorkload:
             raise RuntimeError(f"gdn_quantized_matmul failed with {rc}")
 
 
-def bench_qlinear(dev, M, steps, warmup, rotate=True):
+def bench_qlinear(dev, M, steps, warmup, rotate=True, layer_path=False):
     w = QLinearWorkload(dev, M, rotate=rotate)
     total_ms, isolated_ms = time_steps(w.step, steps, warmup)
     ms = total_ms / steps
-    return {"kernel_us": ms * 1e3, "isolated_launch_us": isolated_ms * 1e3,
-            "hbm_gbs": w.bytes / (ms * 1e-3) / 1e9, "tflops": w.flops / (ms * 1e-3) / 1e12,
-            "bytes_per_launch": w.bytes, "flops_per_launch": w.flops,
-            "tokens_per_s": M / (ms * 1e-3)}
+    r = {"kernel_us": ms * 1e3, "isolated_launch_us": isolated_ms * 1e3,
+         "hbm_gbs": w.bytes / (ms * 1e-3) / 1e9, "tflops": w.flops / (ms * 1e-3) / 1e12,
+         "bytes_per_launch": w.bytes, "flops_per_launch": w.flops,
+         "tokens_per_s": M / (ms * 1e-3)}
+    if layer_path:
+        # what the layer runs at this size: quantized_linear (dequantize to
+        # bf16 + vendor BLAS from 512 rows on)
+        wt, sc, bi = w.weights[0]
+        tensors, q = {"weight": wt, "scales": sc, "biases": bi}, gdn.QuantScheme(4, 64)
+        lm, _ = time_steps(lambda s: gdn.quantized_linear(w.x, tensors, q), steps, warmup)
+        r["layer_path_us"] = lm / steps * 1e3
+        r["layer_path_tflops"] = w.flops / (lm / steps * 1e-3) / 1e12
+    return r
 
 
 VARLEN_LENS = np.random.default_rng(0).integers(128, 8193, 16)  # 16 runs, 67,128 tokens
@@ -578,7 +587,8 @@ def main(argv=None):
     if args.workload == "qlinear":
         dec = bench_qlinear(dev, 64, args.steps, args.warmup)
         pre = (None if args.no_also else
-               bench_qlinear(dev, 4096, max(args.steps // 4, 5), args.warmup, rotate=False))
+               bench_qlinear(dev, 4096, max(args.steps // 4, 5), args.warmup, rotate=False,
+                             layer_path=True))
         print(json.dumps({
             "metric": "4-bit affine quantized input projection (hidden 2048 -> qkv|z|a|b 12352)",
             "value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -597,7 +607,9 @@ def main(argv=None):
             "also": {} if pre is None else {"prefill_m4096": {
                 "kernel_us": pre["kernel_us"], "tflops": pre["tflops"],
                 "mfma_frac": pre["tflops"] / BF16_PEAK_TFLOPS,
-                "flops_per_launch": pre["flops_per_launch"]}}}))
+                "flops_per_launch": pre["flops_per_launch"],
+                "layer_path_us": pre["layer_path_us"],
+                "layer_path_mfma_frac": pre["layer_path_tflops"] / BF16_PEAK_TFLOPS}}}))
         return 0
 
     if args.workload in ("prefill", "prefill_varlen"):

@@ -59,6 +59,7 @@ def _decode_kernel_takes(M, K, bits, gs, sb):
     (2, 78, 512, 4, 64, "bf16"),        # decode kernel, one step, last block partial
     (17, 130, 2048, 8, 64, "f16"),      # decode kernel, 8-bit codes, 64-k slices
     (48, 96, 1024, 4, 128, "f32"),      # decode kernel, two slices per group
+    (600, 256, 512, 4, 64, "bf16"),     # quantized_linear: dequantize + BLAS; the ABI: tiled kernel
 ])
 def test_quantized_matmul_matches_oracle(gpu, M, N, K, bits, gs, sb):
     rng = np.random.default_rng(M + N + K)
