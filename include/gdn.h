@@ -194,7 +194,9 @@ int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, co
 /*
  * gdn_quantized_matmul - y = x W^T for an affine-quantized W in MLX's packing,
  * on bf16 MFMA with float32 accumulation.
- *   x: (M, K) bfloat16 (other dtypes: GDN_EUNSUPPORTED, see gdn_dequantize)
+ *   x: (M, K) bfloat16; or float32 with M <= 32 on the decode kernel's shapes,
+ *      staged as bf16 hi + lo (~16 significant bits; other cases:
+ *      GDN_EUNSUPPORTED, see gdn_dequantize)
  *   w: (N, K * bits / 32) uint32, element k of row n at bits [bits * (k % (32 / bits)), +bits)
  *      of word k / (32 / bits), least significant first; 16-byte aligned
  *   scales, biases: (N, K / group_size) sb_dtype; w[n][k] = scales[n][g] * q + biases[n][g]

@@ -15,6 +15,8 @@
 // weights mx.dequantize yields) next to a BM x 64 tile of x; fp32
 // accumulation. Loads of step s + 1 are issued before step s's MFMAs.
 // gdn_dequantize: the dense weights, for dtypes the MFMA kernel does not take.
+#include <type_traits>
+
 #include "gdn_common.h"
 #include "gdn_host.h"
 
@@ -221,9 +223,9 @@ GDN_DEV bf16x8 code_fragment(const uint32_t* words, CodeConsts k) {
     }
 }
 
-template <int kBits, int kSteps, int kMT, int kSlice, int kCols>
+template <int kBits, int kSteps, int kMT, int kSlice, int kCols, bool kXF32>
 __global__ __launch_bounds__(512) void qlinear_decode_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w, const void* __restrict__ scales,
+    const void* __restrict__ xp, const uint32_t* __restrict__ w, const void* __restrict__ scales,
     const void* __restrict__ biases, int sb_dtype, void* __restrict__ y, int y_dtype, int M, int N, int K,
     int group_size) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -236,7 +238,11 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     constexpr int kWS = kWPC + 4;                // word row stride of the weight tile
     constexpr int kXLoads = kRows * kStep / 8 / 512;   // 16-byte x chunks per thread per step
     constexpr int kWLoads = kCols * kWPC / 4 / 512;    // 16-byte weight pieces per thread per step
-    constexpr int kXBytes = kRows * kXS * 2;
+    // float32 x is staged as two bf16 tiles, hi = bf16(x) and lo =
+    // bf16(x - hi) (together x to ~16 significant bits), each fragment
+    // taking two MFMAs into the same accumulator
+    constexpr int kXParts = kXF32 ? 2 : 1;
+    constexpr int kXBytes = kXParts * kRows * kXS * 2;
     constexpr int kWBytes = kCols * kWS * 4;
     constexpr int kPBytes = 4 * kMT * kTN * 64 * 16;  // 4 partial blocks of kMT x kTN tiles of float4 per lane
     constexpr int kSBRow = kCols * (kDecGroups + 1);
@@ -249,7 +255,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     static_assert(kXLoads >= 1 && kWLoads >= 1, "step too small for 512 threads");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kMain];
     __shared__ float sbs[2 * kSBRow];
-    auto xs = [&](int buf) { return reinterpret_cast<uint16_t*>(lds + buf * kXBytes); };              // [kRows][kXS]
+    auto xs = [&](int buf) { return reinterpret_cast<uint16_t*>(lds + buf * kXBytes); };  // [kXParts][kRows][kXS]
     auto ws = [&](int buf) { return reinterpret_cast<uint32_t*>(lds + kBufs * kXBytes + buf * kWBytes); };  // [kCols][kWS]
     f32x4* part = reinterpret_cast<f32x4*>(lds);  // [4][kMT][kTN][64] after the steps
 
@@ -282,22 +288,42 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
 
     // x chunk p = tid + 512 i of a step: row p / (kStep / 8) (clamped to
     // M - 1), k 8 (p % (kStep / 8)) .. +7
-    u16x8 xv[kXLoads];
+    typedef float f32x8 __attribute__((ext_vector_type(8)));
+    using xchunk_t = std::conditional_t<kXF32, f32x8, u16x8>;
+    using xelem_t = std::conditional_t<kXF32, float, uint16_t>;
+    const xelem_t* x = static_cast<const xelem_t*>(xp);
+    xchunk_t xv[kXLoads];
     auto fetch_x = [&](int s) {
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
             const int p = tid + 512 * i, r = p / (kStep / 8), ch = p % (kStep / 8);
             const int row = r < M ? r : M - 1;
-            xv[i] = *reinterpret_cast<const u16x8*>(x + int64_t(row) * K + kStep * s + 8 * ch);
+            xv[i] = *reinterpret_cast<const xchunk_t*>(x + int64_t(row) * K + kStep * s + 8 * ch);
         }
+    };
+    // 4-bit fragments pair codes i and i + 4 of a word: stage each chunk in
+    // that order
+    auto order = [&](u16x8 v) {
+        if constexpr (kBits == 4) return u16x8(__builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7));
+        else return v;
     };
     auto stage_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
             const int p = tid + 512 * i, r = p / (kStep / 8), ch = p % (kStep / 8);
-            u16x8 o = xv[i];
-            if constexpr (kBits == 4) o = __builtin_shufflevector(xv[i], xv[i], 0, 4, 1, 5, 2, 6, 3, 7);
-            *reinterpret_cast<u16x8*>(&xs(buf)[r * kXS + 8 * ch]) = o;
+            uint16_t* dst = &xs(buf)[r * kXS + 8 * ch];
+            if constexpr (kXF32) {
+                bf16x8 hi, lo;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    hi[j] = static_cast<__bf16>(xv[i][j]);
+                    lo[j] = static_cast<__bf16>(xv[i][j] - static_cast<float>(hi[j]));
+                }
+                *reinterpret_cast<u16x8*>(dst) = order(__builtin_bit_cast(u16x8, hi));
+                *reinterpret_cast<u16x8*>(dst + kRows * kXS) = order(__builtin_bit_cast(u16x8, lo));
+            } else {
+                *reinterpret_cast<u16x8*>(dst) = order(xv[i]);
+            }
         }
     };
     fetch_x(0);
@@ -357,15 +383,19 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         const uint16_t* xb = xs(buf);
         const uint32_t* wb = ws(buf);
         const int g = (kStep * s + kSlice * wv) / group_size;
-        bf16x8 a[kMT][kKB];
+        bf16x8 a[kXParts][kMT][kKB];
         f32x4 X[kMT];
 #pragma unroll
         for (int tm = 0; tm < kMT; ++tm) {
+            X[tm] = zero;
 #pragma unroll
-            for (int kb = 0; kb < kKB; ++kb)
-                a[tm][kb] = *reinterpret_cast<const bf16x8*>(&xb[(16 * tm + lr) * kXS + kSlice * wv + 32 * kb + 8 * lq]);
-            X[tm] = mfma_bf16(a[tm][0], ones, zero);
-            if constexpr (kKB == 2) X[tm] = mfma_bf16(a[tm][1], ones, X[tm]);
+            for (int h = 0; h < kXParts; ++h)
+#pragma unroll
+                for (int kb = 0; kb < kKB; ++kb) {
+                    a[h][tm][kb] = *reinterpret_cast<const bf16x8*>(
+                        &xb[(h * kRows + 16 * tm + lr) * kXS + kSlice * wv + 32 * kb + 8 * lq]);
+                    X[tm] = mfma_bf16(a[h][tm][kb], ones, X[tm]);
+                }
         }
 #pragma unroll
         for (int tn = 0; tn < kTN; ++tn) {
@@ -378,8 +408,11 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
                 bq[kb] = code_fragment<kBits>(&wb[c * kWS + (kSlice * wv + 32 * kb + 8 * lq) * kBits / 32], kc);
 #pragma unroll
             for (int tm = 0; tm < kMT; ++tm) {
-                f32x4 P = mfma_bf16(a[tm][0], bq[0], zero);
-                if constexpr (kKB == 2) P = mfma_bf16(a[tm][1], bq[1], P);
+                f32x4 P = zero;
+#pragma unroll
+                for (int h = 0; h < kXParts; ++h)
+#pragma unroll
+                    for (int kb = 0; kb < kKB; ++kb) P = mfma_bf16(a[h][tm][kb], bq[kb], P);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     acc[tm][tn][i] = __builtin_fmaf(cb, X[tm][i], __builtin_fmaf(sp, P[i], acc[tm][tn][i]));
@@ -460,14 +493,13 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         store([&](int64_t i, float v) { static_cast<float*>(y)[i] = v; });
 }
 
-template <int kBits, int kMT, int kSlice, int kCols>
+template <int kBits, int kMT, int kSlice, int kCols, bool kXF32>
 int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
                      void* y, int y_dtype, int M, int N, int K, int group_size, hipStream_t s) {
     const dim3 grid(unsigned((N + kCols - 1) / kCols));
 #define GDN_DEC(STEPS)                                                                              \
-    hipLaunchKernelGGL((qlinear_decode_kernel<kBits, STEPS, kMT, kSlice, kCols>), grid, dim3(512), 0, s, \
-                       static_cast<const uint16_t*>(x), w, scales, biases, sb_dtype, y, y_dtype, M, N,   \
-                       K, group_size)
+    hipLaunchKernelGGL((qlinear_decode_kernel<kBits, STEPS, kMT, kSlice, kCols, kXF32>), grid, dim3(512), 0, s, \
+                       x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size)
     switch (K / (8 * kSlice)) {
         case 1: GDN_DEC(1); break;
         case 2: GDN_DEC(2); break;
@@ -511,15 +543,22 @@ bool decode_kernel_fits(const void* x, const uint32_t* w, const void* scales, co
 // weight piece (64-k slices or 8-bit codes): two fit on a CU, which doubles
 // the waves that hide the LDS and MFMA latencies and spreads the columns
 // over all CUs. 33-64 rows keep 64 columns (the LDS holds one workgroup).
-int launch_decode(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
-                  void* y, int y_dtype, int M, int N, int K, int bits, int group_size, hipStream_t s) {
+// float32 x (twice the x tiles) runs up to 32 rows: 32 columns up to 16
+// rows, 64 beyond.
+int launch_decode(const void* x, bool x_f32, const uint32_t* w, const void* scales, const void* biases,
+                  int sb_dtype, void* y, int y_dtype, int M, int N, int K, int bits, int group_size,
+                  hipStream_t s) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
 #define GDN_ARGS x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s
-#define GDN_MT(BITS, SLICE, NARROW)                                                \
-    do {                                                                           \
-        if (mt == 1) return launch_decode_mt<BITS, 1, SLICE, NARROW>(GDN_ARGS);    \
-        if (mt == 2) return launch_decode_mt<BITS, 2, SLICE, NARROW>(GDN_ARGS);    \
-        return launch_decode_mt<BITS, 4, SLICE, 64>(GDN_ARGS);                     \
+#define GDN_MT(BITS, SLICE, NARROW)                                                       \
+    do {                                                                                  \
+        if (x_f32) {                                                                      \
+            if (mt == 1) return launch_decode_mt<BITS, 1, SLICE, NARROW, true>(GDN_ARGS); \
+            return launch_decode_mt<BITS, 2, SLICE, 64, true>(GDN_ARGS);                  \
+        }                                                                                 \
+        if (mt == 1) return launch_decode_mt<BITS, 1, SLICE, NARROW, false>(GDN_ARGS);    \
+        if (mt == 2) return launch_decode_mt<BITS, 2, SLICE, NARROW, false>(GDN_ARGS);    \
+        return launch_decode_mt<BITS, 4, SLICE, 64, false>(GDN_ARGS);                     \
     } while (0)
     if (bits == 4) {
         if (decode_slice(group_size) == 32) GDN_MT(4, 32, 64);
@@ -641,17 +680,22 @@ extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, c
         return rc;
     GDN_REQUIRE(M >= 0, "gdn_quantized_matmul: bad M=%d", M);
     GDN_REQUIRE(valid_dtype(x_dtype) && valid_dtype(y_dtype), "gdn_quantized_matmul: bad dtype");
-    if (x_dtype != GDN_BF16)
-        return fail(GDN_EUNSUPPORTED, "gdn_quantized_matmul: x must be bfloat16 (use gdn_dequantize)");
+    const bool x_f32 = x_dtype == GDN_F32;
+    if (x_dtype != GDN_BF16 && !(x_f32 && M <= 32))
+        return fail(GDN_EUNSUPPORTED,
+                    "gdn_quantized_matmul: x must be bfloat16, or float32 with at most 32 rows "
+                    "(else use gdn_dequantize)");
     if (M == 0) return 0;
     GDN_REQUIRE(x && y, "gdn_quantized_matmul: null x or y");
     GDN_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, "gdn_quantized_matmul: x must be 16-byte aligned");
-    GDN_REQUIRE(!overlaps(x, int64_t(M) * K * 2, y, int64_t(M) * N * dtype_size(y_dtype)),
+    GDN_REQUIRE(!overlaps(x, int64_t(M) * K * dtype_size(x_dtype), y, int64_t(M) * N * dtype_size(y_dtype)),
                 "gdn_quantized_matmul: y overlaps x");
     hipStream_t s = as_stream(stream);
     const auto* wp = static_cast<const uint32_t*>(w);
     if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, N, K, bits, group_size))
-        return launch_decode(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size, s);
+        return launch_decode(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size, s);
+    if (x_f32)
+        return fail(GDN_EUNSUPPORTED, "gdn_quantized_matmul: float32 x needs a shape the decode kernel takes");
     if (bits == 4) return dispatch_sb<4>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);
     return dispatch_sb<8>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);
 }

@@ -107,6 +107,23 @@ def dequantize(tensors: dict, quant: QuantScheme, dtype: torch.dtype | None = No
     return out
 
 
+def decode_kernel_takes(M: int, K: int, bits: int, group_size: int, sb_dtype: torch.dtype) -> bool:
+    """Whether gdn_quantized_matmul runs this shape on its decode kernel
+    (the rule of decode_kernel_fits in gdn_qlinear.hip, for aligned
+    operands): up to 64 rows, K in whole steps of 8 quantization slices (32
+    k for group 32, else 64) with at most 16 steps and the packed words of a
+    thread's share in 64 registers, K / group_size <= 64 and whole 16-byte
+    pieces of scales per column. That kernel multiplies by the exact weights
+    scale * q + bias; the tiled kernels by the weights rounded to bf16."""
+
+    if M > 64:
+        return False
+    step = 8 * (32 if group_size == 32 else 64)
+    ks, gpr = K // step, K // group_size
+    return (K % step == 0 and ks in (1, 2, 4, 8, 16) and ks * step * bits // 256 <= 64
+            and gpr <= 64 and gpr % (4 if sb_dtype == torch.float32 else 8) == 0)
+
+
 def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None) -> torch.Tensor:
     """Linear projection for self-describing, legacy quantized, or dense
     weights (moe_block.py:27-55): ``x @ W.T`` over the last axis of ``x``.
@@ -127,7 +144,10 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None)
     if x.device.type != "cuda":
         raise RuntimeError(f"quantized projections run on ROCm devices only; got {x.device}")
     lead = x.shape[:-1]
-    if x.dtype != torch.bfloat16:
+    rows = x.reshape(-1, K).shape[0]
+    x_f32 = (x.dtype == torch.float32 and rows <= 32
+             and decode_kernel_takes(rows, K, quant.bits, quant.group_size, scales.dtype))
+    if x.dtype != torch.bfloat16 and not x_f32:
         return x @ dequantize(tensors, quant, x.dtype).T
     x2 = _c(x.reshape(-1, K))
     if x2.shape[0] >= _BLAS_ROWS:
@@ -139,7 +159,7 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None)
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
     w, scales, biases = _c(w), _c(scales), _c(biases)
-    _lib.call("gdn_quantized_matmul", _lib.ptr(x2), _lib.GDN_BF16, _lib.ptr(w), _lib.ptr(scales),
+    _lib.call("gdn_quantized_matmul", _lib.ptr(x2), _lib.dtype_code(x2.dtype), _lib.ptr(w), _lib.ptr(scales),
               _lib.ptr(biases), _lib.dtype_code(scales.dtype), _lib.ptr(y),
               _lib.dtype_code(y.dtype), M, N, K, quant.bits, quant.group_size,
               _lib.stream_ptr(x.device))

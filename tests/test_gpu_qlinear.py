@@ -10,6 +10,7 @@ import torch
 
 import mlx_lean_moe_amd as gdn
 from mlx_lean_moe_amd import _lib
+from mlx_lean_moe_amd.quant import decode_kernel_takes
 from oracle import quant_ref as Q
 from oracle import gated_delta_ref as R
 from tests.helpers import assert_bf16_out_close, layer_inputs, layer_params
@@ -31,15 +32,7 @@ def _dev_weights(gpu, words, s, b, sb):
 
 
 def _decode_kernel_takes(M, K, bits, gs, sb):
-    """Mirror of gdn_quantized_matmul's kernel choice (decode_kernel_fits in
-    gdn_qlinear.hip): the decode kernel multiplies by the exact weights
-    s * q + b in float, the tiled kernels by the weights rounded to bf16."""
-    if M > 64:
-        return False
-    step = 8 * (32 if gs == 32 else 64)
-    ks, gpr = K // step, K // gs
-    return (K % step == 0 and ks in (1, 2, 4, 8, 16) and ks * step * bits // 256 <= 64
-            and gpr <= 64 and gpr % (4 if sb == "f32" else 8) == 0)
+    return decode_kernel_takes(M, K, bits, gs, _TORCH[sb])
 
 
 @pytest.mark.parametrize("M,N,K,bits,gs,sb", [
@@ -83,6 +76,32 @@ def test_quantized_matmul_matches_oracle(gpu, M, N, K, bits, gs, sb):
               _lib.ptr(y32), _lib.GDN_F32, M, N, K, bits, gs, _lib.stream_ptr(xt.device))
     err = np.abs(y32.cpu().numpy() - ref).max()
     assert err <= 1e-5 * np.abs(ref).max() + 1e-6, err
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,sb", [
+    (1, 4096, 2048, 4, 64, "bf16"),     # one decode row, as the reference runs (float32 activations)
+    (16, 200, 1024, 4, 32, "f32"),
+    (17, 130, 2048, 8, 64, "f16"),      # 17-32 rows: 64-column workgroups
+    (32, 78, 512, 4, 64, "bf16"),
+])
+def test_float32_activations_on_the_decode_kernel(gpu, M, N, K, bits, gs, sb):
+    """float32 x (split into bf16 hi + lo, ~16 significant bits) against the
+    exact weights: what mx.quantized_matmul computes for float32 x."""
+    assert decode_kernel_takes(M, K, bits, gs, _TORCH[sb])
+    rng = np.random.default_rng(M * 7 + N)
+    words, s, b = _weights(rng, N, K, bits, gs, sb)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ref = Q.quantized_matmul(x, words, s, b, bits, gs, w_round="f32")
+    W = _dev_weights(gpu, words, s, b, sb)
+    y = gdn.quantized_linear(torch.tensor(x, device=gpu), W, gdn.QuantScheme(bits, gs))
+    assert y.dtype == torch.float32
+    err = np.abs(y.cpu().numpy() - ref).max()
+    assert err <= 1e-4 * np.abs(ref).max() + 1e-6, err
+    # more than 32 float32 rows: the C entry declines, quantized_linear dequantizes
+    assert _lib.load().gdn_quantized_matmul(
+        None, _lib.GDN_F32, _lib.ptr(W["weight"]), _lib.ptr(W["scales"]), _lib.ptr(W["biases"]),
+        _lib.dtype_code(W["scales"].dtype), None, _lib.GDN_F32, 33, N, K, bits, gs,
+        None) == _lib.GDN_EUNSUPPORTED
 
 
 @pytest.mark.parametrize("bits,gs,sb,out", [(4, 64, "bf16", "bf16"), (8, 32, "f16", "f32"),
