@@ -13,9 +13,10 @@ Also measured in the same run (reported under "also"):
   prefill:      B=1, T=4096 chunked prefill (bf16 MFMA)
   prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
   decode_slots: B=64 active sequences at random slots of a 256-sequence pool
+  (--workload layer_decode: the whole layer with 4-bit projections, alone)
 
 python bench.py [--steps K] [--warmup W]
-                [--workload decode|decode_large|decode_slots|prefill|prefill_varlen|qlinear|copy]
+                [--workload decode|decode_large|decode_slots|layer_decode|prefill|prefill_varlen|qlinear|copy]
 """
 
 from __future__ import annotations
@@ -190,6 +191,57 @@ class SlotDecodeWorkload:
         rc = self._fn(*self.args[s % len(self.args)])
         if rc != 0:
             raise RuntimeError(f"gdn_decode_step failed with {rc}")
+
+
+def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
+    """The whole gated-delta layer (Hk=16, Hv=32, d=128) decoding B active
+    sequences out of a pool of 4 B slots, 4-bit group-64 projections
+    (stacked qkv|z|a|b in, out_proj out) with bf16 activations: one
+    decode_batch call per step, slot sets rotating as in decode_slots. Also
+    times its three launches alone (input projection, fused decode,
+    out_proj) so the per-part figures add up."""
+
+    d = gdn.QWEN3_5_LINEAR
+    q = gdn.QuantScheme(4, 64)
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def qweights(n, k):
+        return gdn.LinearWeights({
+            "weight": torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), generator=g, device=dev,
+                                    dtype=torch.int32),
+            "scales": (torch.rand(n, k // 64, generator=g, device=dev) * 0.004 + 0.001).to(torch.bfloat16),
+            "biases": ((torch.rand(n, k // 64, generator=g, device=dev) - 0.5) * 0.05).to(torch.bfloat16)}, q)
+
+    rnd = lambda *s_: torch.randn(*s_, generator=g, device=dev)
+    layer = gdn.Qwen3_5LinearAttention(
+        d, qweights(d.conv_dim, hidden), qweights(d.value_dim, hidden),
+        qweights(d.num_value_heads, hidden), qweights(d.num_value_heads, hidden),
+        rnd(d.conv_dim, 4, 1) * 0.2, torch.rand(d.num_value_heads, generator=g, device=dev) * 2.7,
+        rnd(d.num_value_heads), torch.rand(d.value_head_dim, generator=g, device=dev) + 0.5,
+        qweights(hidden, d.value_dim))
+    P = 4 * B
+    pool = gdn.RecurrentStatePool(P, 4, d.conv_dim, d.num_value_heads, 128, 128,
+                                  dtype=torch.bfloat16, device=dev)
+    pool.ssm_state.normal_(0, 0.05, generator=g)
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(0)).tolist()
+    sets = [perm[i * B:(i + 1) * B] for i in range(4)]
+    xs = [rnd(B, hidden).to(torch.bfloat16) for _ in range(4)]
+    total_ms, _ = time_steps(lambda s_: layer.decode_batch(xs[s_ % 4], pool, slots=sets[s_ % 4]),
+                             steps, warmup)
+    # the same steps replayed from HIP graphs (one per slot set)
+    graphs = [gdn.DecodeGraph(layer, pool, sets[i], xs[i]) for i in range(4)]
+    graph_ms, _ = time_steps(lambda s_: graphs[s_ % 4].step(), steps, warmup)
+    x = xs[0]
+    in_ms, _ = time_steps(lambda s_: layer._project(x), steps, warmup)
+    o = rnd(B, d.value_dim).to(torch.bfloat16)
+    out_ms, _ = time_steps(lambda s_: gdn.quantized_linear(o, layer.out_proj), steps, warmup)
+    ms = total_ms / steps
+    return {"workload": f"gated-delta layer decode, B={B} active of {P} slots, hidden {hidden}, "
+                        f"4-bit group-64 projections, bf16 activations",
+            "tokens_per_s": B / (ms * 1e-3), "step_us": ms * 1e3,
+            "graph_step_us": graph_ms / steps * 1e3,
+            "graph_tokens_per_s": B / (graph_ms / steps * 1e-3),
+            "input_projection_us": in_ms / steps * 1e3, "out_proj_us": out_ms / steps * 1e3}
 
 
 def bench_decode_slots(dev, B, Hk, Hv, steps, warmup):
@@ -478,7 +530,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "decode_slots", "prefill",
+                    choices=["decode", "decode_large", "decode_slots", "layer_decode", "prefill",
                              "prefill_varlen", "qlinear", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary workloads")
@@ -567,6 +619,19 @@ def main(argv=None):
                     "tokens_per_s": pv["tokens_per_s"], "call_us": pv["call_us"],
                     "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"]}}
         print(json.dumps(line))
+        return 0
+
+    if args.workload == "layer_decode":
+        r = bench_layer_decode(dev, 64, args.steps, args.warmup)
+        print(json.dumps({"metric": "gated-delta layer decode tokens/s (projections included)",
+                          "value": r["graph_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["graph_step_us"] * 1e-3, "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic", "config": {"workload": r["workload"] + ", HIP-graph steps"},
+                          "eager_step_us": r["step_us"],
+                          "parts_us": {"input_projection": r["input_projection_us"],
+                                       "out_proj": r["out_proj_us"]}}))
         return 0
 
     if args.workload == "decode_slots":

@@ -379,3 +379,48 @@ class Qwen3_5LinearAttention:
             conv_rows=pool.device_conv_rows(slot_t), conv_out=pool.conv_buf)
         pool.advance(slot_list, slot_t)
         return self._proj(out.reshape(rows, d.value_dim), self.out_proj)
+
+
+class DecodeGraph:
+    """One ``decode_batch`` step of ``layer`` for a fixed set of pool slots,
+    captured in a HIP graph: a replay launches the step's kernels (the
+    projections, the fused decode, out_proj and the pool's conv-row and bit
+    updates) without the host work of issuing them one by one.
+
+    The graph reads ``self.x`` and writes ``self.out``; ``step(x)`` copies
+    ``x`` into ``self.x`` (skip it by writing ``self.x`` directly), replays
+    and keeps the pool's host-side bits and sizes in step with the device.
+    Shapes, slots and every buffer are fixed at capture; the pool's contents
+    may change between steps (e.g. ``pool.load``)."""
+
+    def __init__(self, layer: "Qwen3_5LinearAttention", pool: RecurrentStatePool, slots,
+                 x_example: torch.Tensor) -> None:
+        self.layer, self.pool = layer, pool
+        self.slots = check_slots(slots, len(slots), pool.batch)
+        if x_example.ndim != 2 or x_example.shape[0] != len(self.slots):
+            raise ValueError("x_example must be (len(slots), hidden)")
+        self.x = x_example.detach().clone()
+        self._idx = torch.tensor(self.slots, dtype=torch.int64)
+        # the slot array must exist before capture (no host copy in the graph)
+        side = torch.cuda.Stream(self.x.device)
+        side.wait_stream(torch.cuda.current_stream(self.x.device))
+        with torch.cuda.stream(side):
+            pool.device_slots(self.slots)
+        torch.cuda.current_stream(self.x.device).wait_stream(side)
+        torch.cuda.synchronize(self.x.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = layer.decode_batch(self.x, pool, slots=self.slots)
+        # capture ran decode_batch's host bookkeeping once and none of its
+        # device work: undo the former
+        pool.conv_half[self._idx] ^= 1
+        pool.size[self._idx] -= 1
+
+    def step(self, x: torch.Tensor | None = None) -> torch.Tensor:
+        if x is not None and x is not self.x:
+            self.x.copy_(x)
+        self.graph.replay()
+        self.pool.conv_half[self._idx] ^= 1
+        self.pool.size[self._idx] += 1
+        return self.out
+

@@ -144,3 +144,35 @@ def test_pooled_decode_after_chunked_prefill_matches_per_sequence_calls(gpu):
         assert int(pool.size[slot]) == cache.size
     for free in (0, 3, 5):
         assert not pool.ssm_state[free].any() and not pool.conv_state[free].any()
+
+
+def test_decode_graph_replays_equal_eager_decode(gpu):
+    """A captured decode step replayed several times, with other eager GPU
+    work and synchronizations between replays, equals eager decode_batch on
+    a twin pool at every step (outputs and both states)."""
+
+    layer, _ = _build(7, DIMS, gpu, dtype=torch.bfloat16)
+    rng = np.random.default_rng(107)
+    P, slots = 6, [5, 2, 3]
+    pools = [gdn.RecurrentStatePool(P, 4, DIMS.conv_dim, DIMS.num_value_heads, 128, 128,
+                                    dtype=torch.bfloat16, device=gpu) for _ in range(2)]
+    for i, p in enumerate((rng.standard_normal((4, HIDDEN)), rng.standard_normal((2, HIDDEN)),
+                           rng.standard_normal((7, HIDDEN)))):
+        cache = layer.new_cache(torch.bfloat16)
+        layer(torch.tensor(p, dtype=torch.bfloat16, device=gpu), cache)
+        for pool in pools:
+            pool.load(slots[i], cache)
+    eager, graphed = pools
+    xs = [torch.tensor(rng.standard_normal((3, HIDDEN)), dtype=torch.bfloat16, device=gpu)
+          for _ in range(4)]
+    step = gdn.DecodeGraph(layer, graphed, slots, xs[0])
+    scratch = torch.randn(1 << 20, device=gpu)
+    for x in xs:
+        ref = layer.decode_batch(x, eager, slots=slots)
+        out = step.step(x)
+        torch.testing.assert_close(out.float(), ref.float(), rtol=0, atol=0)
+        scratch.mul_(1.0001).sum()  # unrelated eager work between replays
+        torch.cuda.synchronize()
+    torch.testing.assert_close(graphed.ssm_state, eager.ssm_state, rtol=0, atol=0)
+    torch.testing.assert_close(graphed.conv_state, eager.conv_state, rtol=0, atol=0)
+    assert torch.equal(graphed.size, eager.size) and torch.equal(graphed.conv_half, eager.conv_half)
