@@ -100,7 +100,7 @@ class DecodeWorkload:
                 self.z[s % n_i].data_ptr() if self.with_z else None,
                 self.norm_w.data_ptr() if self.with_z else None, 1e-6, self.out.data_ptr(),
                 _lib.GDN_BF16, self.B, d.num_key_heads, d.num_value_heads, 128, 128, 4,
-                _lib.GDN_BF16, None, 0, None, 0, stream))
+                _lib.GDN_BF16, None, 0, None, None, stream))
         self._fn = lib.gdn_decode_step
         return phases
 
@@ -165,13 +165,12 @@ class SlotDecodeWorkload:
         self.out = torch.empty(B, Hv, d, dtype=bf, device=dev)
         perm = torch.randperm(P, generator=torch.Generator().manual_seed(seed))
         sets = [perm[i * B:(i + 1) * B] for i in range(4)]
-        # a slot set's k-th visit reads half k % 2 and writes the other; 8
-        # phases (two visits of each set) close the cycle
-        phases = []
-        for ph in range(8):
-            sl, h = sets[ph % 4], (ph // 4) % 2
-            rows = torch.stack([sl + P * h, sl + P * (1 - h)], 1).reshape(-1)
-            phases.append((sl.to(torch.int32).to(dev), rows.to(torch.int32).to(dev)))
+        # a slot set's k-th visit reads half k % 2 and writes the other (the
+        # pool's half bits all 0, then all 1); 8 phases (two visits of each
+        # set) close the cycle
+        self.halves = [torch.full((P,), h, dtype=torch.int32, device=dev) for h in (0, 1)]
+        phases = [(sets[ph % 4].to(torch.int32).to(dev), self.halves[(ph // 4) % 2])
+                  for ph in range(8)]
         self.phases = phases
         self.B, self.P = B, P
         _, _, self.bytes_per_step = decode_bytes(B, Hk, Hv, d, K, False)
@@ -184,8 +183,8 @@ class SlotDecodeWorkload:
                       self.b[ph % n_inputs].data_ptr(), self.A_log.data_ptr(),
                       self.dt_bias.data_ptr(), self.state.data_ptr(), self.state.data_ptr(), None,
                       None, 1e-6, self.out.data_ptr(), _lib.GDN_BF16, B, Hk, Hv, d, d, K,
-                      _lib.GDN_BF16, sl.data_ptr(), P, rows.data_ptr(), 2 * P, stream)
-                     for ph, (sl, rows) in enumerate(phases)]
+                      _lib.GDN_BF16, sl.data_ptr(), P, half.data_ptr(), None, stream)
+                     for ph, (sl, half) in enumerate(phases)]
 
     def step(self, s):
         rc = self._fn(*self.args[s % len(self.args)])
@@ -644,7 +643,7 @@ def main(argv=None):
                           "roofline": {"bound": "hbm", "achieved": r["hbm_gbs"],
                                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                        "frac": r["hbm_frac"], "traffic": None,
-                                       "kernel": "gdn_decode_step (slots, conv rows)",
+                                       "kernel": "gdn_decode_step (slots, conv half bits)",
                                        "kernel_us": r["kernel_us"],
                                        "algorithmic_bytes_per_launch": r["bytes_per_step"]}}))
         return 0

@@ -46,7 +46,8 @@ typedef enum {
 
 /* Library ABI version (bumped on any signature change or addition; 2 adds the
  * quantized matmul and dequantize entry points, 3 the decode step's state
- * slots, 4 its conv rows). */
+ * slots, 4 its conv rows, 5 replaces the conv rows with the pool's half bits,
+ * adds input row strides and gdn_pool_advance). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -131,19 +132,23 @@ int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dt
  *   slots:          NULL (row b is state slot b), or (B) int32 distinct slot
  *                   indices into a pool of `pool` sequences: state_in/state_out
  *                   are (pool, Hv, Dv, Dk) and the tile of slots[b] is read and
- *                   written (pass state_out == state_in); without conv_rows,
+ *                   written (pass state_out == state_in); without conv_half,
  *                   conv_state_in is (pool, K-1, C) read at slots[b] and
  *                   conv_state_out (B, K-1, C) written at row b (the caller
  *                   copies it back). pool is ignored when slots is NULL.
- *   conv_rows:      NULL, or (B, 2) int32 (in row, out row) per batch row into
- *                   conv arrays of conv_pool rows each (needs slots): row b
- *                   reads its conv state at conv_rows[2b] of conv_state_in and
- *                   writes the rolled state at conv_rows[2b+1] of
- *                   conv_state_out. The two arrays may be one (a pool's two
- *                   halves); out rows must be distinct and no out row may be
- *                   an in row of the launch.
- *   A row whose slot or conv rows fall outside the pools writes NaN to its
- *   output and touches no state.
+ *   conv_half:      NULL, or (pool) int32 (needs slots): the pool's conv state
+ *                   is one (2 pool, K-1, C) array of two halves, passed as both
+ *                   conv_state_in and conv_state_out; slot s holds its current
+ *                   state at row s + pool * (conv_half[s] & 1) and row b rolls
+ *                   it into the other half, row s + pool * (1 - (conv_half[s] & 1)).
+ *                   The bits are read, not flipped: gdn_pool_advance flips them
+ *                   once the step is enqueued.
+ *   row_strides:    NULL (dense inputs), or host int64[4]: the row strides, in
+ *                   elements, of qkv, z, a and b (each at least its row width
+ *                   C, Hv * Dv, Hv, Hv), so that slices of one stacked
+ *                   projection output are read in place.
+ *   A row whose slot falls outside the pool writes NaN to its output and
+ *   touches no state.
  * Specialised for Dk = Dv = 128, K = 4; act_dtype in {F32, BF16}.
  * Replaces one decode call of Qwen3_5LinearAttention.__call__ between the
  * projections (linear_attention.py:103-124) with the Metal scan at T=1.
@@ -153,8 +158,17 @@ int gdn_decode_step(const void *qkv, const void *conv_state_in, void *conv_state
                     const float *A_log, const float *dt_bias, const float *state_in,
                     float *state_out, const void *z, const float *norm_weight, float norm_eps,
                     void *out, int y_dtype, int B, int Hk, int Hv, int Dk, int Dv, int K,
-                    int act_dtype, const int32_t *slots, int pool, const int32_t *conv_rows,
-                    int conv_pool, void *stream);
+                    int act_dtype, const int32_t *slots, int pool, const int32_t *conv_half,
+                    const int64_t *row_strides, void *stream);
+
+/*
+ * gdn_pool_advance - flip conv_half[slots[b]] for b < B: the slots decoded by
+ * a gdn_decode_step call with conv_half now hold their conv state in the
+ * other half. Slots outside [0, pool) are skipped; slots must be distinct.
+ * One launch on `stream`, so a captured decode step includes it. Replaces the
+ * cache update after a decode step (cache/recurrent_cache.py:24-41).
+ */
+int gdn_pool_advance(const int32_t *slots, int B, int32_t *conv_half, int pool, void *stream);
 
 /*
  * gdn_prefill_chunked - chunked (WY/UT, 64-token chunks) prefill on bf16

@@ -114,7 +114,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* S_in,
     float* S_out, const typename Act::storage* __restrict__ z, const float* __restrict__ norm_w,
     float eps, void* __restrict__ out, int y_dtype, int Hk, int Hv,
-    const int32_t* __restrict__ slots, int pool, const int32_t* __restrict__ conv_rows, int conv_pool) {
+    const int32_t* __restrict__ slots, int pool, const int32_t* __restrict__ conv_half,
+    int64_t qkv_stride, int64_t z_stride, int64_t a_stride, int64_t b_stride) {
     __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
     __shared__ float gate_g, gate_beta, norm_r;
 
@@ -125,20 +126,25 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const int tid = threadIdx.x;
     const int w = tid >> 6, l = tid & 63, half = l >> 5, l32 = l & 31;
     // the state slot of batch row b (its state tile is read and written
-    // there) and its conv state rows (read at ci, rolled into co); everything
-    // else is indexed by row
+    // there) and its conv state rows (read at ci, rolled into co): the slot
+    // and the batch row, or with conv_half the slot's current and other half
+    // of a two-half array; the inputs are read at their row strides
     const int sl = slots ? slots[b] : b;
-    const int ci = conv_rows ? conv_rows[2 * b] : sl, co = conv_rows ? conv_rows[2 * b + 1] : b;
-    if (unsigned(sl) >= unsigned(pool) || unsigned(ci) >= unsigned(conv_pool) ||
-        unsigned(co) >= unsigned(conv_pool)) {  // outside the pools: touch no state
+    if (unsigned(sl) >= unsigned(pool)) {  // a slot outside the pool: touch no state
         if (tid < kD) store_any(out, size_t(bh) * kD + tid, kNorm ? Act::code : y_dtype, __builtin_nanf(""));
         return;
+    }
+    int ci = sl, co = b;
+    if (conv_half) {
+        const int hb = conv_half[sl] & 1;
+        ci = sl + pool * hb;
+        co = sl + pool * (1 - hb);
     }
     const size_t sh = size_t(sl) * Hv + h;  // the state tile's index
 
     // A. the front-end's few inputs first, then the 16 float4 state loads:
     // waiting for the former does not wait for the latter.
-    const typename Act::storage* x = qkv + size_t(b) * C;
+    const typename Act::storage* x = qkv + b * qkv_stride;
     const typename Act::storage* cs = cs_in + size_t(ci) * (kTaps - 1) * C;
     typename Act::storage* cso = cs_out + size_t(co) * (kTaps - 1) * C;
     const float4* w4 = reinterpret_cast<const float4*>(conv_w);
@@ -150,7 +156,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     // (unconditional, so no branch forces a wait before the state loads)
     const ConvTaps t1 = load_taps<Act>(x, cs, w4, C, c1);
     const ConvTaps t2 = load_taps<Act>(x, cs, w4, C, c2);
-    const float av = Act::load(a_in, bh), bv = Act::load(b_in, bh);
+    const float av = Act::load(a_in, b * a_stride + h), bv = Act::load(b_in, b * b_stride + h);
     const float alog = A_log[h], dtb = dt_bias[h];
 
     const float4* Sb = reinterpret_cast<const float4*>(S_in + sh * kD * kD);
@@ -238,7 +244,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     if (tid < kD) {
         const float yv = Act::round(ys[tid]);
         const float normed = Act::round(yv * norm_r * norm_w[tid]);
-        const float zz = Act::load(z, size_t(bh) * kD + tid);
+        const float zz = Act::load(z, b * z_stride + h * kD + tid);
         Act::store(static_cast<typename Act::storage*>(out), size_t(bh) * kD + tid,
                    silu(zz) * normed);
     }
@@ -254,7 +260,8 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                                float* state_out, const void* z, const float* norm_weight,
                                float norm_eps, void* out, int y_dtype, int B, int Hk, int Hv,
                                int Dk, int Dv, int K, int act_dtype, const int32_t* slots,
-                               int pool, const int32_t* conv_rows, int conv_pool, void* stream) {
+                               int pool, const int32_t* conv_half, const int64_t* row_strides,
+                               void* stream) {
     GDN_REQUIRE(B >= 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, "gdn_decode_step: bad head counts");
     GDN_REQUIRE(act_dtype == GDN_F32 || act_dtype == GDN_BF16,
                 "gdn_decode_step: activations must be float32 or bfloat16");
@@ -269,16 +276,25 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
     GDN_REQUIRE(!z || norm_weight, "gdn_decode_step: z without norm_weight");
     if (!slots) pool = B;
     GDN_REQUIRE(pool >= 1, "gdn_decode_step: bad pool size %d", pool);
-    GDN_REQUIRE(!conv_rows || slots, "gdn_decode_step: conv_rows needs slots");
-    GDN_REQUIRE(!conv_rows || conv_pool >= 1, "gdn_decode_step: bad conv row count %d", conv_pool);
+    GDN_REQUIRE(!conv_half || slots, "gdn_decode_step: conv_half needs slots");
     const int64_t C = 2LL * Hk * kD + int64_t(Hv) * kD;
     const int64_t row_bytes = (kTaps - 1) * C * dtype_size(act_dtype);
-    // with conv_rows the in and out rows may share one array (the caller
-    // keeps them disjoint); otherwise the two arrays must not overlap
-    if (!conv_rows)
+    // with conv_half both conv pointers are the pool's two-half array (a
+    // slot reads one half and writes the other); otherwise the two arrays
+    // must not overlap
+    if (conv_half)
+        GDN_REQUIRE(conv_state_in == conv_state_out,
+                    "gdn_decode_step: with conv_half, conv_state_in and conv_state_out are one array");
+    else
         GDN_REQUIRE(!overlaps(conv_state_in, int64_t(pool) * row_bytes, conv_state_out, int64_t(B) * row_bytes),
                     "gdn_decode_step: conv_state_out overlaps conv_state_in");
-    const int rows_bound = conv_rows ? conv_pool : (pool > B ? pool : B);
+    int64_t st[4] = {C, int64_t(Hv) * kD, Hv, Hv};  // qkv, z, a, b row strides
+    if (row_strides)
+        for (int i = 0; i < 4; ++i) {
+            GDN_REQUIRE(row_strides[i] >= st[i], "gdn_decode_step: row stride %d is %lld, below %lld", i,
+                        (long long)row_strides[i], (long long)st[i]);
+            st[i] = row_strides[i];
+        }
     const int64_t state_bytes = int64_t(pool) * Hv * kD * kD * 4;
     GDN_REQUIRE(state_in == state_out || !overlaps(state_in, state_bytes, state_out, state_bytes),
                 "gdn_decode_step: state_out partially overlaps state_in");
@@ -294,7 +310,8 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                        static_cast<ACT::storage*>(conv_state_out), conv_weight,               \
                        static_cast<const ACT::storage*>(a), static_cast<const ACT::storage*>(b), \
                        A_log, dt_bias, state_in, state_out, static_cast<const ACT::storage*>(z), \
-                       norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool, conv_rows, rows_bound)
+                       norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool, conv_half, st[0],     \
+                       st[1], st[2], st[3])
     if (act_dtype == GDN_BF16) {
         if (z) GDN_DECODE_LAUNCH(ActBF16, true); else GDN_DECODE_LAUNCH(ActBF16, false);
     } else {
@@ -303,3 +320,28 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
 #undef GDN_DECODE_LAUNCH
     return check_launch("gdn_decode_step");
 }
+
+namespace gdn {
+namespace {
+
+__global__ void pool_advance_kernel(const int32_t* __restrict__ slots, int B, int32_t* __restrict__ half,
+                                    int pool) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) {
+        const int sl = slots[b];
+        if (unsigned(sl) < unsigned(pool)) half[sl] ^= 1;
+    }
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_pool_advance(const int32_t* slots, int B, int32_t* conv_half, int pool, void* stream) {
+    GDN_REQUIRE(B >= 0 && pool >= 1, "gdn_pool_advance: bad sizes");
+    if (B == 0) return 0;
+    GDN_REQUIRE(slots && conv_half, "gdn_pool_advance: null pointer");
+    hipLaunchKernelGGL(pool_advance_kernel, dim3(unsigned((B + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       slots, B, conv_half, pool);
+    return check_launch("gdn_pool_advance");
+}
+

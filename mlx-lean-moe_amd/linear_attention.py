@@ -22,6 +22,8 @@ from a :class:`RecurrentStatePool`.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -109,20 +111,31 @@ def check_slots(slots, batch: int, pool: int) -> list[int]:
     return slots
 
 
-def check_conv_rows(conv_rows, batch: int, rows: int) -> list[int]:
-    """Host-side check of per-row (in, out) conv rows: ``2 batch`` integers
-    in ``[0, rows)``, the out rows distinct and none of them an in row (a
-    row read by one batch row must not be overwritten by another)."""
+def check_half_bits(bits, pool: int) -> list[int]:
+    """Host-side check of a pool's conv half bits: ``pool`` entries, each 0
+    or 1."""
 
-    conv_rows = [int(v) for v in conv_rows]
-    if len(conv_rows) != 2 * batch:
-        raise ValueError(f"expected {2 * batch} conv rows, got {len(conv_rows)}")
-    if any(v < 0 or v >= rows for v in conv_rows):
-        raise ValueError(f"conv rows must lie in [0, {rows})")
-    ins, outs = conv_rows[0::2], conv_rows[1::2]
-    if len(set(outs)) != len(outs) or set(outs) & set(ins):
-        raise ValueError("conv out rows must be distinct and disjoint from the in rows")
-    return conv_rows
+    bits = [int(v) for v in bits]
+    if len(bits) != pool or any(v not in (0, 1) for v in bits):
+        raise ValueError(f"conv_half must be {pool} bits (0 or 1)")
+    return bits
+
+
+def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """``t`` as the decode kernel reads it in place: every row packed (the
+    trailing dims contiguous) and rows at any stride of at least a row's
+    width, e.g. a column slice of a stacked projection output; anything else
+    is copied. Returns the tensor and its row stride in elements."""
+
+    width, packed = 1, True
+    for n, st in zip(reversed(t.shape[1:]), reversed(t.stride()[1:])):
+        packed &= n == 1 or st == width
+        width *= n
+    if t.shape[0] <= 1:
+        return (t if packed else t.contiguous()), width
+    if not packed or t.stride(0) < width:
+        t = t.contiguous()
+    return t, t.stride(0)
 
 
 def _index_array(values, n: int, device, check, name: str) -> torch.Tensor:
@@ -138,7 +151,7 @@ def _index_array(values, n: int, device, check, name: str) -> torch.Tensor:
 
 def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias,
                       norm_weight, eps, dims: LinearAttentionDims, *, conv_out=None,
-                      state_out=None, y_dtype=None, slots=None, conv_rows=None):
+                      state_out=None, y_dtype=None, slots=None, conv_half=None):
     """One decode token for ``B`` sequences in a single kernel launch: conv +
     SiLU + roll, q/k scaling, gates, recurrence and gated RMSNorm
     (linear_attention.py:103-124 at L = 1).
@@ -156,13 +169,17 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     updates the state tiles of ``slots[b]`` in place (``state_out`` must be
     ``ssm_state`` or None); ``conv_out`` is ``(B, K-1, C)`` with the rolled
     rows in batch order, for the caller to put back at the slots. With
-    ``conv_rows`` as well (``2 B`` row indices: where row ``b`` reads its conv
-    state in ``conv_state`` and writes the rolled one in ``conv_out``, which
-    may be the same ``(R, K-1, C)`` array), nothing is left to copy back.
-    ``slots`` and ``conv_rows`` given as host sequences are checked on the
-    host; given as int32 device tensors they are used as they are (no host
-    round trip), and the caller guarantees they are distinct and disjoint as
-    required — the kernel itself still refuses indices outside the arrays.
+    ``conv_half`` as well (the pool's ``P`` bits, 0 or 1), ``conv_state`` is
+    the pool's two-half ``(2 P, K-1, C)`` array: slot ``s`` reads its conv
+    state at row ``s + P * conv_half[s]`` and rolls it into the other half,
+    so nothing is left to copy back (``conv_out`` must be ``conv_state`` or
+    None). The bits are read, not flipped: :meth:`RecurrentStatePool.advance`
+    flips them after the step. ``slots`` and ``conv_half`` given as host
+    sequences are checked on the host; given as int32 device tensors they
+    are used as they are (no host round trip), and the caller guarantees the
+    slots are distinct — the kernel itself still refuses slots outside the
+    pool. ``qkv``, ``z``, ``a`` and ``b`` may be row-strided views (column
+    slices of one stacked projection output); they are read in place.
     Returns ``(out (B, Hv, Dv), conv_out, state_out)``."""
 
     device = _require_device(qkv, z, a, b, conv_state, ssm_state)
@@ -172,25 +189,28 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
         raise ValueError("the fused decode kernel needs Dk = Dv = 128, K = 4 and float32 or "
                          "bfloat16 activations")
     P = B
-    slot_t = rows_t = None
+    slot_t = half_t = None
     if slots is not None:
         P = ssm_state.shape[0]
         slot_t = _index_array(slots, B, device, lambda v: check_slots(v, B, P), "slots")
         if state_out is not None and state_out is not ssm_state:
             raise ValueError("with slots the state is updated in place (state_out=ssm_state)")
         state_out = ssm_state
-    conv_in_rows = P
-    if conv_rows is not None:
-        if slots is None or conv_out is None:
-            raise ValueError("conv_rows needs slots and an explicit conv_out")
-        conv_in_rows = conv_state.shape[0]
-        if conv_out.shape[0] != conv_in_rows:
-            raise ValueError("conv_state and conv_out must have the same number of rows")
-        rows_t = _index_array(conv_rows, 2 * B, device,
-                              lambda v: check_conv_rows(v, B, conv_in_rows), "conv_rows")
+    conv_rows = P
+    if conv_half is not None:
+        if slots is None:
+            raise ValueError("conv_half needs slots")
+        if conv_out is not None and conv_out is not conv_state:
+            raise ValueError("with conv_half the conv state rolls within conv_state "
+                             "(conv_out=conv_state or None)")
+        if not conv_state.is_contiguous():
+            raise ValueError("with conv_half, conv_state must be contiguous")
+        half_t = _index_array(conv_half, P, device, lambda v: check_half_bits(v, P), "conv_half")
+        conv_rows = 2 * P
+        conv_out = conv_state
     if (tuple(qkv.shape) != (B, dims.conv_dim) or tuple(a.shape) != (B, dims.num_value_heads)
             or b.shape != a.shape
-            or tuple(conv_state.shape) != (conv_in_rows, dims.conv_kernel_dim - 1, dims.conv_dim)
+            or tuple(conv_state.shape) != (conv_rows, dims.conv_kernel_dim - 1, dims.conv_dim)
             or tuple(ssm_state.shape) != (P, dims.num_value_heads, dims.value_head_dim,
                                            dims.key_head_dim)
             or (z is not None and tuple(z.shape) != (B, dims.num_value_heads, dims.value_head_dim))):
@@ -199,18 +219,20 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
         raise ValueError("qkv, z, a, b and conv_state must share the activation dtype")
     if ssm_state.dtype != torch.float32 or not ssm_state.is_contiguous():
         raise ValueError("ssm state must be contiguous float32")
-    qkv, a, b, conv_state = _c(qkv), _c(a), _c(b), _c(conv_state)
-    z = _c(z) if z is not None else None
+    (qkv, s_qkv), (a, s_a), (b, s_b) = _rows(qkv), _rows(a), _rows(b)
+    z, s_z = _rows(z) if z is not None else (None, dims.value_dim)
+    conv_state = _c(conv_state)
+    strides = (s_qkv, s_z, s_a, s_b)
+    dense = (dims.conv_dim, dims.value_dim, dims.num_value_heads, dims.num_value_heads)
+    row_strides = None if strides == dense else (ctypes.c_int64 * 4)(*strides)
     conv_weight = _c(conv_weight.float().reshape(dims.conv_dim, dims.conv_kernel_dim))
     A_log, dt_bias = _c(A_log.float()), _c(dt_bias.float())
     norm_weight = _c(norm_weight.float()) if z is not None else None
     if conv_out is None:
         conv_out = torch.empty((B,) + tuple(conv_state.shape[1:]), dtype=act, device=device)
-    elif (tuple(conv_out.shape[1:]) != (dims.conv_kernel_dim - 1, dims.conv_dim) or conv_out.dtype != act
-          or not conv_out.is_contiguous()
-          or (conv_rows is None and conv_out.shape[0] != B)):
-        raise ValueError("conv_out must be contiguous (B, K-1, C) in the activation dtype "
-                         "(or conv_state's rows with conv_rows)")
+    elif half_t is None and (tuple(conv_out.shape) != (B, dims.conv_kernel_dim - 1, dims.conv_dim)
+                             or conv_out.dtype != act or not conv_out.is_contiguous()):
+        raise ValueError("conv_out must be contiguous (B, K-1, C) in the activation dtype")
     if state_out is None:
         state_out = torch.empty_like(ssm_state)
     out_dtype = act if z is not None else (y_dtype or torch.float32)
@@ -221,8 +243,8 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
               _lib.ptr(dt_bias), _lib.ptr(ssm_state), _lib.ptr(state_out), _lib.ptr(z),
               _lib.ptr(norm_weight), float(eps), _lib.ptr(out), _lib.dtype_code(out_dtype), B,
               dims.num_key_heads, dims.num_value_heads, dims.key_head_dim, dims.value_head_dim,
-              dims.conv_kernel_dim, _lib.dtype_code(act), _lib.ptr(slot_t), P, _lib.ptr(rows_t),
-              conv_in_rows, _stream(device))
+              dims.conv_kernel_dim, _lib.dtype_code(act), _lib.ptr(slot_t), P, _lib.ptr(half_t),
+              row_strides, _stream(device))
     return out, conv_out, state_out
 
 
@@ -293,8 +315,9 @@ class Qwen3_5LinearAttention:
             out = quantized_linear(rows, self._in_stacked)
             qkv, z, a, b = torch.split(out, [d.conv_dim, d.value_dim, d.num_value_heads,
                                              d.num_value_heads], dim=-1)
-            return (qkv.contiguous(), z.reshape(L, d.num_value_heads, d.value_head_dim),
-                    a.contiguous(), b.contiguous())
+            # column slices of one output: the fused decode reads them in
+            # place, every other consumer copies what it needs packed
+            return qkv, z.reshape(L, d.num_value_heads, d.value_head_dim), a, b
         qkv = self._proj(rows, self.in_proj_qkv)
         z = self._proj(rows, self.in_proj_z).reshape(L, d.num_value_heads, d.value_head_dim)
         a = self._proj(rows, self.in_proj_a)
@@ -376,7 +399,7 @@ class Qwen3_5LinearAttention:
         out, _, _ = fused_decode_step(
             qkv, z, a, b, pool.conv_buf, pool.ssm_state, self.conv1d_weight, self.A_log,
             self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_t,
-            conv_rows=pool.device_conv_rows(slot_t), conv_out=pool.conv_buf)
+            conv_half=pool.conv_half_dev)
         pool.advance(slot_list, slot_t)
         return self._proj(out.reshape(rows, d.value_dim), self.out_proj)
 
@@ -384,8 +407,8 @@ class Qwen3_5LinearAttention:
 class DecodeGraph:
     """One ``decode_batch`` step of ``layer`` for a fixed set of pool slots,
     captured in a HIP graph: a replay launches the step's kernels (the
-    projections, the fused decode, out_proj and the pool's conv-row and bit
-    updates) without the host work of issuing them one by one.
+    stacked projection, the fused decode, out_proj and the flip of the
+    pool's conv half bits) without the host work of issuing them one by one.
 
     The graph reads ``self.x`` and writes ``self.out``; ``step(x)`` copies
     ``x`` into ``self.x`` (skip it by writing ``self.x`` directly), replays

@@ -12,6 +12,8 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
+
 
 class RecurrentCache:
     """One gated-delta layer's rolling state for one sequence."""
@@ -45,7 +47,10 @@ class RecurrentStatePool:
     be rolled in place: ``conv_buf`` holds two ``(B, K-1, C)`` halves and
     slot ``s`` currently lives in row ``s + B * conv_half[s]``; a decode reads
     that row and writes the rolled state into the slot's other half, then
-    the slot's half flips (no copy, and slots decode independently)."""
+    the slot's half flips (no copy, and slots decode independently). The
+    bits live on the device (``conv_half_dev``, read by the decode kernel and
+    flipped by ``advance`` in one launch) with a host copy (``conv_half``)
+    for host-side reads."""
 
     def __init__(self, batch: int, conv_kernel_dim: int, conv_dim: int, num_value_heads: int,
                  value_head_dim: int, key_head_dim: int, dtype: torch.dtype = torch.bfloat16,
@@ -53,9 +58,7 @@ class RecurrentStatePool:
         self.conv_buf = torch.zeros((2 * batch, conv_kernel_dim - 1, conv_dim), dtype=dtype,
                                     device=device)
         self.conv_half = torch.zeros(batch, dtype=torch.int64)
-        # the same bits on the device, so a decode step's conv rows are
-        # computed without a host round trip
-        self._half_dev = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.conv_half_dev = torch.zeros(batch, dtype=torch.int32, device=device)
         self._slot_sets: dict[tuple[int, ...], torch.Tensor] = {}
         self.ssm_state = torch.zeros((batch, num_value_heads, value_head_dim, key_head_dim),
                                      dtype=torch.float32, device=device)
@@ -76,14 +79,6 @@ class RecurrentStatePool:
     def state(self) -> tuple[torch.Tensor, torch.Tensor]:
         return self.conv_state, self.ssm_state
 
-    def conv_rows(self, slots: list[int]) -> list[int]:
-        """(current row, other row) of each slot's conv state, flattened."""
-        rows = []
-        for s in slots:
-            h = int(self.conv_half[s])
-            rows += [s + self.batch * h, s + self.batch * (1 - h)]
-        return rows
-
     def device_slots(self, slots: list[int]) -> torch.Tensor:
         """``slots`` as an int32 device array, kept per active set (a serving
         loop decodes the same set for many steps), copied without blocking."""
@@ -96,19 +91,18 @@ class RecurrentStatePool:
             t = self._slot_sets[key] = host.to(self.ssm_state.device, non_blocking=True)
         return t
 
-    def device_conv_rows(self, slot_t: torch.Tensor) -> torch.Tensor:
-        """conv_rows for an int32 device array of slots, on the device."""
-        h = self._half_dev[slot_t.long()]
-        return torch.stack([slot_t + self.batch * h, slot_t + self.batch * (1 - h)], 1).reshape(-1)
-
     def advance(self, slots: list[int], slot_t: torch.Tensor | None = None) -> None:
-        """After a decode of ``slots``: their conv state now lives in the
-        other half, and each holds one more token."""
+        """After a decode of ``slots`` (distinct; ``slot_t`` the same as an
+        int32 device array, if the caller has it): their conv state now lives
+        in the other half, and each holds one more token."""
         idx = torch.tensor(slots, dtype=torch.int64)
         self.conv_half[idx] ^= 1
         self.size[idx] += 1
-        dev_idx = slot_t.long() if slot_t is not None else idx.to(self._half_dev.device)
-        self._half_dev[dev_idx] ^= 1
+        if slot_t is None:
+            slot_t = self.device_slots(slots)
+        device = self.conv_half_dev.device
+        _lib.call("gdn_pool_advance", _lib.ptr(slot_t), len(slots), _lib.ptr(self.conv_half_dev),
+                  self.batch, _lib.stream_ptr(device))
 
     def load(self, slot: int, cache: RecurrentCache) -> None:
         """Copy one sequence's state (e.g. after its prefill) into ``slot``."""

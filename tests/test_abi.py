@@ -53,9 +53,19 @@ def test_invalid_arguments_return_einval_without_launching():
                                 ctypes.c_void_p(16), 0, None, 0, None, 3, 4, 1, 1, 32, 8, None)
     assert rc == _lib.GDN_EINVAL and "divisible" in _err(lib)
     # the fused decode kernel is specialised for Dk = Dv = 128
-    rc = lib.gdn_decode_step(*([None] * 12), 1e-6, None, 0, 1, 2, 4, 64, 64, 4, 1, None, 0, None, 0,
-                             None)
+    rc = lib.gdn_decode_step(*([None] * 12), 1e-6, None, 0, 1, 2, 4, 64, 64, 4, 1, None, 0, None,
+                             None, None)
     assert rc == _lib.GDN_EUNSUPPORTED
+    # row strides below a row's width, and conv_half with two conv arrays
+    fake = [ctypes.c_void_p(1 << (20 + i)) for i in range(12)]
+    C = 2 * 1 * 128 + 2 * 128
+    slots = ctypes.c_void_p(1 << 40)
+    for strides, conv_out, what in (((C - 1, 256, 2, 2), fake[1], "row stride 0"),
+                                    ((C, 256, 2, 1), fake[1], "row stride 3"),
+                                    ((C, 256, 2, 2), fake[2], "one array")):
+        rc = lib.gdn_decode_step(fake[0], fake[1], conv_out, *fake[3:12], 1e-6, fake[11], 0, 1, 1, 2,
+                                 128, 128, 4, 1, slots, 4, slots, (ctypes.c_int64 * 4)(*strides), None)
+        assert rc == _lib.GDN_EINVAL and what in _err(lib), (what, _err(lib))
     # overlapping conv state buffers are rejected
     p = ctypes.c_void_p(4096)
     rc = lib.gdn_frontend(p, p, p, 1, p, None, 1, 1, p, p, p, 1, 2, 32, 32, 4, 1, None)

@@ -59,39 +59,80 @@ def test_slot_decode_equals_decode_of_gathered_sequences(gpu, act, with_z):
     assert torch.equal(c["conv"], conv_before)  # the pool's conv rows are the caller's to update
 
 
-def test_conv_rows_roll_into_the_other_half_without_a_copy(gpu):
-    """Conv state in the two halves of one array: each row reads its slot's
-    current row and writes the other; untouched rows keep their bytes."""
+def test_conv_half_rolls_into_the_other_half_without_a_copy(gpu):
+    """Conv state in the two halves of one array, each slot's half given by
+    the pool's bits: a row reads its slot's current row and writes the
+    other; untouched rows keep their bytes, and the bits are not changed."""
 
     P, slots = 6, [4, 1]
     c = _pool_case(13, P, len(slots), torch.bfloat16, gpu)
     buf = torch.cat([c["conv"], torch.zeros_like(c["conv"])])  # slot s in row s (half 0)
     buf[P + 1] = c["conv"][1]  # slot 1 currently in half 1: row 7 (row 1 is stale)
     buf[1].fill_(3.0)
-    half = {4: 0, 1: 1}
-    rows = []
-    for s_ in slots:
-        rows += [s_ + P * half[s_], s_ + P * (1 - half[s_])]
+    bits = [0, 1, 0, 1, 0, 0]
+    half = torch.tensor(bits, dtype=torch.int32, device=gpu)
     idx = torch.tensor(slots, device=gpu)
     ref_out, ref_conv, ref_state = gdn.fused_decode_step(
         c["qkv"], c["z"], c["a"], c["b"], c["conv"][idx].clone(), c["state"][idx].clone(),
         c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS)
     before = buf.clone()
-    out, _, _ = gdn.fused_decode_step(
+    out, conv_out, _ = gdn.fused_decode_step(
         c["qkv"], c["z"], c["a"], c["b"], buf, c["state"], c["conv_w"], c["A_log"], c["dt_bias"],
-        c["norm_w"], 1e-6, DIMS, slots=slots, conv_rows=rows, conv_out=buf)
+        c["norm_w"], 1e-6, DIMS, slots=slots, conv_half=half)
+    assert conv_out is buf
     assert torch.equal(out, ref_out)
-    assert torch.equal(buf[rows[1]], ref_conv[0]) and torch.equal(buf[rows[3]], ref_conv[1])
-    assert torch.equal(c["state"][idx], ref_state)
-    written = {rows[1], rows[3]}
+    written = {4 + P: ref_conv[0], 1: ref_conv[1]}  # slot 4: half 0 -> 1; slot 1: half 1 -> 0
     for r in range(2 * P):
-        if r not in written:
-            assert torch.equal(buf[r], before[r]), r
-    for bad in ([4, 4, 7, 1], [4, 10, 7, 4], [4, 12, 7, 1]):  # out rows shared, out = an in row, range
+        assert torch.equal(buf[r], written[r] if r in written else before[r]), r
+    assert torch.equal(c["state"][idx], ref_state)
+    assert half.tolist() == bits
+    for bad, conv_out in (([0, 2, 0, 0, 0, 0], None), ([0, 1], None), (bits, buf.clone())):
         with pytest.raises(ValueError):
             gdn.fused_decode_step(c["qkv"], c["z"], c["a"], c["b"], buf, c["state"], c["conv_w"],
                                   c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS, slots=slots,
-                                  conv_rows=bad, conv_out=buf)
+                                  conv_half=bad, conv_out=conv_out)
+    with pytest.raises(ValueError, match="needs slots"):
+        gdn.fused_decode_step(c["qkv"], c["z"], c["a"], c["b"], buf[:2], c["state"][:2],
+                              c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS,
+                              conv_half=bits[:2])
+
+
+def test_pool_advance_flips_the_bits_of_the_decoded_slots(gpu):
+    pool = gdn.RecurrentStatePool(300, 4, DIMS.conv_dim, DIMS.num_value_heads, 128, 128,
+                                  dtype=torch.bfloat16, device=gpu)
+    rng = np.random.default_rng(5)
+    want = np.zeros(300, np.int64)
+    for n in (3, 257, 300, 1):  # more slots than one workgroup holds, and all of them
+        slots = rng.permutation(300)[:n].tolist()
+        pool.advance(slots)
+        want[slots] ^= 1
+        assert pool.conv_half.tolist() == want.tolist()
+        assert pool.conv_half_dev.cpu().tolist() == want.tolist()
+
+
+@pytest.mark.parametrize("with_z", [False, True])
+def test_row_strided_inputs_are_read_in_place(gpu, with_z):
+    """qkv, z, a and b as column slices of one stacked (B, C + Hv Dv + 2 Hv)
+    array (the stacked projection's output) give the same bits as packed
+    copies."""
+
+    P, slots = 5, [3, 0, 4]
+    c = _pool_case(14, P, len(slots), torch.bfloat16, gpu)
+    B = len(slots)
+    stacked = torch.cat([c["qkv"], c["z"].reshape(B, -1), c["a"], c["b"], c["a"][:, :3]], 1)
+    qkv, z, a, b = torch.split(stacked, [DIMS.conv_dim, DIMS.value_dim, DIMS.num_value_heads,
+                                         DIMS.num_value_heads, 3], 1)[:4]
+    z = z.reshape(B, DIMS.num_value_heads, 128)
+    assert not qkv.is_contiguous() and not z.is_contiguous() and not a.is_contiguous()
+    state = c["state"].clone()
+    conv = c["conv"]
+    res = []
+    for args, st in (((c["qkv"], c["z"], c["a"], c["b"]), c["state"]), ((qkv, z, a, b), state)):
+        res.append(gdn.fused_decode_step(args[0], args[1] if with_z else None, args[2], args[3], conv,
+                                         st, c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"],
+                                         1e-6, DIMS, slots=slots))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    assert torch.equal(c["state"], state)
 
 
 def test_slot_outside_pool_touches_no_state(gpu):
@@ -108,7 +149,7 @@ def test_slot_outside_pool_touches_no_state(gpu):
               _lib.ptr(c["conv_w"].reshape(DIMS.conv_dim, 4).contiguous()), _lib.ptr(c["a"]),
               _lib.ptr(c["b"]), _lib.ptr(c["A_log"]), _lib.ptr(c["dt_bias"]), _lib.ptr(c["state"]),
               _lib.ptr(c["state"]), None, None, 1e-6, _lib.ptr(out), _lib.GDN_F32, B, 2, 4, 128,
-              128, 4, _lib.GDN_BF16, _lib.ptr(slots), P, None, 0, _lib.stream_ptr(gpu))
+              128, 4, _lib.GDN_BF16, _lib.ptr(slots), P, None, None, _lib.stream_ptr(gpu))
     torch.cuda.synchronize()
     assert torch.isnan(out[0]).all() and torch.isfinite(out[1]).all()
     assert torch.equal(c["state"][0], before[0]) and torch.equal(c["state"][2:], before[2:])
@@ -176,3 +217,5 @@ def test_decode_graph_replays_equal_eager_decode(gpu):
     torch.testing.assert_close(graphed.ssm_state, eager.ssm_state, rtol=0, atol=0)
     torch.testing.assert_close(graphed.conv_state, eager.conv_state, rtol=0, atol=0)
     assert torch.equal(graphed.size, eager.size) and torch.equal(graphed.conv_half, eager.conv_half)
+    assert torch.equal(graphed.conv_half_dev, eager.conv_half_dev)
+    assert graphed.conv_half_dev.cpu().tolist() == graphed.conv_half.tolist()

@@ -120,7 +120,7 @@ def test_layer_varlen_prefill_then_fused_decode(gpu):
                                             bf(x_b[:, 0]), pool.conv_buf, pool.ssm_state,
                                             layer.conv1d_weight, layer.A_log, layer.dt_bias,
                                             layer.norm_weight, 1e-6, dims, slots=slots,
-                                            conv_rows=pool.conv_rows(slots), conv_out=pool.conv_buf)
+                                            conv_half=pool.conv_half_dev)
         pool.advance(slots)
         for i in range(N):
             o, conv_ref[i], ssm_ref[i] = R.linear_attention_core(
