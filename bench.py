@@ -100,7 +100,7 @@ class DecodeWorkload:
                 self.z[s % n_i].data_ptr() if self.with_z else None,
                 self.norm_w.data_ptr() if self.with_z else None, 1e-6, self.out.data_ptr(),
                 _lib.GDN_BF16, self.B, d.num_key_heads, d.num_value_heads, 128, 128, 4,
-                _lib.GDN_BF16, None, 0, None, None, stream))
+                _lib.GDN_BF16, None, 0, None, None, None, stream))
         self._fn = lib.gdn_decode_step
         return phases
 
@@ -183,7 +183,7 @@ class SlotDecodeWorkload:
                       self.b[ph % n_inputs].data_ptr(), self.A_log.data_ptr(),
                       self.dt_bias.data_ptr(), self.state.data_ptr(), self.state.data_ptr(), None,
                       None, 1e-6, self.out.data_ptr(), _lib.GDN_BF16, B, Hk, Hv, d, d, K,
-                      _lib.GDN_BF16, sl.data_ptr(), P, half.data_ptr(), None, stream)
+                      _lib.GDN_BF16, sl.data_ptr(), P, half.data_ptr(), None, None, stream)
                      for ph, (sl, half) in enumerate(phases)]
 
     def step(self, s):
@@ -365,9 +365,13 @@ class QLinearWorkload:
 
         self._fn = _lib.load().gdn_quantized_matmul
         stream = torch.cuda.current_stream().cuda_stream
+        ws_bytes = int(_lib.load().gdn_quantized_matmul_workspace_size(
+            _lib.GDN_BF16, _lib.GDN_BF16, M, N, K, bits, group_size))
+        self.ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
         self._args = [(self.x.data_ptr(), _lib.GDN_BF16, w.data_ptr(), sc.data_ptr(),
                        bi.data_ptr(), _lib.GDN_BF16, self.y.data_ptr(), _lib.GDN_BF16, M, N, K,
-                       bits, group_size, stream) for w, sc, bi in self.weights]
+                       bits, group_size, self.ws.data_ptr(), ws_bytes, stream)
+                      for w, sc, bi in self.weights]
 
     def step(self, s):
         rc = self._fn(*self._args[s % self.copies])

@@ -47,7 +47,8 @@ typedef enum {
 /* Library ABI version (bumped on any signature change or addition; 2 adds the
  * quantized matmul and dequantize entry points, 3 the decode step's state
  * slots, 4 its conv rows, 5 replaces the conv rows with the pool's half bits,
- * adds input row strides and gdn_pool_advance). */
+ * adds input row strides and gdn_pool_advance, 6 the quantized matmul's
+ * workspace and the decode step's conv_arrivals). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -141,12 +142,16 @@ int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dt
  *                   conv_state_in and conv_state_out; slot s holds its current
  *                   state at row s + pool * (conv_half[s] & 1) and row b rolls
  *                   it into the other half, row s + pool * (1 - (conv_half[s] & 1)).
- *                   The bits are read, not flipped: gdn_pool_advance flips them
- *                   once the step is enqueued.
+ *                   Without conv_arrivals the bits are only read (gdn_pool_advance
+ *                   flips them after the step).
  *   row_strides:    NULL (dense inputs), or host int64[4]: the row strides, in
  *                   elements, of qkv, z, a and b (each at least its row width
  *                   C, Hv * Dv, Hv, Hv), so that slices of one stacked
  *                   projection output are read in place.
+ *   conv_arrivals:  NULL, or (pool) int32 counters, all zero between calls (needs
+ *                   conv_half): the step flips conv_half[slots[b]] itself (the
+ *                   last of row b's Hv workgroups to finish, counted here, flips
+ *                   it and resets the count), so no gdn_pool_advance follows.
  *   A row whose slot falls outside the pool writes NaN to its output and
  *   touches no state.
  * Specialised for Dk = Dv = 128, K = 4; act_dtype in {F32, BF16}.
@@ -158,8 +163,8 @@ int gdn_decode_step(const void *qkv, const void *conv_state_in, void *conv_state
                     const float *A_log, const float *dt_bias, const float *state_in,
                     float *state_out, const void *z, const float *norm_weight, float norm_eps,
                     void *out, int y_dtype, int B, int Hk, int Hv, int Dk, int Dv, int K,
-                    int act_dtype, const int32_t *slots, int pool, const int32_t *conv_half,
-                    const int64_t *row_strides, void *stream);
+                    int act_dtype, const int32_t *slots, int pool, int32_t *conv_half,
+                    const int64_t *row_strides, int32_t *conv_arrivals, void *stream);
 
 /*
  * gdn_pool_advance - flip conv_half[slots[b]] for b < B: the slots decoded by
@@ -226,13 +231,30 @@ int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, co
  * kernels do). Otherwise the weights enter the MFMAs as bf16(scale * q + bias)
  * (the product is exact in float32; one rounding), i.e. x times the weights
  * mx.dequantize yields (as MLX's matrix-matrix kernels do).
+ *   workspace: NULL, or device scratch of workspace_bytes (16-byte aligned).
+ *      With gdn_quantized_matmul_workspace_size(...) bytes, a decode-kernel
+ *      call with few column tiles (small N) splits K over several
+ *      workgroups, which store float32 partial products there, and a second
+ *      kernel adds them in a fixed order (deterministic; the sum's order,
+ *      and so its last bits, differ from the unsplit kernel's). With less,
+ *      it splits less or not at all. Calls sharing a workspace must not
+ *      overlap.
  * Replaces mx.quantized_matmul(..., mode="affine") in quantized_linear
  * (model/moe_block.py:44-55), used for the layer's projections
  * (model/qwen3_5/linear_attention.py:96-101,125).
  */
 int gdn_quantized_matmul(const void *x, int x_dtype, const void *w, const void *scales,
                          const void *biases, int sb_dtype, void *y, int y_dtype, int M, int N,
-                         int K, int bits, int group_size, void *stream);
+                         int K, int bits, int group_size, void *workspace,
+                         int64_t workspace_bytes, void *stream);
+
+/*
+ * gdn_quantized_matmul_workspace_size - workspace bytes gdn_quantized_matmul
+ * uses for these sizes and dtypes with its full K split (0: it does not
+ * split K). No reference counterpart: MLX's kernels allocate their own.
+ */
+int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype, int M, int N, int K,
+                                            int bits, int group_size);
 
 /*
  * gdn_dequantize - the dense weights of gdn_quantized_matmul's layout:

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* S_in,
     float* S_out, const typename Act::storage* __restrict__ z, const float* __restrict__ norm_w,
     float eps, void* __restrict__ out, int y_dtype, int Hk, int Hv,
-    const int32_t* __restrict__ slots, int pool, const int32_t* __restrict__ conv_half,
+    const int32_t* __restrict__ slots, int pool, int32_t* conv_half, int32_t* arrivals,
     int64_t qkv_stride, int64_t z_stride, int64_t a_stride, int64_t b_stride) {
     __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
     __shared__ float gate_g, gate_beta, norm_r;
@@ -215,6 +215,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
         else ys[row] = g * tot + delta_pair * kq;
     }
     __syncthreads();
+    // Every thread has read the slot's half bit (its conv loads used it). The
+    // last of the row's Hv workgroups to get here flips it and resets the
+    // count, so the next launch reads the half this one wrote.
+    if (arrivals && tid == 0 && atomicAdd(&arrivals[sl], 1) == Hv - 1) {
+        atomicXor(&conv_half[sl], 1);
+        atomicExch(&arrivals[sl], 0);
+    }
 
     // H. update and store the tile.
     float4* So = reinterpret_cast<float4*>(S_out + sh * kD * kD);
@@ -260,8 +267,8 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                                float* state_out, const void* z, const float* norm_weight,
                                float norm_eps, void* out, int y_dtype, int B, int Hk, int Hv,
                                int Dk, int Dv, int K, int act_dtype, const int32_t* slots,
-                               int pool, const int32_t* conv_half, const int64_t* row_strides,
-                               void* stream) {
+                               int pool, int32_t* conv_half, const int64_t* row_strides,
+                               int32_t* conv_arrivals, void* stream) {
     GDN_REQUIRE(B >= 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, "gdn_decode_step: bad head counts");
     GDN_REQUIRE(act_dtype == GDN_F32 || act_dtype == GDN_BF16,
                 "gdn_decode_step: activations must be float32 or bfloat16");
@@ -277,6 +284,7 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
     if (!slots) pool = B;
     GDN_REQUIRE(pool >= 1, "gdn_decode_step: bad pool size %d", pool);
     GDN_REQUIRE(!conv_half || slots, "gdn_decode_step: conv_half needs slots");
+    GDN_REQUIRE(!conv_arrivals || conv_half, "gdn_decode_step: conv_arrivals needs conv_half");
     const int64_t C = 2LL * Hk * kD + int64_t(Hv) * kD;
     const int64_t row_bytes = (kTaps - 1) * C * dtype_size(act_dtype);
     // with conv_half both conv pointers are the pool's two-half array (a
@@ -310,8 +318,8 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                        static_cast<ACT::storage*>(conv_state_out), conv_weight,               \
                        static_cast<const ACT::storage*>(a), static_cast<const ACT::storage*>(b), \
                        A_log, dt_bias, state_in, state_out, static_cast<const ACT::storage*>(z), \
-                       norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool, conv_half, st[0],     \
-                       st[1], st[2], st[3])
+                       norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool, conv_half,         \
+                       conv_arrivals, st[0], st[1], st[2], st[3])
     if (act_dtype == GDN_BF16) {
         if (z) GDN_DECODE_LAUNCH(ActBF16, true); else GDN_DECODE_LAUNCH(ActBF16, false);
     } else {

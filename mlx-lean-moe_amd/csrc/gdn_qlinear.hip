@@ -187,6 +187,12 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
 // blocks are summed in LDS in a fixed order at the end. Needs K a multiple
 // of 8 kSlice (kSteps steps), K / group_size <= kDecGroups and a multiple of
 // the 16-byte piece's entry count, and 16-byte aligned operands.
+//
+// Split K: with gridDim.y = S > 1, workgroup (t, j) takes the k range
+// [j K / S, (j + 1) K / S) of column tile t (kSteps steps of it) and stores
+// its float32 block at partial[j][M][N]; qlinear_split_sum_kernel adds the
+// S blocks in order. It spreads few column tiles (a projection with small
+// N) over the CUs.
 constexpr int kDecGroups = 64;  // scale groups per column the LDS holds
 
 // The two constants of the 4-bit code fragment, held in registers so that
@@ -227,7 +233,7 @@ template <int kBits, int kSteps, int kMT, int kSlice, int kCols, bool kXF32>
 __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     const void* __restrict__ xp, const uint32_t* __restrict__ w, const void* __restrict__ scales,
     const void* __restrict__ biases, int sb_dtype, void* __restrict__ y, int y_dtype, int M, int N, int K,
-    int group_size) {
+    int group_size, float* __restrict__ partial) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     constexpr int kStep = 8 * kSlice;            // k per step
     constexpr int kKB = kSlice / 32;             // MFMA k blocks per wave per step
@@ -263,15 +269,17 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     const int n0 = blockIdx.x * kCols;
     const int gpr = K / group_size;
     const int64_t wpr = int64_t(K) * kBits / 32;
+    // this workgroup's k range: split blockIdx.y, kSteps steps from k0, whose
+    // gl groups start at group split gl of each column
+    const int split = blockIdx.y, k0 = split * kSteps * kStep, gl = kSteps * kStep / group_size;
 
-    // Scales and biases of the kCols columns: one contiguous span of kCols gpr
-    // entries each, in 16-byte pieces (a piece holds groups of one column),
-    // at most 4 per thread. Pieces past the arrays' end (columns >= N, whose
-    // outputs are not stored) read the last piece; threads past the last
-    // piece repeat it.
+    // Scales and biases of the range's groups of the kCols columns, in
+    // 16-byte pieces (a piece holds groups of one column), at most 4 per
+    // thread. Columns >= N (whose outputs are not stored) read column N - 1;
+    // threads past the last piece repeat it.
     const int esz = sb_dtype == GDN_F32 ? 4 : 2, per_piece = 16 / esz;
-    const int span_pieces = kCols * gpr / per_piece;
-    const int64_t base_piece = int64_t(n0) * gpr / per_piece, last_piece = int64_t(N) * gpr / per_piece - 1;
+    const int ppc = gl / per_piece;  // pieces per column
+    const int span_pieces = kCols * ppc;
     u32x4 pv[4];
     int pdst[4];
     const int sb_rounds = (2 * span_pieces + 511) / 512;  // pieces per thread, at most 4
@@ -280,10 +288,10 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         int p = tid + 512 * i;
         p = p < 2 * span_pieces ? p : 2 * span_pieces - 1;
         const int which = p >= span_pieces, o = p - which * span_pieces;
-        const int64_t gp = base_piece + o < last_piece ? base_piece + o : last_piece;
-        pv[i] = reinterpret_cast<const u32x4*>(which ? biases : scales)[gp];
-        const int e = o * per_piece, c = e / gpr;
-        pdst[i] = which * kSBRow + c * (gpr + 1) + (e - c * gpr);
+        const int c = o / ppc, pc = o - c * ppc;
+        const int64_t col = n0 + c < N ? n0 + c : N - 1;
+        pv[i] = reinterpret_cast<const u32x4*>(which ? biases : scales)[(col * gpr + int64_t(split) * gl) / per_piece + pc];
+        pdst[i] = which * kSBRow + c * (gl + 1) + pc * per_piece;
     }
 
     // x chunk p = tid + 512 i of a step: row p / (kStep / 8) (clamped to
@@ -298,7 +306,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         for (int i = 0; i < kXLoads; ++i) {
             const int p = tid + 512 * i, r = p / (kStep / 8), ch = p % (kStep / 8);
             const int row = r < M ? r : M - 1;
-            xv[i] = *reinterpret_cast<const xchunk_t*>(x + int64_t(row) * K + kStep * s + 8 * ch);
+            xv[i] = *reinterpret_cast<const xchunk_t*>(x + int64_t(row) * K + k0 + kStep * s + 8 * ch);
         }
     };
     // 4-bit fragments pair codes i and i + 4 of a word: stage each chunk in
@@ -337,7 +345,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         for (int i = 0; i < kWLoads; ++i) {
             const int p = tid + 512 * i, c = p / (kWPC / 4), pc = p % (kWPC / 4);
             const int64_t col = n0 + c < N ? n0 + c : N - 1;
-            wq[s][i] = *reinterpret_cast<const u32x4*>(w + col * wpr + kWPC * s + 4 * pc);
+            wq[s][i] = *reinterpret_cast<const u32x4*>(w + col * wpr + int64_t(k0) * kBits / 32 + kWPC * s + 4 * pc);
         }
     auto stage_w = [&](int buf, int s) {
 #pragma unroll
@@ -347,7 +355,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         }
     };
 
-    // scales and biases to float, [which][column][group] with rows of gpr + 1;
+    // scales and biases to float, [which][column][group] with rows of gl + 1;
     // only threads holding a piece store it (the repeats would pile onto
     // one LDS address)
 #pragma unroll
@@ -400,7 +408,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
 #pragma unroll
         for (int tn = 0; tn < kTN; ++tn) {
             const int c = 16 * tn + lr;
-            const float sc = sbs[c * (gpr + 1) + g], bi = sbs[kSBRow + c * (gpr + 1) + g];
+            const float sc = sbs[c * (gl + 1) + g], bi = sbs[kSBRow + c * (gl + 1) + g];
             const float sp = kQScale * sc, cb = kBits == 4 ? __builtin_fmaf(-kQScale, sc, bi) : bi;
             bf16x8 bq[kKB];
 #pragma unroll
@@ -485,7 +493,10 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
             }
         }
     };
-    if (y_dtype == GDN_BF16)
+    if (partial) {
+        float* pp = partial + int64_t(split) * M * N;
+        store([&](int64_t i, float v) { pp[i] = v; });
+    } else if (y_dtype == GDN_BF16)
         store([&](int64_t i, float v) { static_cast<uint16_t*>(y)[i] = f32_to_bf16_bits(v); });
     else if (y_dtype == GDN_F16)
         store([&](int64_t i, float v) { static_cast<uint16_t*>(y)[i] = f32_to_f16_bits(v); });
@@ -493,14 +504,51 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         store([&](int64_t i, float v) { static_cast<float*>(y)[i] = v; });
 }
 
+// y = the sum, in split order, of the split-K kernel's S float32 blocks
+// partial[S][count].
+__global__ __launch_bounds__(256) void qlinear_split_sum_kernel(const float* __restrict__ partial, int splits,
+                                                                int64_t count, void* __restrict__ y, int y_dtype) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= count) return;
+    float v = partial[i];
+    for (int j = 1; j < splits; ++j) v += partial[j * count + i];
+    store_any(y, i, y_dtype, v);
+}
+
+constexpr int kCUs = 256;  // compute units of an MI355X
+
+// Split count for `tiles` column tiles of `ks` steps: the largest power of
+// two S <= 16 dividing ks whose k ranges hold whole 16-byte scale pieces of
+// each column, with at most one workgroup per CU (measured: beyond that the
+// partial blocks cost more than the extra workgroups gain) and S M N floats
+// in the workspace; 1 is no split.
+int decode_splits(int tiles, int ks, int K, int group_size, int per_piece, int M, int N, int64_t ws_bytes) {
+    int best = 1;
+    for (int sp = 2; sp <= 16 && ks % sp == 0; sp *= 2) {
+        const int gl = K / sp / group_size;
+        if (gl % per_piece != 0 || int64_t(tiles) * sp > kCUs || int64_t(sp) * M * N * 4 > ws_bytes) break;
+        best = sp;
+    }
+    return best;
+}
+
 template <int kBits, int kMT, int kSlice, int kCols, bool kXF32>
 int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
-                     void* y, int y_dtype, int M, int N, int K, int group_size, hipStream_t s) {
-    const dim3 grid(unsigned((N + kCols - 1) / kCols));
+                     void* y, int y_dtype, int M, int N, int K, int group_size, void* workspace,
+                     int64_t ws_bytes, hipStream_t s) {
+    const int tiles = (N + kCols - 1) / kCols, ks = K / (8 * kSlice);
+    const int splits = decode_splits(tiles, ks, K, group_size, sb_dtype == GDN_F32 ? 4 : 8, M, N,
+                                     workspace ? ws_bytes : 0);
+    float* partial = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    if (partial)
+        GDN_REQUIRE(!overlaps(partial, int64_t(splits) * M * N * 4, y, int64_t(M) * N * dtype_size(y_dtype)) &&
+                        !overlaps(partial, int64_t(splits) * M * N * 4, x, int64_t(M) * K * (kXF32 ? 4 : 2)),
+                    "gdn_quantized_matmul: workspace overlaps x or y");
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
 #define GDN_DEC(STEPS)                                                                              \
     hipLaunchKernelGGL((qlinear_decode_kernel<kBits, STEPS, kMT, kSlice, kCols, kXF32>), grid, dim3(512), 0, s, \
-                       x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size)
-    switch (K / (8 * kSlice)) {
+                       x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, partial)
+    switch (ks / splits) {
         case 1: GDN_DEC(1); break;
         case 2: GDN_DEC(2); break;
         case 4: GDN_DEC(4); break;
@@ -519,24 +567,40 @@ int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const
         default: return -1;
     }
 #undef GDN_DEC
+    if (int rc = check_launch("gdn_quantized_matmul")) return rc;
+    if (!partial) return 0;
+    const int64_t count = int64_t(M) * N;
+    hipLaunchKernelGGL(qlinear_split_sum_kernel, dim3(unsigned((count + 255) / 256)), dim3(256), 0, s, partial,
+                       splits, count, y, y_dtype);
     return check_launch("gdn_quantized_matmul");
 }
 
 // The k slice a wave takes per step: one whole group of 32, else 64 k.
 int decode_slice(int group_size) { return group_size == 32 ? 32 : 64; }
 
-// Whether the decode kernel takes this call (M <= 64 checked by the caller):
-// the step counts launch_decode_mt instantiates, the scale rows the LDS
-// holds, scales in whole 16-byte pieces of one column, aligned operands.
-bool decode_kernel_fits(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
-                        int N, int K, int bits, int group_size) {
+// Whether the decode kernel takes this shape (M <= 64 checked by the
+// caller): the step counts launch_decode_mt instantiates, the scale rows the
+// LDS holds, scales in whole 16-byte pieces of one column.
+bool decode_shape_fits(int sb_dtype, int K, int bits, int group_size) {
     const int slice = decode_slice(group_size), step = 8 * slice;
     const int ks = K / step, gpr = K / group_size, per_piece = sb_dtype == GDN_F32 ? 4 : 8;
     const int words_per_thread = ks * step * bits / 32 / 8;  // packed weight words each thread holds
     const bool steps_ok = K % step == 0 && (ks == 1 || ks == 2 || ks == 4 || ks == 8 || ks == 16) &&
                           words_per_thread <= 64;
+    return steps_ok && gpr <= kDecGroups && gpr % per_piece == 0;
+}
+
+// ... and these operands: 16-byte aligned.
+bool decode_kernel_fits(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
+                        int K, int bits, int group_size) {
     const auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    return steps_ok && gpr <= kDecGroups && gpr % per_piece == 0 && al(x) && al(w) && al(scales) && al(biases);
+    return decode_shape_fits(sb_dtype, K, bits, group_size) && al(x) && al(w) && al(scales) && al(biases);
+}
+
+// Columns per decode workgroup (the choice launch_decode makes).
+int decode_cols(bool x_f32, int mt, int bits, int group_size) {
+    const int narrow = bits == 4 && decode_slice(group_size) == 32 ? 64 : 32;
+    return (x_f32 ? mt == 1 : mt <= 2) ? narrow : 64;
 }
 
 // Up to 32 rows, workgroups of 32 columns where every thread still gets a
@@ -547,9 +611,9 @@ bool decode_kernel_fits(const void* x, const uint32_t* w, const void* scales, co
 // rows, 64 beyond.
 int launch_decode(const void* x, bool x_f32, const uint32_t* w, const void* scales, const void* biases,
                   int sb_dtype, void* y, int y_dtype, int M, int N, int K, int bits, int group_size,
-                  hipStream_t s) {
+                  void* workspace, int64_t ws_bytes, hipStream_t s) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-#define GDN_ARGS x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s
+#define GDN_ARGS x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, workspace, ws_bytes, s
 #define GDN_MT(BITS, SLICE, NARROW)                                                       \
     do {                                                                                  \
         if (x_f32) {                                                                      \
@@ -568,6 +632,15 @@ int launch_decode(const void* x, bool x_f32, const uint32_t* w, const void* scal
     GDN_MT(8, 64, 32);
 #undef GDN_MT
 #undef GDN_ARGS
+}
+
+// Workspace bytes launch_decode uses for a call (0: it does not split K).
+int64_t decode_workspace_bytes(bool x_f32, int sb_dtype, int M, int N, int K, int bits, int group_size) {
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4, slice = decode_slice(group_size);
+    const int cols = decode_cols(x_f32, mt, bits, group_size);
+    const int splits = decode_splits((N + cols - 1) / cols, K / (8 * slice), K, group_size,
+                                     sb_dtype == GDN_F32 ? 4 : 8, M, N, INT64_MAX);
+    return splits > 1 ? int64_t(splits) * M * N * 4 : 0;
 }
 
 template <int kBits, class SB, class O>
@@ -672,14 +745,28 @@ int check_quant_args(const char* fn, const void* w, const void* scales, const vo
 
 using namespace gdn;
 
+extern "C" int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype, int M, int N, int K, int bits,
+                                                       int group_size) {
+    const bool x_f32 = x_dtype == GDN_F32;
+    if (M < 1 || M > 64 || N < 1 || K < 1 || (bits != 4 && bits != 8) ||
+        (group_size != 32 && group_size != 64 && group_size != 128) || K % group_size != 0 ||
+        !valid_dtype(sb_dtype) || !(x_dtype == GDN_BF16 || (x_f32 && M <= 32)) ||
+        !decode_shape_fits(sb_dtype, K, bits, group_size))
+        return 0;
+    return decode_workspace_bytes(x_f32, sb_dtype, M, N, K, bits, group_size);
+}
+
 extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, const void* scales,
                                     const void* biases, int sb_dtype, void* y, int y_dtype, int M,
-                                    int N, int K, int bits, int group_size, void* stream) {
+                                    int N, int K, int bits, int group_size, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
     if (int rc = check_quant_args("gdn_quantized_matmul", w, scales, biases, sb_dtype, N, K, bits,
                                   group_size))
         return rc;
     GDN_REQUIRE(M >= 0, "gdn_quantized_matmul: bad M=%d", M);
     GDN_REQUIRE(valid_dtype(x_dtype) && valid_dtype(y_dtype), "gdn_quantized_matmul: bad dtype");
+    GDN_REQUIRE(workspace_bytes >= 0 && reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+                "gdn_quantized_matmul: workspace must be 16-byte aligned");
     const bool x_f32 = x_dtype == GDN_F32;
     if (x_dtype != GDN_BF16 && !(x_f32 && M <= 32))
         return fail(GDN_EUNSUPPORTED,
@@ -692,8 +779,9 @@ extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, c
                 "gdn_quantized_matmul: y overlaps x");
     hipStream_t s = as_stream(stream);
     const auto* wp = static_cast<const uint32_t*>(w);
-    if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, N, K, bits, group_size))
-        return launch_decode(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size, s);
+    if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, K, bits, group_size))
+        return launch_decode(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size,
+                             workspace, workspace_bytes, s);
     if (x_f32)
         return fail(GDN_EUNSUPPORTED, "gdn_quantized_matmul: float32 x needs a shape the decode kernel takes");
     if (bits == 4) return dispatch_sb<4>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);

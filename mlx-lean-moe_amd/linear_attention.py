@@ -151,7 +151,8 @@ def _index_array(values, n: int, device, check, name: str) -> torch.Tensor:
 
 def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias,
                       norm_weight, eps, dims: LinearAttentionDims, *, conv_out=None,
-                      state_out=None, y_dtype=None, slots=None, conv_half=None):
+                      state_out=None, y_dtype=None, slots=None, conv_half=None,
+                      conv_arrivals=None):
     """One decode token for ``B`` sequences in a single kernel launch: conv +
     SiLU + roll, q/k scaling, gates, recurrence and gated RMSNorm
     (linear_attention.py:103-124 at L = 1).
@@ -173,8 +174,10 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     the pool's two-half ``(2 P, K-1, C)`` array: slot ``s`` reads its conv
     state at row ``s + P * conv_half[s]`` and rolls it into the other half,
     so nothing is left to copy back (``conv_out`` must be ``conv_state`` or
-    None). The bits are read, not flipped: :meth:`RecurrentStatePool.advance`
-    flips them after the step. ``slots`` and ``conv_half`` given as host
+    None). The bits are read, not flipped (:meth:`RecurrentStatePool.advance`
+    flips them after the step), unless ``conv_arrivals`` is given as well:
+    the pool's ``P`` int32 counters, zero between steps, with which the
+    kernel flips the decoded slots' bits itself. ``slots`` and ``conv_half`` given as host
     sequences are checked on the host; given as int32 device tensors they
     are used as they are (no host round trip), and the caller guarantees the
     slots are distinct — the kernel itself still refuses slots outside the
@@ -208,6 +211,13 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
         half_t = _index_array(conv_half, P, device, lambda v: check_half_bits(v, P), "conv_half")
         conv_rows = 2 * P
         conv_out = conv_state
+    if conv_arrivals is not None:
+        if half_t is None or half_t is not conv_half:
+            raise ValueError("conv_arrivals needs conv_half as an int32 device tensor")
+        if (not isinstance(conv_arrivals, torch.Tensor) or conv_arrivals.device != device
+                or conv_arrivals.dtype != torch.int32 or conv_arrivals.shape != (P,)
+                or not conv_arrivals.is_contiguous()):
+            raise ValueError(f"conv_arrivals must be a contiguous int32 device tensor of {P} counters")
     if (tuple(qkv.shape) != (B, dims.conv_dim) or tuple(a.shape) != (B, dims.num_value_heads)
             or b.shape != a.shape
             or tuple(conv_state.shape) != (conv_rows, dims.conv_kernel_dim - 1, dims.conv_dim)
@@ -244,7 +254,7 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
               _lib.ptr(norm_weight), float(eps), _lib.ptr(out), _lib.dtype_code(out_dtype), B,
               dims.num_key_heads, dims.num_value_heads, dims.key_head_dim, dims.value_head_dim,
               dims.conv_kernel_dim, _lib.dtype_code(act), _lib.ptr(slot_t), P, _lib.ptr(half_t),
-              row_strides, _stream(device))
+              row_strides, _lib.ptr(conv_arrivals), _stream(device))
     return out, conv_out, state_out
 
 
@@ -399,16 +409,17 @@ class Qwen3_5LinearAttention:
         out, _, _ = fused_decode_step(
             qkv, z, a, b, pool.conv_buf, pool.ssm_state, self.conv1d_weight, self.A_log,
             self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_t,
-            conv_half=pool.conv_half_dev)
-        pool.advance(slot_list, slot_t)
+            conv_half=pool.conv_half_dev, conv_arrivals=pool.conv_arrivals)
+        pool.advance(slot_list, device_flipped=True)
         return self._proj(out.reshape(rows, d.value_dim), self.out_proj)
 
 
 class DecodeGraph:
     """One ``decode_batch`` step of ``layer`` for a fixed set of pool slots,
     captured in a HIP graph: a replay launches the step's kernels (the
-    stacked projection, the fused decode, out_proj and the flip of the
-    pool's conv half bits) without the host work of issuing them one by one.
+    stacked projection, the fused decode, which also flips the pool's conv
+    half bits, and out_proj) without the host work of issuing them one by
+    one.
 
     The graph reads ``self.x`` and writes ``self.out``; ``step(x)`` copies
     ``x`` into ``self.x`` (skip it by writing ``self.x`` directly), replays

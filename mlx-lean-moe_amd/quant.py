@@ -14,6 +14,8 @@ multiply on the vendor BLAS. Dense projections are ``x @ W.T``.
 
 from __future__ import annotations
 
+import functools
+
 from dataclasses import dataclass
 
 import torch
@@ -159,11 +161,24 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None)
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
     w, scales, biases = _c(w), _c(scales), _c(biases)
+    ws_bytes = workspace_bytes(x2.dtype, scales.dtype, M, N, K, quant.bits, quant.group_size)
+    # a transient from the caching allocator (graph-capture safe); the split
+    # kernels overwrite what they read
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     _lib.call("gdn_quantized_matmul", _lib.ptr(x2), _lib.dtype_code(x2.dtype), _lib.ptr(w), _lib.ptr(scales),
               _lib.ptr(biases), _lib.dtype_code(scales.dtype), _lib.ptr(y),
-              _lib.dtype_code(y.dtype), M, N, K, quant.bits, quant.group_size,
-              _lib.stream_ptr(x.device))
+              _lib.dtype_code(y.dtype), M, N, K, quant.bits, quant.group_size, _lib.ptr(ws),
+              ws_bytes, _lib.stream_ptr(x.device))
     return y.reshape(*lead, N)
+
+
+@functools.lru_cache(maxsize=256)
+def workspace_bytes(x_dtype: torch.dtype, sb_dtype: torch.dtype, M: int, N: int, K: int, bits: int,
+                    group_size: int) -> int:
+    """Workspace gdn_quantized_matmul splits K with for these sizes (0: none)."""
+
+    return int(_lib.load().gdn_quantized_matmul_workspace_size(
+        _lib.dtype_code(x_dtype), _lib.dtype_code(sb_dtype), M, N, K, bits, group_size))
 
 
 def concat_quantized(parts: list[dict]) -> dict:

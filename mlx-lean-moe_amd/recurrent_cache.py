@@ -48,8 +48,9 @@ class RecurrentStatePool:
     slot ``s`` currently lives in row ``s + B * conv_half[s]``; a decode reads
     that row and writes the rolled state into the slot's other half, then
     the slot's half flips (no copy, and slots decode independently). The
-    bits live on the device (``conv_half_dev``, read by the decode kernel and
-    flipped by ``advance`` in one launch) with a host copy (``conv_half``)
+    bits live on the device (``conv_half_dev``, read by the decode kernel,
+    which also flips them with the help of the zeroed ``conv_arrivals``
+    counters, or flipped by ``advance``) with a host copy (``conv_half``)
     for host-side reads."""
 
     def __init__(self, batch: int, conv_kernel_dim: int, conv_dim: int, num_value_heads: int,
@@ -59,6 +60,7 @@ class RecurrentStatePool:
                                     device=device)
         self.conv_half = torch.zeros(batch, dtype=torch.int64)
         self.conv_half_dev = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.conv_arrivals = torch.zeros(batch, dtype=torch.int32, device=device)
         self._slot_sets: dict[tuple[int, ...], torch.Tensor] = {}
         self.ssm_state = torch.zeros((batch, num_value_heads, value_head_dim, key_head_dim),
                                      dtype=torch.float32, device=device)
@@ -91,13 +93,18 @@ class RecurrentStatePool:
             t = self._slot_sets[key] = host.to(self.ssm_state.device, non_blocking=True)
         return t
 
-    def advance(self, slots: list[int], slot_t: torch.Tensor | None = None) -> None:
+    def advance(self, slots: list[int], slot_t: torch.Tensor | None = None, *,
+                device_flipped: bool = False) -> None:
         """After a decode of ``slots`` (distinct; ``slot_t`` the same as an
         int32 device array, if the caller has it): their conv state now lives
-        in the other half, and each holds one more token."""
+        in the other half, and each holds one more token. ``device_flipped``:
+        the decode kernel has flipped the device bits already (it was given
+        ``conv_arrivals``); only the host copy and sizes change."""
         idx = torch.tensor(slots, dtype=torch.int64)
         self.conv_half[idx] ^= 1
         self.size[idx] += 1
+        if device_flipped:
+            return
         if slot_t is None:
             slot_t = self.device_slots(slots)
         device = self.conv_half_dev.device

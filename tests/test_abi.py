@@ -54,7 +54,7 @@ def test_invalid_arguments_return_einval_without_launching():
     assert rc == _lib.GDN_EINVAL and "divisible" in _err(lib)
     # the fused decode kernel is specialised for Dk = Dv = 128
     rc = lib.gdn_decode_step(*([None] * 12), 1e-6, None, 0, 1, 2, 4, 64, 64, 4, 1, None, 0, None,
-                             None, None)
+                             None, None, None)
     assert rc == _lib.GDN_EUNSUPPORTED
     # row strides below a row's width, and conv_half with two conv arrays
     fake = [ctypes.c_void_p(1 << (20 + i)) for i in range(12)]
@@ -64,7 +64,8 @@ def test_invalid_arguments_return_einval_without_launching():
                                     ((C, 256, 2, 1), fake[1], "row stride 3"),
                                     ((C, 256, 2, 2), fake[2], "one array")):
         rc = lib.gdn_decode_step(fake[0], fake[1], conv_out, *fake[3:12], 1e-6, fake[11], 0, 1, 1, 2,
-                                 128, 128, 4, 1, slots, 4, slots, (ctypes.c_int64 * 4)(*strides), None)
+                                 128, 128, 4, 1, slots, 4, slots, (ctypes.c_int64 * 4)(*strides), None,
+                                 None)
         assert rc == _lib.GDN_EINVAL and what in _err(lib), (what, _err(lib))
     # overlapping conv state buffers are rejected
     p = ctypes.c_void_p(4096)
@@ -76,3 +77,26 @@ def test_empty_work_is_a_no_op():
     lib = _lib.load()
     assert lib.gdn_gates(None, None, 0, None, None, None, None, 0, 0, 4, None) == 0
     assert lib.gdn_gated_rmsnorm(None, 0, None, 0, None, 1e-6, None, 0, 0, 8, None) == 0
+
+
+def test_quantized_matmul_workspace_size():
+    """K is split only where the decode kernel runs few column tiles: the
+    layer's out_proj (N = 2048: 32 tiles of 64 columns at 64 rows) takes 8
+    splits of float32 (M, N) blocks, the stacked input projection (N =
+    12352) none; shapes the decode kernel does not take need none."""
+
+    lib = _lib.load()
+    size = lambda *a: lib.gdn_quantized_matmul_workspace_size(*a)
+    bf, f32 = _lib.GDN_BF16, _lib.GDN_F32
+    assert size(bf, bf, 64, 2048, 4096, 4, 64) == 8 * 64 * 2048 * 4
+    assert size(bf, bf, 1, 2048, 4096, 4, 64) == 4 * 2048 * 4     # 64 tiles of 32 columns
+    assert size(bf, bf, 64, 12352, 2048, 4, 64) == 0
+    assert size(f32, bf, 5, 300, 1024, 4, 32) == 4 * 5 * 300 * 4  # 4 steps: at most 4 splits
+    assert size(bf, bf, 65, 2048, 4096, 4, 64) == 0                # tiled kernel
+    assert size(f32, bf, 33, 2048, 4096, 4, 64) == 0               # float32 x beyond 32 rows
+    assert size(bf, bf, 64, 2048, 4160, 4, 64) == 0                # not whole steps
+    # a misaligned workspace is refused before anything runs
+    p = ctypes.c_void_p(1 << 30)
+    rc = lib.gdn_quantized_matmul(p, bf, p, p, p, bf, ctypes.c_void_p(1 << 31), bf, 1, 64, 512, 4, 64,
+                                  ctypes.c_void_p((1 << 32) + 8), 1024, None)
+    assert rc == _lib.GDN_EINVAL and "workspace" in _err(lib)

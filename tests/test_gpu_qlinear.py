@@ -73,7 +73,7 @@ def test_quantized_matmul_matches_oracle(gpu, M, N, K, bits, gs, sb):
     y32 = torch.empty(M, N, device=gpu)
     _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.GDN_BF16, _lib.ptr(W["weight"]),
               _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
-              _lib.ptr(y32), _lib.GDN_F32, M, N, K, bits, gs, _lib.stream_ptr(xt.device))
+              _lib.ptr(y32), _lib.GDN_F32, M, N, K, bits, gs, None, 0, _lib.stream_ptr(xt.device))
     err = np.abs(y32.cpu().numpy() - ref).max()
     assert err <= 1e-5 * np.abs(ref).max() + 1e-6, err
 
@@ -101,7 +101,52 @@ def test_float32_activations_on_the_decode_kernel(gpu, M, N, K, bits, gs, sb):
     assert _lib.load().gdn_quantized_matmul(
         None, _lib.GDN_F32, _lib.ptr(W["weight"]), _lib.ptr(W["scales"]), _lib.ptr(W["biases"]),
         _lib.dtype_code(W["scales"].dtype), None, _lib.GDN_F32, 33, N, K, bits, gs,
-        None) == _lib.GDN_EUNSUPPORTED
+        None, 0, None) == _lib.GDN_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,sb,x32,splits", [
+    (64, 2048, 4096, 4, 64, "bf16", False, 8),   # the layer's out_proj: 32 column tiles
+    (16, 2048, 4096, 4, 64, "bf16", False, 4),
+    (1, 1000, 2048, 8, 32, "f16", False, 8),     # ragged last tile
+    (40, 100, 4096, 4, 64, "f32", False, 8),
+    (5, 300, 1024, 4, 32, "bf16", True, 4),      # float32 x
+])
+def test_split_k_matches_the_unsplit_kernel_and_the_oracle(gpu, M, N, K, bits, gs, sb, x32, splits):
+    """Few column tiles: with the workspace the decode kernel splits K over
+    workgroups (float32 partial blocks, added in a fixed order). Both the
+    split and the unsplit result meet the oracle's bound, they agree to
+    float32 rounding, and two split runs agree bit for bit."""
+
+    rng = np.random.default_rng(M * 31 + N)
+    words, s, b = _weights(rng, N, K, bits, gs, sb)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if not x32:
+        x = R.bf16_round(x)
+    ref = Q.quantized_matmul(x, words, s, b, bits, gs, w_round="f32")
+    W = _dev_weights(gpu, words, s, b, sb)
+    xdt = torch.float32 if x32 else torch.bfloat16
+    xt = torch.tensor(x, device=gpu).to(xdt)
+    lib = _lib.load()
+    ws_bytes = lib.gdn_quantized_matmul_workspace_size(_lib.dtype_code(xdt), _lib.dtype_code(_TORCH[sb]),
+                                                       M, N, K, bits, gs)
+    assert ws_bytes == splits * M * N * 4
+    ws = torch.full((ws_bytes // 4,), float("nan"), device=gpu)  # every partial is written
+    outs = []
+    for w_ptr, w_len in ((None, 0), (_lib.ptr(ws), ws_bytes), (_lib.ptr(ws), ws_bytes),
+                         (_lib.ptr(ws), ws_bytes // 2)):
+        y = torch.empty(M, N, device=gpu)
+        _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.dtype_code(xdt), _lib.ptr(W["weight"]),
+                  _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
+                  _lib.ptr(y), _lib.GDN_F32, M, N, K, bits, gs, w_ptr, w_len, _lib.stream_ptr(gpu))
+        outs.append(y.cpu().numpy())
+    tol = (1e-4 if x32 else 1e-5) * np.abs(ref).max() + 1e-6
+    for y in outs:
+        assert np.abs(y - ref).max() <= tol
+    assert np.array_equal(outs[1], outs[2])
+    assert np.abs(outs[1] - outs[0]).max() <= 1e-5 * np.abs(ref).max() + 1e-6
+    # through quantized_linear (its own workspace), in x's dtype
+    y = gdn.quantized_linear(xt, W, gdn.QuantScheme(bits, gs))
+    np.testing.assert_array_equal(y.float().cpu().numpy(), torch.tensor(outs[1]).to(xdt).float().numpy())
 
 
 @pytest.mark.parametrize("bits,gs,sb,out", [(4, 64, "bf16", "bf16"), (8, 32, "f16", "f32"),

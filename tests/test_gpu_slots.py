@@ -86,6 +86,24 @@ def test_conv_half_rolls_into_the_other_half_without_a_copy(gpu):
         assert torch.equal(buf[r], written[r] if r in written else before[r]), r
     assert torch.equal(c["state"][idx], ref_state)
     assert half.tolist() == bits
+    # with the arrival counters the kernel flips the decoded slots' bits, and
+    # a second step reads the halves the first one wrote
+    half[4] = 1  # the step above left slot 4 in half 1 and slot 1 in half 0
+    half[1] = 0
+    arrivals = torch.zeros(P, dtype=torch.int32, device=gpu)
+    state2 = c["state"].clone()
+    out2, _, _ = gdn.fused_decode_step(
+        c["qkv"], c["z"], c["a"], c["b"], buf, state2, c["conv_w"], c["A_log"], c["dt_bias"],
+        c["norm_w"], 1e-6, DIMS, slots=slots, conv_half=half, conv_arrivals=arrivals)
+    assert half.tolist() == bits and not arrivals.any()
+    ref2 = gdn.fused_decode_step(c["qkv"], c["z"], c["a"], c["b"], ref_conv.clone(), ref_state.clone(),
+                                 c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS)
+    assert torch.equal(out2, ref2[0])
+    assert torch.equal(buf[4], ref2[1][0]) and torch.equal(buf[1 + P], ref2[1][1])
+    with pytest.raises(ValueError, match="conv_arrivals"):
+        gdn.fused_decode_step(c["qkv"], c["z"], c["a"], c["b"], buf, c["state"], c["conv_w"],
+                              c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS, slots=slots,
+                              conv_half=bits, conv_arrivals=arrivals)
     for bad, conv_out in (([0, 2, 0, 0, 0, 0], None), ([0, 1], None), (bits, buf.clone())):
         with pytest.raises(ValueError):
             gdn.fused_decode_step(c["qkv"], c["z"], c["a"], c["b"], buf, c["state"], c["conv_w"],
@@ -149,7 +167,7 @@ def test_slot_outside_pool_touches_no_state(gpu):
               _lib.ptr(c["conv_w"].reshape(DIMS.conv_dim, 4).contiguous()), _lib.ptr(c["a"]),
               _lib.ptr(c["b"]), _lib.ptr(c["A_log"]), _lib.ptr(c["dt_bias"]), _lib.ptr(c["state"]),
               _lib.ptr(c["state"]), None, None, 1e-6, _lib.ptr(out), _lib.GDN_F32, B, 2, 4, 128,
-              128, 4, _lib.GDN_BF16, _lib.ptr(slots), P, None, None, _lib.stream_ptr(gpu))
+              128, 4, _lib.GDN_BF16, _lib.ptr(slots), P, None, None, None, _lib.stream_ptr(gpu))
     torch.cuda.synchronize()
     assert torch.isnan(out[0]).all() and torch.isfinite(out[1]).all()
     assert torch.equal(c["state"][0], before[0]) and torch.equal(c["state"][2:], before[2:])
@@ -179,6 +197,10 @@ def test_pooled_decode_after_chunked_prefill_matches_per_sequence_calls(gpu):
         out = layer.decode_batch(x, pool, slots=active)
         ref = torch.stack([layer(x[i], caches[slots.index(s)]) for i, s in enumerate(active)])
         torch.testing.assert_close(out.float(), ref.float(), rtol=0, atol=0)
+        # the decode kernel flipped the decoded slots' bits itself and left
+        # its arrival counters at zero
+        assert pool.conv_half_dev.cpu().tolist() == pool.conv_half.tolist()
+        assert not pool.conv_arrivals.any()
     for slot, cache in zip(slots, caches):
         torch.testing.assert_close(pool.ssm_state[slot], cache.ssm_state, rtol=0, atol=0)
         torch.testing.assert_close(pool.conv_state[slot], cache.conv_state, rtol=0, atol=0)
