@@ -242,7 +242,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     constexpr int kXS = kStep + 8;               // bf16 row stride of the x tile
     constexpr int kWPC = kStep * kBits / 32;     // packed words of one column per step
     constexpr int kWS = kWPC + 4;                // word row stride of the weight tile
-    constexpr int kXLoads = kRows * kStep / 8 / 512;   // 16-byte x chunks per thread per step
+    constexpr int kXLoads = kRows * kStep / 8 / 512;   // 8-element x chunks per thread per step
     constexpr int kWLoads = kCols * kWPC / 4 / 512;    // 16-byte weight pieces per thread per step
     // float32 x is staged as two bf16 tiles, hi = bf16(x) and lo =
     // bf16(x - hi) (together x to ~16 significant bits), each fragment
@@ -251,13 +251,17 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     constexpr int kXBytes = kXParts * kRows * kXS * 2;
     constexpr int kWBytes = kCols * kWS * 4;
     constexpr int kPBytes = 4 * kMT * kTN * 64 * 16;  // 4 partial blocks of kMT x kTN tiles of float4 per lane
-    constexpr int kSBRow = kCols * (kDecGroups + 1);
+    // a group spans at least one slice, so the k range holds at most
+    // 8 kSteps groups (and at most kDecGroups, the host's limit)
+    constexpr int kGroups = 8 * kSteps < kDecGroups ? 8 * kSteps : kDecGroups;
+    constexpr int kSBRow = kCols * (kGroups + 1);
     constexpr int kSBBytes = 2 * kSBRow * 4;
     // double-buffered tiles (one barrier per step) where the LDS holds them,
     // for two workgroups per CU with 32 columns
     constexpr int kBudget = kCols == 32 ? 80 * 1024 : 160 * 1024;
     constexpr int kBufs = 2 * (kXBytes + kWBytes) + kSBBytes <= kBudget ? 2 : 1;
     constexpr int kMain = kBufs * (kXBytes + kWBytes) > kPBytes ? kBufs * (kXBytes + kWBytes) : kPBytes;
+    constexpr int kBQ = (kSteps + 3) / 4;        // bias MFMAs (four of a wave's slices each) per tile
     static_assert(kXLoads >= 1 && kWLoads >= 1, "step too small for 512 threads");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kMain];
     __shared__ float sbs[2 * kSBRow];
@@ -268,45 +272,63 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, lr = l & 15, lq = l >> 4;
     const int n0 = blockIdx.x * kCols;
     const int gpr = K / group_size;
-    const int64_t wpr = int64_t(K) * kBits / 32;
     // this workgroup's k range: split blockIdx.y, kSteps steps from k0, whose
     // gl groups start at group split gl of each column
     const int split = blockIdx.y, k0 = split * kSteps * kStep, gl = kSteps * kStep / group_size;
 
+    // Operands are read with buffer loads: a 32-bit per-thread offset that
+    // stays fixed over the steps (rows clamped to M - 1, columns to N - 1;
+    // their outputs are not stored) plus a uniform offset in an SGPR.
+    // Sizes below 2^31 bytes are checked by the host.
+    constexpr int kRaw = 0x00020000;  // buffer resource word 3 of a raw buffer
+    const int esx = kXF32 ? 4 : 2, esz = sb_dtype == GDN_F32 ? 4 : 2;
+    const int wpr4 = K * kBits / 8;  // bytes of one weight row
+    const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(xp), 0, M * K * esx, kRaw);
+    const auto wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(w), 0, N * wpr4, kRaw);
+    const auto sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(scales), 0, N * gpr * esz, kRaw);
+    const auto br = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(biases), 0, N * gpr * esz, kRaw);
+
     // Scales and biases of the range's groups of the kCols columns, in
-    // 16-byte pieces (a piece holds groups of one column), at most 4 per
-    // thread. Columns >= N (whose outputs are not stored) read column N - 1;
-    // threads past the last piece repeat it.
-    const int esz = sb_dtype == GDN_F32 ? 4 : 2, per_piece = 16 / esz;
-    const int ppc = gl / per_piece;  // pieces per column
+    // 16-byte pieces (a piece holds groups of one column): piece p of either
+    // array is piece p % ppc of column p / ppc; thread t takes pieces t and
+    // t + 512 of both (ppc and per_piece are powers of two).
+    const int per_piece = 16 / esz, ppc = gl / per_piece, ppc_shift = __builtin_ctz(ppc);
     const int span_pieces = kCols * ppc;
-    u32x4 pv[4];
-    int pdst[4];
-    const int sb_rounds = (2 * span_pieces + 511) / 512;  // pieces per thread, at most 4
+    u32x4 sv[2], bv[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int p = tid + 512 * i;
-        p = p < 2 * span_pieces ? p : 2 * span_pieces - 1;
-        const int which = p >= span_pieces, o = p - which * span_pieces;
-        const int c = o / ppc, pc = o - c * ppc;
-        const int64_t col = n0 + c < N ? n0 + c : N - 1;
-        pv[i] = reinterpret_cast<const u32x4*>(which ? biases : scales)[(col * gpr + int64_t(split) * gl) / per_piece + pc];
-        pdst[i] = which * kSBRow + c * (gl + 1) + pc * per_piece;
+    for (int i = 0; i < 2; ++i) {
+        const int p = tid + 512 * i;
+        if (p < span_pieces) {
+            const int c = p >> ppc_shift, pc = p & (ppc - 1);
+            const int col = n0 + c < N ? n0 + c : N - 1;
+            const int off = col * gpr * esz + 16 * pc, soff = split * gl * esz;
+            sv[i] = __builtin_amdgcn_raw_buffer_load_b128(sr, off, soff, 0);
+            bv[i] = __builtin_amdgcn_raw_buffer_load_b128(br, off, soff, 0);
+        }
     }
 
-    // x chunk p = tid + 512 i of a step: row p / (kStep / 8) (clamped to
-    // M - 1), k 8 (p % (kStep / 8)) .. +7
+    constexpr int kChunksPerRow = kStep / 8, kXRowStep = 512 / kChunksPerRow;
     typedef float f32x8 __attribute__((ext_vector_type(8)));
     using xchunk_t = std::conditional_t<kXF32, f32x8, u16x8>;
-    using xelem_t = std::conditional_t<kXF32, float, uint16_t>;
-    const xelem_t* x = static_cast<const xelem_t*>(xp);
+    int xoffs[kXLoads];
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) {
+        const int r = tid / kChunksPerRow + i * kXRowStep;
+        xoffs[i] = ((r < M ? r : M - 1) * K + 8 * (tid % kChunksPerRow)) * esx;
+    }
     xchunk_t xv[kXLoads];
     auto fetch_x = [&](int s) {
+        const int soff = (k0 + kStep * s) * esx;
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
-            const int p = tid + 512 * i, r = p / (kStep / 8), ch = p % (kStep / 8);
-            const int row = r < M ? r : M - 1;
-            xv[i] = *reinterpret_cast<const xchunk_t*>(x + int64_t(row) * K + k0 + kStep * s + 8 * ch);
+            const int o = xoffs[i];
+            if constexpr (kXF32) {
+                const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(xr, o, soff, 0);
+                const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(xr, o + 16, soff, 0);
+                xv[i] = __builtin_bit_cast(f32x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            } else {
+                xv[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, o, soff, 0));
+            }
         }
     };
     // 4-bit fragments pair codes i and i + 4 of a word: stage each chunk in
@@ -318,7 +340,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     auto stage_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
-            const int p = tid + 512 * i, r = p / (kStep / 8), ch = p % (kStep / 8);
+            const int r = tid / kChunksPerRow + i * kXRowStep, ch = tid % kChunksPerRow;
             uint16_t* dst = &xs(buf)[r * kXS + 8 * ch];
             if constexpr (kXF32) {
                 bf16x8 hi, lo;
@@ -336,41 +358,56 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     };
     fetch_x(0);
 
-    // packed weights of every step: piece p = tid + 512 i of a step's
-    // kCols x kWPC words is 16-byte piece p % (kWPC / 4) of column p / (kWPC / 4)
-    u32x4 wq[kSteps][kWLoads];
+    // packed weights of every step: piece i of a step is 16-byte piece wpc of
+    // column wc0 + i kWColStep (clamped)
+    constexpr int kPiecesPerCol = kWPC / 4, kWColStep = 512 / kPiecesPerCol;
+    const int wc0 = tid / kPiecesPerCol, wpc = tid % kPiecesPerCol;
+    int woff[kWLoads];
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s)
+    for (int i = 0; i < kWLoads; ++i) {
+        const int col = n0 + wc0 + i * kWColStep;
+        woff[i] = (col < N ? col : N - 1) * wpr4 + 16 * wpc;
+    }
+    // the first kPre steps' pieces are requested now (all of them where 32
+    // registers hold them; 16 for the 16-step kernels, whose unrolled loop
+    // holds more), each later step's when its slot is staged
+    constexpr int kWRegPieces = kSteps >= 16 ? 4 : 8;
+    constexpr int kPre = kWRegPieces / kWLoads < kSteps ? (kWRegPieces / kWLoads > 0 ? kWRegPieces / kWLoads : 1) : kSteps;
+    u32x4 wq[kPre][kWLoads];
+    auto load_w = [&](int s) {
 #pragma unroll
-        for (int i = 0; i < kWLoads; ++i) {
-            const int p = tid + 512 * i, c = p / (kWPC / 4), pc = p % (kWPC / 4);
-            const int64_t col = n0 + c < N ? n0 + c : N - 1;
-            wq[s][i] = *reinterpret_cast<const u32x4*>(w + col * wpr + int64_t(k0) * kBits / 32 + kWPC * s + 4 * pc);
-        }
+        for (int i = 0; i < kWLoads; ++i)
+            wq[s % kPre][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[i], (k0 * kBits / 8) + 4 * kWPC * s, 0);
+    };
+#pragma unroll
+    for (int s = 0; s < kPre; ++s) load_w(s);
     auto stage_w = [&](int buf, int s) {
 #pragma unroll
-        for (int i = 0; i < kWLoads; ++i) {
-            const int p = tid + 512 * i, c = p / (kWPC / 4), pc = p % (kWPC / 4);
-            *reinterpret_cast<u32x4*>(&ws(buf)[c * kWS + 4 * pc]) = wq[s][i];
-        }
+        for (int i = 0; i < kWLoads; ++i)
+            *reinterpret_cast<u32x4*>(&ws(buf)[(wc0 + i * kWColStep) * kWS + 4 * wpc]) = wq[s % kPre][i];
+        if (s + kPre < kSteps) load_w(s + kPre);
     };
 
-    // scales and biases to float, [which][column][group] with rows of gl + 1;
-    // only threads holding a piece store it (the repeats would pile onto
-    // one LDS address)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (i >= sb_rounds || tid + 512 * i >= 2 * span_pieces) break;
-        float* d = sbs + pdst[i];
+    // scales and biases to float, [which][column][group] with rows of gl + 1
+    auto to_float = [&](u32x4 v, float* d) {
         if (sb_dtype == GDN_F32) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) d[j] = __uint_as_float(pv[i][j]);
+            for (int j = 0; j < 4; ++j) d[j] = __uint_as_float(v[j]);
         } else if (sb_dtype == GDN_BF16) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) d[j] = __uint_as_float((j & 1) ? pv[i][j >> 1] & 0xFFFF0000u : pv[i][j >> 1] << 16);
+            for (int j = 0; j < 8; ++j) d[j] = __uint_as_float((j & 1) ? v[j >> 1] & 0xFFFF0000u : v[j >> 1] << 16);
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) d[j] = f16_bits_to_f32(uint16_t(pv[i][j >> 1] >> (16 * (j & 1))));
+            for (int j = 0; j < 8; ++j) d[j] = f16_bits_to_f32(uint16_t(v[j >> 1] >> (16 * (j & 1))));
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int p = tid + 512 * i;
+        if (p < span_pieces) {
+            const int c = p >> ppc_shift, pc = p & (ppc - 1);
+            to_float(sv[i], sbs + c * (gl + 1) + pc * per_piece);
+            to_float(bv[i], sbs + kSBRow + c * (gl + 1) + pc * per_piece);
         }
     }
 
@@ -379,6 +416,13 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     for (int tm = 0; tm < kMT; ++tm)
 #pragma unroll
         for (int tn = 0; tn < kTN; ++tn) acc[tm][tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // xa[q][tm]: the row sum X of row 16 tm + lr over this wave's slice of
+    // step 4 q + lq, the A operand of the bias MFMAs
+    float xa[kBQ][kMT];
+#pragma unroll
+    for (int q = 0; q < kBQ; ++q)
+#pragma unroll
+        for (int tm = 0; tm < kMT; ++tm) xa[q][tm] = 0.f;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     bf16x8 ones;
 #pragma unroll
@@ -386,30 +430,31 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     constexpr float kQScale = kBits == 4 ? 16.f : 1.f;  // P = kQScale (P' - X) for 4-bit codes
     const CodeConsts kc = code_consts();
 
-    // wave wv's slice of step s from tile buffer buf
+    // wave wv's slice of step s from tile buffer buf: acc += kQScale s P'
     auto compute = [&](int buf, int s) {
         const uint16_t* xb = xs(buf);
         const uint32_t* wb = ws(buf);
         const int g = (kStep * s + kSlice * wv) / group_size;
         bf16x8 a[kXParts][kMT][kKB];
-        f32x4 X[kMT];
 #pragma unroll
         for (int tm = 0; tm < kMT; ++tm) {
-            X[tm] = zero;
+            // ones times the x fragment as the B operand: every element of
+            // lane (r, *) is the sum of row 16 tm + r over the slice
+            f32x4 X = zero;
 #pragma unroll
             for (int h = 0; h < kXParts; ++h)
 #pragma unroll
                 for (int kb = 0; kb < kKB; ++kb) {
                     a[h][tm][kb] = *reinterpret_cast<const bf16x8*>(
                         &xb[(h * kRows + 16 * tm + lr) * kXS + kSlice * wv + 32 * kb + 8 * lq]);
-                    X[tm] = mfma_bf16(a[h][tm][kb], ones, X[tm]);
+                    X = mfma_bf16(ones, a[h][tm][kb], X);
                 }
+            if (lq == (s & 3)) xa[s / 4][tm] = X[0];
         }
 #pragma unroll
         for (int tn = 0; tn < kTN; ++tn) {
             const int c = 16 * tn + lr;
-            const float sc = sbs[c * (gl + 1) + g], bi = sbs[kSBRow + c * (gl + 1) + g];
-            const float sp = kQScale * sc, cb = kBits == 4 ? __builtin_fmaf(-kQScale, sc, bi) : bi;
+            const float sp = kQScale * sbs[c * (gl + 1) + g];
             bf16x8 bq[kKB];
 #pragma unroll
             for (int kb = 0; kb < kKB; ++kb)
@@ -422,8 +467,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
 #pragma unroll
                     for (int kb = 0; kb < kKB; ++kb) P = mfma_bf16(a[h][tm][kb], bq[kb], P);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[tm][tn][i] = __builtin_fmaf(cb, X[tm][i], __builtin_fmaf(sp, P[i], acc[tm][tn][i]));
+                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = __builtin_fmaf(sp, P[i], acc[tm][tn][i]);
             }
         }
     };
@@ -454,6 +498,30 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
             compute(0, s);
         }
         __syncthreads();
+    }
+
+    // The bias terms of the wave's slices: acc += X b' summed over the
+    // slices, b' = b - 16 s for 4-bit codes (undoing their 1 + q / 16
+    // offset) and b for 8-bit ones,
+    // as v_mfma_f32_16x16x4f32 with A[row][j] = X of step 4 q + j and
+    // B[j][column] = b' of that step's group (the sbs rows are
+    // still intact: only the tile region of the LDS is reused below).
+#pragma unroll
+    for (int q = 0; q < kBQ; ++q) {
+        const int st = 4 * q + lq;
+        const int g = (kStep * st + kSlice * wv) / group_size;
+#pragma unroll
+        for (int tn = 0; tn < kTN; ++tn) {
+            const int c = 16 * tn + lr;
+            float bb = 0.f;
+            if (st < kSteps) {
+                bb = sbs[kSBRow + c * (gl + 1) + g];
+                if constexpr (kBits == 4) bb = __builtin_fmaf(-kQScale, sbs[c * (gl + 1) + g], bb);
+            }
+#pragma unroll
+            for (int tm = 0; tm < kMT; ++tm)
+                acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[q][tm], bb, acc[tm][tn], 0, 0, 0);
+        }
     }
 
     // Sum of the 8 waves' blocks: waves 4-7 hand theirs to waves 0-3, which
@@ -581,20 +649,21 @@ int decode_slice(int group_size) { return group_size == 32 ? 32 : 64; }
 // Whether the decode kernel takes this shape (M <= 64 checked by the
 // caller): the step counts launch_decode_mt instantiates, the scale rows the
 // LDS holds, scales in whole 16-byte pieces of one column.
-bool decode_shape_fits(int sb_dtype, int K, int bits, int group_size) {
+bool decode_shape_fits(int sb_dtype, int N, int K, int bits, int group_size) {
     const int slice = decode_slice(group_size), step = 8 * slice;
     const int ks = K / step, gpr = K / group_size, per_piece = sb_dtype == GDN_F32 ? 4 : 8;
     const int words_per_thread = ks * step * bits / 32 / 8;  // packed weight words each thread holds
     const bool steps_ok = K % step == 0 && (ks == 1 || ks == 2 || ks == 4 || ks == 8 || ks == 16) &&
                           words_per_thread <= 64;
-    return steps_ok && gpr <= kDecGroups && gpr % per_piece == 0;
+    // 32-bit buffer offsets: the packed weights under 2^31 bytes
+    return steps_ok && gpr <= kDecGroups && gpr % per_piece == 0 && int64_t(N) * K * bits / 8 < (int64_t(1) << 31);
 }
 
 // ... and these operands: 16-byte aligned.
 bool decode_kernel_fits(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
-                        int K, int bits, int group_size) {
+                        int N, int K, int bits, int group_size) {
     const auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    return decode_shape_fits(sb_dtype, K, bits, group_size) && al(x) && al(w) && al(scales) && al(biases);
+    return decode_shape_fits(sb_dtype, N, K, bits, group_size) && al(x) && al(w) && al(scales) && al(biases);
 }
 
 // Columns per decode workgroup (the choice launch_decode makes).
@@ -751,7 +820,7 @@ extern "C" int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype
     if (M < 1 || M > 64 || N < 1 || K < 1 || (bits != 4 && bits != 8) ||
         (group_size != 32 && group_size != 64 && group_size != 128) || K % group_size != 0 ||
         !valid_dtype(sb_dtype) || !(x_dtype == GDN_BF16 || (x_f32 && M <= 32)) ||
-        !decode_shape_fits(sb_dtype, K, bits, group_size))
+        !decode_shape_fits(sb_dtype, N, K, bits, group_size))
         return 0;
     return decode_workspace_bytes(x_f32, sb_dtype, M, N, K, bits, group_size);
 }
@@ -779,7 +848,7 @@ extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, c
                 "gdn_quantized_matmul: y overlaps x");
     hipStream_t s = as_stream(stream);
     const auto* wp = static_cast<const uint32_t*>(w);
-    if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, K, bits, group_size))
+    if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, N, K, bits, group_size))
         return launch_decode(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size,
                              workspace, workspace_bytes, s);
     if (x_f32)
