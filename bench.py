@@ -13,9 +13,10 @@ Also measured in the same run (reported under "also"):
   prefill:      B=1, T=4096 chunked prefill (bf16 MFMA)
   prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
   decode_slots: B=64 active sequences at random slots of a 256-sequence pool
-  (--workload layer_decode: the whole layer with 4-bit projections, alone)
+  (--workload layer_decode: the whole layer with 4-bit projections, alone,
+  --batch B active sequences, 64 by default)
 
-python bench.py [--steps K] [--warmup W]
+python bench.py [--steps K] [--warmup W] [--batch B]
                 [--workload decode|decode_large|decode_slots|layer_decode|prefill|prefill_varlen|qlinear|copy]
 """
 
@@ -230,17 +231,37 @@ def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
     # the same steps replayed from HIP graphs (one per slot set)
     graphs = [gdn.DecodeGraph(layer, pool, sets[i], xs[i]) for i in range(4)]
     graph_ms, _ = time_steps(lambda s_: graphs[s_ % 4].step(), steps, warmup)
+    # the two projections alone, 20 calls a graph (device time, not the
+    # host's launch rate)
     x = xs[0]
-    in_ms, _ = time_steps(lambda s_: layer._project(x), steps, warmup)
     o = rnd(B, d.value_dim).to(torch.bfloat16)
-    out_ms, _ = time_steps(lambda s_: gdn.quantized_linear(o, layer.out_proj), steps, warmup)
+
+    def graph_us(fn, reps=20, replays=20):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(reps):
+                fn()
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * replays)
+
+    in_us = graph_us(lambda: layer._project(x))
+    out_us = graph_us(lambda: gdn.quantized_linear(o, layer.out_proj))
     ms = total_ms / steps
     return {"workload": f"gated-delta layer decode, B={B} active of {P} slots, hidden {hidden}, "
                         f"4-bit group-64 projections, bf16 activations",
             "tokens_per_s": B / (ms * 1e-3), "step_us": ms * 1e3,
             "graph_step_us": graph_ms / steps * 1e3,
             "graph_tokens_per_s": B / (graph_ms / steps * 1e-3),
-            "input_projection_us": in_ms / steps * 1e3, "out_proj_us": out_ms / steps * 1e3}
+            "input_projection_us": in_us, "out_proj_us": out_us}
 
 
 def bench_decode_slots(dev, B, Hk, Hv, steps, warmup):
@@ -535,6 +556,8 @@ def main(argv=None):
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode_large", "decode_slots", "layer_decode", "prefill",
                              "prefill_varlen", "qlinear", "copy"])
+    ap.add_argument("--batch", type=int, default=64,
+                    help="active sequences of the layer_decode workload (pool of 4x as many slots)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary workloads")
     args = ap.parse_args(argv)
@@ -625,7 +648,7 @@ def main(argv=None):
         return 0
 
     if args.workload == "layer_decode":
-        r = bench_layer_decode(dev, 64, args.steps, args.warmup)
+        r = bench_layer_decode(dev, args.batch, args.steps, args.warmup)
         print(json.dumps({"metric": "gated-delta layer decode tokens/s (projections included)",
                           "value": r["graph_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup,
@@ -634,7 +657,8 @@ def main(argv=None):
                           "data": "synthetic", "config": {"workload": r["workload"] + ", HIP-graph steps"},
                           "eager_step_us": r["step_us"],
                           "parts_us": {"input_projection": r["input_projection_us"],
-                                       "out_proj": r["out_proj_us"]}}))
+                                       "out_proj": r["out_proj_us"],
+                                       "note": "each part alone, 20 calls a HIP graph"}}))
         return 0
 
     if args.workload == "decode_slots":

@@ -672,6 +672,245 @@ int decode_cols(bool x_f32, int mt, int bits, int group_size) {
     return (x_f32 ? mt == 1 : mt <= 2) ? narrow : 64;
 }
 
+// Sum over the 64 lanes of a wave, complete in lane 63: pairs and quads
+// (quad_perm), then row_shr 4 and 8 (lane 15 of each row holds the row's
+// sum), then row_bcast 15 and 31 (DPP lanes with no source add 0).
+GDN_DEV float wave_sum_lane63(float v) {
+#define GDN_DPP_ADD(CTRL, ROWS) \
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false))
+    GDN_DPP_ADD(0xB1, 0xF);   // quad_perm [1, 0, 3, 2]
+    GDN_DPP_ADD(0x4E, 0xF);   // quad_perm [2, 3, 0, 1]
+    GDN_DPP_ADD(0x114, 0xF);  // row_shr 4
+    GDN_DPP_ADD(0x118, 0xF);  // row_shr 8
+    GDN_DPP_ADD(0x142, 0xA);  // row_bcast 15 into rows 1 and 3
+    GDN_DPP_ADD(0x143, 0xC);  // row_bcast 31 into rows 2 and 3
+#undef GDN_DPP_ADD
+    return v;
+}
+
+// Matrix-vector kernel for kM rows of x (the dispatch uses one) and 4-bit
+// codes: one wave per output column at a time, two columns per wave and
+// round of the grid. Lane l takes 16 bytes of packed codes of each of kR
+// rounds of a weight row (chunk 64 r + l: 32 codes inside one quantization
+// group) and holds the matching x in registers for every column it visits.
+// Per chunk and row, with P = sum x q and X = sum x over the chunk,
+// y += s P + b X, the wave's lanes summed at the end of the column (the
+// per-group float scaling of MLX's matrix-vector kernels). bf16 x: q enters
+// as the bf16 pair 1 + q / 16 of codes i and i + 4 of a word (one shift and
+// one v_and_or_b32 per pair) against x held as the bf16 pairs
+// (x[i], x[i + 4]) in v_dot2c_f32_bf16, so P' = X + P / 16 and
+// y += 16 s P' + (b - 16 s) X. float32 x: exact float products of the codes
+// (byte conversions) and x.
+template <int kBits, int kM, int kR, bool kXF32>
+__global__ __launch_bounds__(256) void qlinear_gemv_kernel(
+    const void* __restrict__ xp, const uint32_t* __restrict__ w, const void* __restrict__ scales,
+    const void* __restrict__ biases, int sb_dtype, void* __restrict__ y, int y_dtype, int M, int N, int K,
+    int group_size) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    static_assert(kBits == 4, "4-bit codes");
+    constexpr int kCodes = 128 / kBits;                  // codes of a lane's 16-byte chunk
+    constexpr bool kPairs = kBits == 4 && !kXF32;         // bf16 pairs and v_dot2c
+    constexpr int kXRegs = kPairs ? kCodes / 2 : kCodes;  // x registers per row and round
+    constexpr int kRaw = 0x00020000;
+    const int lane = threadIdx.x & 63;
+    const int wave = int(blockIdx.x) * 4 + int(threadIdx.x >> 6), waves = int(gridDim.x) * 4;
+    const int gpr = K / group_size, wpr4 = K * kBits / 8;
+    const int esx = kXF32 ? 4 : 2, esz = sb_dtype == GDN_F32 ? 4 : 2;
+    const auto wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(w), 0, N * wpr4, kRaw);
+    const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(xp), 0, M * K * esx, kRaw);
+    const auto sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(scales), 0, N * gpr * esz, kRaw);
+    const auto br = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(biases), 0, N * gpr * esz, kRaw);
+
+    // this lane's chunks: k0 = kCodes (64 r + lane), active below K
+    bool active[kR];
+    int grp[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+        const int k0 = kCodes * (64 * r + lane);
+        active[r] = k0 < K;
+        grp[r] = active[r] ? k0 / group_size : 0;
+    }
+    // columns kC (wave + i waves) + c, c < kC: the loads of a wave's kC
+    // columns are issued together (the first batch's before x is read), and
+    // the other waves of the SIMD cover their latency
+    constexpr int kC = 2;
+    u32x4 cq[kC][kR];
+    uint32_t cs[kC][kR], cb[kC][kR];
+    const int esz4 = esz;
+    auto fetch = [&](int n0) {
+#pragma unroll
+        for (int c = 0; c < kC; ++c)
+#pragma unroll
+            for (int r = 0; r < kR; ++r) {
+                const int n = n0 + c;
+                cq[c][r] = u32x4{0u, 0u, 0u, 0u};
+                cs[c][r] = cb[c][r] = 0u;
+                if (active[r] && n < N) {
+                    cq[c][r] = __builtin_amdgcn_raw_buffer_load_b128(wr, n * wpr4 + 16 * (64 * r + lane), 0, 0);
+                    const int so = (n * gpr + grp[r]) * esz4;
+                    if (esz4 == 4) {
+                        cs[c][r] = __builtin_amdgcn_raw_buffer_load_b32(sr, so, 0, 0);
+                        cb[c][r] = __builtin_amdgcn_raw_buffer_load_b32(br, so, 0, 0);
+                    } else {
+                        cs[c][r] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
+                        cb[c][r] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+                    }
+                }
+            }
+    };
+    int n0 = kC * wave;
+    if (n0 < N) fetch(n0);
+
+    // x of the chunks and their sums; rows >= M and inactive chunks hold 0
+    uint32_t xq[kM][kR][kXRegs];
+    float xs[kM][kR];
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+#pragma unroll
+        for (int r = 0; r < kR; ++r) {
+            float v[kCodes];
+#pragma unroll
+            for (int j = 0; j < kCodes; ++j) v[j] = 0.f;
+            if (m < M && active[r]) {
+                const int off = (m * K + kCodes * (64 * r + lane)) * esx;
+#pragma unroll
+                for (int c = 0; c < kCodes * esx / 16; ++c) {
+                    const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * c, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (kXF32) {
+                            v[4 * c + e] = __uint_as_float(d[e]);
+                        } else {
+                            v[8 * c + 2 * e] = __uint_as_float(d[e] << 16);
+                            v[8 * c + 2 * e + 1] = __uint_as_float(d[e] & 0xFFFF0000u);
+                        }
+                    }
+                }
+            }
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < kCodes; ++j) sum += v[j];
+            xs[m][r] = sum;
+            if constexpr (kPairs) {
+                // dword 4 t + i: (x[8 t + i], x[8 t + i + 4]) as bf16 (exact: x is bf16)
+#pragma unroll
+                for (int t = 0; t < kCodes / 8; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        xq[m][r][4 * t + i] = (__float_as_uint(v[8 * t + i]) >> 16) |
+                                              (__float_as_uint(v[8 * t + i + 4]) & 0xFFFF0000u);
+            } else {
+#pragma unroll
+                for (int j = 0; j < kCodes; ++j) xq[m][r][j] = __float_as_uint(v[j]);
+            }
+        }
+
+    auto sb_value = [&](uint32_t raw) {
+        if (sb_dtype == GDN_F32) return __uint_as_float(raw);
+        if (sb_dtype == GDN_BF16) return __uint_as_float(raw << 16);
+        return f16_bits_to_f32(uint16_t(raw));
+    };
+    const CodeConsts kc = code_consts();
+    // byte j of v as a float (one v_cvt_f32_ubyte<j>)
+    auto ubyte = [](uint32_t v, int j) { return float((v >> (8 * j)) & 0xFFu); };
+
+    for (; n0 < N; n0 += kC * waves) {
+#pragma unroll
+        for (int c = 0; c < kC; ++c) {
+            const int n = n0 + c;
+            float acc[kM];
+#pragma unroll
+            for (int m = 0; m < kM; ++m) acc[m] = 0.f;
+#pragma unroll
+            for (int r = 0; r < kR; ++r) {
+                const float s = sb_value(cs[c][r]), b = sb_value(cb[c][r]);
+                float P[kM];
+#pragma unroll
+                for (int m = 0; m < kM; ++m) P[m] = 0.f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {  // the chunk's four words
+                    const uint32_t q = cq[c][r][t];
+                    if constexpr (kPairs) {
+                        // the code_fragment dwords, as scalars (a bit cast of a
+                        // vector element reads element 0 on this compiler)
+                        const uint32_t d[4] = {((q << 3) & kc.mask) | kc.one, ((q >> 1) & kc.mask) | kc.one,
+                                               ((q >> 5) & kc.mask) | kc.one, ((q >> 9) & kc.mask) | kc.one};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+#pragma unroll
+                            for (int m = 0; m < kM; ++m)
+                                P[m] = __builtin_amdgcn_fdot2_f32_bf16(
+                                    __builtin_bit_cast(bf16x2, d[i]), __builtin_bit_cast(bf16x2, xq[m][r][4 * t + i]),
+                                    P[m], false);
+                    } else {
+                        // even codes in the bytes of e, odd ones in those of o
+                        const uint32_t e = q & 0x0F0F0F0Fu, o = (q >> 4) & 0x0F0F0F0Fu;
+                        const float qv[8] = {ubyte(e, 0), ubyte(o, 0), ubyte(e, 1), ubyte(o, 1),
+                                             ubyte(e, 2), ubyte(o, 2), ubyte(e, 3), ubyte(o, 3)};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+#pragma unroll
+                            for (int m = 0; m < kM; ++m)
+                                P[m] = __builtin_fmaf(__uint_as_float(xq[m][r][8 * t + j]), qv[j], P[m]);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < kM; ++m) {
+                    if constexpr (kPairs)
+                        acc[m] += __builtin_fmaf(16.f * s, P[m], __builtin_fmaf(-16.f, s, b) * xs[m][r]);
+                    else
+                        acc[m] += __builtin_fmaf(s, P[m], b * xs[m][r]);
+                }
+            }
+            // the column's sum over the wave's lanes, in lane 63
+#pragma unroll
+            for (int m = 0; m < kM; ++m) acc[m] = wave_sum_lane63(acc[m]);
+            if (lane == 63 && n < N) {
+#pragma unroll
+                for (int m = 0; m < kM; ++m)
+                    if (m < M) store_any(y, int64_t(m) * N + n, y_dtype, acc[m]);
+            }
+        }
+        if (n0 + kC * waves < N) fetch(n0 + kC * waves);
+    }
+}
+
+// Rounds of 64 lane chunks a row needs, or 0 where the matrix-vector kernel
+// does not take the call. It runs one row of 4-bit codes (K up to 4096,
+// all the decode kernel takes at this width): measured against the decode
+// kernel at N=12352, K=2048 it takes 6.4 vs 8.3 us (bf16 x) and 10.3 vs
+// 10.7 us (float32 x), at N=2048, K=4096 4.8 vs 6.8 us; from two rows on,
+// and for 8-bit codes, the decode kernel was as fast or faster.
+int gemv_rounds(bool, int M, int K, int bits) {
+    if (M != 1 || bits != 4) return 0;
+    const int chunk_k = 64 * 32;
+    const int r = (K + chunk_k - 1) / chunk_k;
+    return r <= 1 ? 1 : r <= 2 ? 2 : 0;
+}
+
+template <int kBits, int kM, int kR, bool kXF32>
+int launch_gemv_t(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype, void* y,
+                  int y_dtype, int M, int N, int K, int group_size, hipStream_t s) {
+    const int waves = (N + 1) / 2 < 16384 ? (N + 1) / 2 : 16384;  // two columns a wave
+    hipLaunchKernelGGL((qlinear_gemv_kernel<kBits, kM, kR, kXF32>), dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s,
+                       x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size);
+    return check_launch("gdn_quantized_matmul");
+}
+
+int launch_gemv(const void* x, bool x_f32, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
+                void* y, int y_dtype, int M, int N, int K, int, int group_size, int rounds, hipStream_t s) {
+#define GDN_GEMV(R, XF32) \
+    return launch_gemv_t<4, 1, R, XF32>(x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s)
+    if (rounds == 1) {
+        if (x_f32) GDN_GEMV(1, true);
+        GDN_GEMV(1, false);
+    }
+    if (x_f32) GDN_GEMV(2, true);
+    GDN_GEMV(2, false);
+#undef GDN_GEMV
+}
+
 // Up to 32 rows, workgroups of 32 columns where every thread still gets a
 // weight piece (64-k slices or 8-bit codes): two fit on a CU, which doubles
 // the waves that hide the LDS and MFMA latencies and spreads the columns
@@ -820,7 +1059,7 @@ extern "C" int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype
     if (M < 1 || M > 64 || N < 1 || K < 1 || (bits != 4 && bits != 8) ||
         (group_size != 32 && group_size != 64 && group_size != 128) || K % group_size != 0 ||
         !valid_dtype(sb_dtype) || !(x_dtype == GDN_BF16 || (x_f32 && M <= 32)) ||
-        !decode_shape_fits(sb_dtype, N, K, bits, group_size))
+        !decode_shape_fits(sb_dtype, N, K, bits, group_size) || gemv_rounds(x_f32, M, K, bits))
         return 0;
     return decode_workspace_bytes(x_f32, sb_dtype, M, N, K, bits, group_size);
 }
@@ -848,9 +1087,13 @@ extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, c
                 "gdn_quantized_matmul: y overlaps x");
     hipStream_t s = as_stream(stream);
     const auto* wp = static_cast<const uint32_t*>(w);
-    if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, N, K, bits, group_size))
+    if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, N, K, bits, group_size)) {
+        if (const int rounds = gemv_rounds(x_f32, M, K, bits))
+            return launch_gemv(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size,
+                               rounds, s);
         return launch_decode(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size,
                              workspace, workspace_bytes, s);
+    }
     if (x_f32)
         return fail(GDN_EUNSUPPORTED, "gdn_quantized_matmul: float32 x needs a shape the decode kernel takes");
     if (bits == 4) return dispatch_sb<4>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);

@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -434,7 +435,7 @@ class DecodeGraph:
         if x_example.ndim != 2 or x_example.shape[0] != len(self.slots):
             raise ValueError("x_example must be (len(slots), hidden)")
         self.x = x_example.detach().clone()
-        self._idx = torch.tensor(self.slots, dtype=torch.int64)
+        self._idx = np.asarray(self.slots, dtype=np.int64)
         # the slot array must exist before capture (no host copy in the graph)
         side = torch.cuda.Stream(self.x.device)
         side.wait_stream(torch.cuda.current_stream(self.x.device))
@@ -447,14 +448,12 @@ class DecodeGraph:
             self.out = layer.decode_batch(self.x, pool, slots=self.slots)
         # capture ran decode_batch's host bookkeeping once and none of its
         # device work: undo the former
-        pool.conv_half[self._idx] ^= 1
-        pool.size[self._idx] -= 1
+        pool.flip_host(self._idx, tokens=-1)
 
     def step(self, x: torch.Tensor | None = None) -> torch.Tensor:
         if x is not None and x is not self.x:
             self.x.copy_(x)
         self.graph.replay()
-        self.pool.conv_half[self._idx] ^= 1
-        self.pool.size[self._idx] += 1
+        self.pool.flip_host(self._idx)
         return self.out
 

@@ -10,6 +10,7 @@ by the fused decode kernel.
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -65,6 +66,9 @@ class RecurrentStatePool:
         self.ssm_state = torch.zeros((batch, num_value_heads, value_head_dim, key_head_dim),
                                      dtype=torch.float32, device=device)
         self.size = torch.zeros(batch, dtype=torch.int64)
+        # NumPy views of the two host arrays: a decode step's bookkeeping
+        # costs ~1 us through them (a torch CPU index op costs several)
+        self._half_np, self._size_np = self.conv_half.numpy(), self.size.numpy()
 
     @property
     def batch(self) -> int:
@@ -100,9 +104,7 @@ class RecurrentStatePool:
         in the other half, and each holds one more token. ``device_flipped``:
         the decode kernel has flipped the device bits already (it was given
         ``conv_arrivals``); only the host copy and sizes change."""
-        idx = torch.tensor(slots, dtype=torch.int64)
-        self.conv_half[idx] ^= 1
-        self.size[idx] += 1
+        self.flip_host(np.asarray(slots, dtype=np.int64))
         if device_flipped:
             return
         if slot_t is None:
@@ -110,6 +112,12 @@ class RecurrentStatePool:
         device = self.conv_half_dev.device
         _lib.call("gdn_pool_advance", _lib.ptr(slot_t), len(slots), _lib.ptr(self.conv_half_dev),
                   self.batch, _lib.stream_ptr(device))
+
+    def flip_host(self, idx: np.ndarray, tokens: int = 1) -> None:
+        """Host bookkeeping of a decode of the distinct slots ``idx``: flip
+        their half bits and add ``tokens`` (-1 undoes a step) to their sizes."""
+        self._half_np[idx] ^= 1
+        self._size_np[idx] += tokens
 
     def load(self, slot: int, cache: RecurrentCache) -> None:
         """Copy one sequence's state (e.g. after its prefill) into ``slot``."""

@@ -83,13 +83,16 @@ def test_quantized_matmul_workspace_size():
     """K is split only where the decode kernel runs few column tiles: the
     layer's out_proj (N = 2048: 32 tiles of 64 columns at 64 rows) takes 8
     splits of float32 (M, N) blocks, the stacked input projection (N =
-    12352) none; shapes the decode kernel does not take need none."""
+    12352) none; shapes the decode kernel does not take need none, and
+    neither does one row of 4-bit codes (the matrix-vector kernel)."""
 
     lib = _lib.load()
     size = lambda *a: lib.gdn_quantized_matmul_workspace_size(*a)
     bf, f32 = _lib.GDN_BF16, _lib.GDN_F32
     assert size(bf, bf, 64, 2048, 4096, 4, 64) == 8 * 64 * 2048 * 4
-    assert size(bf, bf, 1, 2048, 4096, 4, 64) == 4 * 2048 * 4     # 64 tiles of 32 columns
+    assert size(bf, bf, 2, 2048, 4096, 4, 64) == 4 * 2 * 2048 * 4  # 64 tiles of 32 columns
+    assert size(bf, bf, 1, 2048, 4096, 4, 64) == 0                 # one row: matrix-vector kernel
+    assert size(bf, bf, 1, 2048, 2048, 8, 64) == 4 * 2048 * 4      # (not for 8-bit codes)
     assert size(bf, bf, 64, 12352, 2048, 4, 64) == 0
     assert size(f32, bf, 5, 300, 1024, 4, 32) == 4 * 5 * 300 * 4  # 4 steps: at most 4 splits
     assert size(bf, bf, 65, 2048, 4096, 4, 64) == 0                # tiled kernel

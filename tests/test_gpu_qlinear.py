@@ -104,6 +104,43 @@ def test_float32_activations_on_the_decode_kernel(gpu, M, N, K, bits, gs, sb):
         None, 0, None) == _lib.GDN_EUNSUPPORTED
 
 
+@pytest.mark.parametrize("N,K,gs,sb,x32", [
+    (12352, 2048, 64, "bf16", False),   # the stacked input projection, one sequence
+    (12352, 2048, 64, "bf16", True),
+    (2048, 4096, 64, "bf16", False),    # out_proj: two rounds of lane chunks
+    (2047, 4096, 128, "bf16", True),    # odd N: the last wave's second column is idle
+    (777, 1024, 32, "f16", False),      # half the lanes hold a chunk
+    (130, 512, 128, "f32", True),       # a quarter of them; f32 scales
+])
+def test_one_row_runs_the_matrix_vector_kernel_exactly(gpu, N, K, gs, sb, x32):
+    """One row of x and 4-bit codes (a single sequence's decode step) take
+    the matrix-vector kernel: products against the exact weights s q + b,
+    accumulated in float (bf16 x as bf16 pairs against 1 + q / 16; float32
+    x in float32), within 1e-5 of the float64 product."""
+
+    assert _decode_kernel_takes(1, K, 4, gs, sb)
+    assert _lib.load().gdn_quantized_matmul_workspace_size(
+        _lib.GDN_F32 if x32 else _lib.GDN_BF16, _lib.dtype_code(_TORCH[sb]), 1, N, K, 4, gs) == 0
+    rng = np.random.default_rng(N + K)
+    words, s, b = _weights(rng, N, K, 4, gs, sb)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    if not x32:
+        x = R.bf16_round(x)
+    ref = Q.quantized_matmul(x, words, s, b, 4, gs, w_round="f32")
+    W = _dev_weights(gpu, words, s, b, sb)
+    xt = torch.tensor(x, device=gpu).to(torch.float32 if x32 else torch.bfloat16)
+    y = torch.empty(1, N, device=gpu)
+    _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.dtype_code(xt.dtype), _lib.ptr(W["weight"]),
+              _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
+              _lib.ptr(y), _lib.GDN_F32, 1, N, K, 4, gs, None, 0, _lib.stream_ptr(gpu))
+    err = np.abs(y.cpu().numpy() - ref).max()
+    assert err <= 1e-5 * np.abs(ref).max() + 1e-6, err
+    # a 1-D x through quantized_linear gives the same bits in x's dtype
+    y1 = gdn.quantized_linear(xt[0], W, gdn.QuantScheme(4, gs))
+    assert tuple(y1.shape) == (N,)
+    np.testing.assert_array_equal(y1.float().cpu().numpy(), y[0].to(xt.dtype).float().cpu().numpy())
+
+
 @pytest.mark.parametrize("M,N,K,bits,gs,sb,x32,splits", [
     (64, 2048, 4096, 4, 64, "bf16", False, 8),   # the layer's out_proj: 32 column tiles
     (16, 2048, 4096, 4, 64, "bf16", False, 4),
