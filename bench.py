@@ -390,7 +390,7 @@ class QLinearWorkload:
             _lib.GDN_BF16, _lib.GDN_BF16, M, N, K, bits, group_size))
         self.ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
         self._args = [(self.x.data_ptr(), _lib.GDN_BF16, w.data_ptr(), sc.data_ptr(),
-                       bi.data_ptr(), _lib.GDN_BF16, self.y.data_ptr(), _lib.GDN_BF16, M, N, K,
+                       bi.data_ptr(), _lib.GDN_BF16, self.y.data_ptr(), _lib.GDN_BF16, None, M, N, K,
                        bits, group_size, self.ws.data_ptr(), ws_bytes, stream)
                       for w, sc, bi in self.weights]
 

@@ -48,7 +48,8 @@ typedef enum {
  * quantized matmul and dequantize entry points, 3 the decode step's state
  * slots, 4 its conv rows, 5 replaces the conv rows with the pool's half bits,
  * adds input row strides and gdn_pool_advance, 6 the quantized matmul's
- * workspace and the decode step's conv_arrivals). */
+ * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
+ * residual). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -231,6 +232,10 @@ int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, co
  * kernels do). Otherwise the weights enter the MFMAs as bf16(scale * q + bias)
  * (the product is exact in float32; one rounding), i.e. x times the weights
  * mx.dequantize yields (as MLX's matrix-matrix kernels do).
+ *   residual: NULL, or (M, N) y_dtype (may be y itself): y = the product
+ *      rounded to y_dtype plus residual, rounded again (the unfused add of
+ *      two y_dtype arrays, as the decoder layer's h = x + attention(...),
+ *      model/qwen3_5/transformer.py:110-112)
  *   workspace: NULL, or device scratch of workspace_bytes (16-byte aligned).
  *      With gdn_quantized_matmul_workspace_size(...) bytes, a decode-kernel
  *      call with few column tiles (small N) splits K over several
@@ -244,9 +249,9 @@ int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, co
  * (model/qwen3_5/linear_attention.py:96-101,125).
  */
 int gdn_quantized_matmul(const void *x, int x_dtype, const void *w, const void *scales,
-                         const void *biases, int sb_dtype, void *y, int y_dtype, int M, int N,
-                         int K, int bits, int group_size, void *workspace,
-                         int64_t workspace_bytes, void *stream);
+                         const void *biases, int sb_dtype, void *y, int y_dtype,
+                         const void *residual, int M, int N, int K, int bits, int group_size,
+                         void *workspace, int64_t workspace_bytes, void *stream);
 
 /*
  * gdn_quantized_matmul_workspace_size - workspace bytes gdn_quantized_matmul

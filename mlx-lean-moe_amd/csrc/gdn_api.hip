@@ -67,7 +67,7 @@ __global__ void gated_rmsnorm_kernel(const void* x, int x_dtype, const void* z, 
 
 using namespace gdn;
 
-extern "C" int gdn_abi_version(void) { return 6; }
+extern "C" int gdn_abi_version(void) { return 7; }
 
 extern "C" const char* gdn_last_error(void) { return g_last_error; }
 

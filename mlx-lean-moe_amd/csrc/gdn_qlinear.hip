@@ -30,6 +30,12 @@ GDN_DEV f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// y[i] with the residual: the product rounded to y's dtype plus residual[i]
+// (the unfused add of two y-dtype arrays; the store rounds the sum).
+GDN_DEV float plus_residual(float v, const void* residual, int64_t i, int dtype) {
+    return residual ? round_to(v, dtype) + load_any(residual, i, dtype) : v;
+}
+
 template <int kBits>
 struct Packing {
     static constexpr int per_word = 32 / kBits;
@@ -75,7 +81,7 @@ template <int BM, int BN, int kBits, class SB, class Y>
 __global__ __launch_bounds__(256) void qlinear_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const typename SB::storage* __restrict__ scales, const typename SB::storage* __restrict__ biases,
-    typename Y::storage* __restrict__ y, int M, int N, int K, int group_size) {
+    typename Y::storage* y, const void* residual, int M, int N, int K, int group_size) {
     static_assert(BN <= 128 && BM * 8 % 256 == 0, "tile shape");
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kTS];
     __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kTS];
@@ -159,7 +165,10 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = m0 + wm + 16 * a + 4 * lq + i;
-                if (m < M && n < N) Y::store(y, int64_t(m) * N + n, acc[a][b][i]);
+                if (m < M && n < N) {
+                    const int64_t e = int64_t(m) * N + n;
+                    Y::store(y, e, plus_residual(acc[a][b][i], residual, e, Y::code));
+                }
             }
         }
 }
@@ -232,8 +241,8 @@ GDN_DEV bf16x8 code_fragment(const uint32_t* words, CodeConsts k) {
 template <int kBits, int kSteps, int kMT, int kSlice, int kCols, bool kXF32>
 __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     const void* __restrict__ xp, const uint32_t* __restrict__ w, const void* __restrict__ scales,
-    const void* __restrict__ biases, int sb_dtype, void* __restrict__ y, int y_dtype, int M, int N, int K,
-    int group_size, float* __restrict__ partial) {
+    const void* __restrict__ biases, int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N,
+    int K, int group_size, float* __restrict__ partial) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     constexpr int kStep = 8 * kSlice;            // k per step
     constexpr int kKB = kSlice / 32;             // MFMA k blocks per wave per step
@@ -565,22 +574,27 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         float* pp = partial + int64_t(split) * M * N;
         store([&](int64_t i, float v) { pp[i] = v; });
     } else if (y_dtype == GDN_BF16)
-        store([&](int64_t i, float v) { static_cast<uint16_t*>(y)[i] = f32_to_bf16_bits(v); });
+        store([&](int64_t i, float v) {
+            static_cast<uint16_t*>(y)[i] = f32_to_bf16_bits(plus_residual(v, residual, i, GDN_BF16));
+        });
     else if (y_dtype == GDN_F16)
-        store([&](int64_t i, float v) { static_cast<uint16_t*>(y)[i] = f32_to_f16_bits(v); });
+        store([&](int64_t i, float v) {
+            static_cast<uint16_t*>(y)[i] = f32_to_f16_bits(plus_residual(v, residual, i, GDN_F16));
+        });
     else
-        store([&](int64_t i, float v) { static_cast<float*>(y)[i] = v; });
+        store([&](int64_t i, float v) { static_cast<float*>(y)[i] = plus_residual(v, residual, i, GDN_F32); });
 }
 
 // y = the sum, in split order, of the split-K kernel's S float32 blocks
 // partial[S][count].
 __global__ __launch_bounds__(256) void qlinear_split_sum_kernel(const float* __restrict__ partial, int splits,
-                                                                int64_t count, void* __restrict__ y, int y_dtype) {
+                                                                int64_t count, void* y, int y_dtype,
+                                                                const void* residual) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= count) return;
     float v = partial[i];
     for (int j = 1; j < splits; ++j) v += partial[j * count + i];
-    store_any(y, i, y_dtype, v);
+    store_any(y, i, y_dtype, plus_residual(v, residual, i, y_dtype));
 }
 
 constexpr int kCUs = 256;  // compute units of an MI355X
@@ -602,8 +616,8 @@ int decode_splits(int tiles, int ks, int K, int group_size, int per_piece, int M
 
 template <int kBits, int kMT, int kSlice, int kCols, bool kXF32>
 int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
-                     void* y, int y_dtype, int M, int N, int K, int group_size, void* workspace,
-                     int64_t ws_bytes, hipStream_t s) {
+                     void* y, int y_dtype, const void* residual, int M, int N, int K, int group_size,
+                     void* workspace, int64_t ws_bytes, hipStream_t s) {
     const int tiles = (N + kCols - 1) / kCols, ks = K / (8 * kSlice);
     const int splits = decode_splits(tiles, ks, K, group_size, sb_dtype == GDN_F32 ? 4 : 8, M, N,
                                      workspace ? ws_bytes : 0);
@@ -615,7 +629,7 @@ int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
 #define GDN_DEC(STEPS)                                                                              \
     hipLaunchKernelGGL((qlinear_decode_kernel<kBits, STEPS, kMT, kSlice, kCols, kXF32>), grid, dim3(512), 0, s, \
-                       x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, partial)
+                       x, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, partial)
     switch (ks / splits) {
         case 1: GDN_DEC(1); break;
         case 2: GDN_DEC(2); break;
@@ -639,7 +653,7 @@ int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const
     if (!partial) return 0;
     const int64_t count = int64_t(M) * N;
     hipLaunchKernelGGL(qlinear_split_sum_kernel, dim3(unsigned((count + 255) / 256)), dim3(256), 0, s, partial,
-                       splits, count, y, y_dtype);
+                       splits, count, y, y_dtype, residual);
     return check_launch("gdn_quantized_matmul");
 }
 
@@ -704,8 +718,8 @@ GDN_DEV float wave_sum_lane63(float v) {
 template <int kBits, int kM, int kR, bool kXF32>
 __global__ __launch_bounds__(256) void qlinear_gemv_kernel(
     const void* __restrict__ xp, const uint32_t* __restrict__ w, const void* __restrict__ scales,
-    const void* __restrict__ biases, int sb_dtype, void* __restrict__ y, int y_dtype, int M, int N, int K,
-    int group_size) {
+    const void* __restrict__ biases, int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N,
+    int K, int group_size) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     static_assert(kBits == 4, "4-bit codes");
@@ -869,7 +883,10 @@ __global__ __launch_bounds__(256) void qlinear_gemv_kernel(
             if (lane == 63 && n < N) {
 #pragma unroll
                 for (int m = 0; m < kM; ++m)
-                    if (m < M) store_any(y, int64_t(m) * N + n, y_dtype, acc[m]);
+                    if (m < M) {
+                        const int64_t e = int64_t(m) * N + n;
+                        store_any(y, e, y_dtype, plus_residual(acc[m], residual, e, y_dtype));
+                    }
             }
         }
         if (n0 + kC * waves < N) fetch(n0 + kC * waves);
@@ -891,17 +908,18 @@ int gemv_rounds(bool, int M, int K, int bits) {
 
 template <int kBits, int kM, int kR, bool kXF32>
 int launch_gemv_t(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype, void* y,
-                  int y_dtype, int M, int N, int K, int group_size, hipStream_t s) {
+                  int y_dtype, const void* residual, int M, int N, int K, int group_size, hipStream_t s) {
     const int waves = (N + 1) / 2 < 16384 ? (N + 1) / 2 : 16384;  // two columns a wave
     hipLaunchKernelGGL((qlinear_gemv_kernel<kBits, kM, kR, kXF32>), dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s,
-                       x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size);
+                       x, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size);
     return check_launch("gdn_quantized_matmul");
 }
 
 int launch_gemv(const void* x, bool x_f32, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
-                void* y, int y_dtype, int M, int N, int K, int, int group_size, int rounds, hipStream_t s) {
+                void* y, int y_dtype, const void* residual, int M, int N, int K, int, int group_size, int rounds,
+                hipStream_t s) {
 #define GDN_GEMV(R, XF32) \
-    return launch_gemv_t<4, 1, R, XF32>(x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s)
+    return launch_gemv_t<4, 1, R, XF32>(x, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, s)
     if (rounds == 1) {
         if (x_f32) GDN_GEMV(1, true);
         GDN_GEMV(1, false);
@@ -918,10 +936,10 @@ int launch_gemv(const void* x, bool x_f32, const uint32_t* w, const void* scales
 // float32 x (twice the x tiles) runs up to 32 rows: 32 columns up to 16
 // rows, 64 beyond.
 int launch_decode(const void* x, bool x_f32, const uint32_t* w, const void* scales, const void* biases,
-                  int sb_dtype, void* y, int y_dtype, int M, int N, int K, int bits, int group_size,
-                  void* workspace, int64_t ws_bytes, hipStream_t s) {
+                  int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N, int K, int bits,
+                  int group_size, void* workspace, int64_t ws_bytes, hipStream_t s) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-#define GDN_ARGS x, w, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, workspace, ws_bytes, s
+#define GDN_ARGS x, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, workspace, ws_bytes, s
 #define GDN_MT(BITS, SLICE, NARROW)                                                       \
     do {                                                                                  \
         if (x_f32) {                                                                      \
@@ -971,13 +989,13 @@ __global__ void dequantize_kernel(const uint32_t* __restrict__ w, const typename
 
 template <int BM, int BN, int kBits, class SB, class Y>
 int launch_qlinear(const void* x, const uint32_t* w, const void* scales, const void* biases, void* y,
-                   int M, int N, int K, int group_size, hipStream_t s) {
+                   const void* residual, int M, int N, int K, int group_size, hipStream_t s) {
     const dim3 grid(unsigned((N + BN - 1) / BN), unsigned((M + BM - 1) / BM));
     hipLaunchKernelGGL((qlinear_kernel<BM, BN, kBits, SB, Y>), grid, dim3(256), 0, s,
                        static_cast<const uint16_t*>(x), w,
                        static_cast<const typename SB::storage*>(scales),
                        static_cast<const typename SB::storage*>(biases),
-                       static_cast<typename Y::storage*>(y), M, N, K, group_size);
+                       static_cast<typename Y::storage*>(y), residual, M, N, K, group_size);
     return check_launch("gdn_quantized_matmul");
 }
 
@@ -986,25 +1004,25 @@ int launch_qlinear(const void* x, const uint32_t* w, const void* scales, const v
 // here.)
 template <int kBits, class SB, class Y>
 int dispatch_qlinear(const void* x, const uint32_t* w, const void* scales, const void* biases,
-                     void* y, int M, int N, int K, int group_size, hipStream_t s) {
-    if (M <= 64) return launch_qlinear<64, 32, kBits, SB, Y>(x, w, scales, biases, y, M, N, K, group_size, s);
-    return launch_qlinear<128, 128, kBits, SB, Y>(x, w, scales, biases, y, M, N, K, group_size, s);
+                     void* y, const void* r, int M, int N, int K, int group_size, hipStream_t s) {
+    if (M <= 64) return launch_qlinear<64, 32, kBits, SB, Y>(x, w, scales, biases, y, r, M, N, K, group_size, s);
+    return launch_qlinear<128, 128, kBits, SB, Y>(x, w, scales, biases, y, r, M, N, K, group_size, s);
 }
 
 template <int kBits, class SB>
 int dispatch_y(const void* x, const uint32_t* w, const void* scales, const void* biases, void* y,
-               int y_dtype, int M, int N, int K, int group_size, hipStream_t s) {
-    if (y_dtype == GDN_F32) return dispatch_qlinear<kBits, SB, ActF32>(x, w, scales, biases, y, M, N, K, group_size, s);
-    if (y_dtype == GDN_BF16) return dispatch_qlinear<kBits, SB, ActBF16>(x, w, scales, biases, y, M, N, K, group_size, s);
-    return dispatch_qlinear<kBits, SB, ActF16>(x, w, scales, biases, y, M, N, K, group_size, s);
+               int y_dtype, const void* r, int M, int N, int K, int group_size, hipStream_t s) {
+    if (y_dtype == GDN_F32) return dispatch_qlinear<kBits, SB, ActF32>(x, w, scales, biases, y, r, M, N, K, group_size, s);
+    if (y_dtype == GDN_BF16) return dispatch_qlinear<kBits, SB, ActBF16>(x, w, scales, biases, y, r, M, N, K, group_size, s);
+    return dispatch_qlinear<kBits, SB, ActF16>(x, w, scales, biases, y, r, M, N, K, group_size, s);
 }
 
 template <int kBits>
 int dispatch_sb(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
-                void* y, int y_dtype, int M, int N, int K, int group_size, hipStream_t s) {
-    if (sb_dtype == GDN_F32) return dispatch_y<kBits, ActF32>(x, w, scales, biases, y, y_dtype, M, N, K, group_size, s);
-    if (sb_dtype == GDN_BF16) return dispatch_y<kBits, ActBF16>(x, w, scales, biases, y, y_dtype, M, N, K, group_size, s);
-    return dispatch_y<kBits, ActF16>(x, w, scales, biases, y, y_dtype, M, N, K, group_size, s);
+                void* y, int y_dtype, const void* r, int M, int N, int K, int group_size, hipStream_t s) {
+    if (sb_dtype == GDN_F32) return dispatch_y<kBits, ActF32>(x, w, scales, biases, y, y_dtype, r, M, N, K, group_size, s);
+    if (sb_dtype == GDN_BF16) return dispatch_y<kBits, ActBF16>(x, w, scales, biases, y, y_dtype, r, M, N, K, group_size, s);
+    return dispatch_y<kBits, ActF16>(x, w, scales, biases, y, y_dtype, r, M, N, K, group_size, s);
 }
 
 template <int kBits, class SB>
@@ -1065,9 +1083,9 @@ extern "C" int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype
 }
 
 extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, const void* scales,
-                                    const void* biases, int sb_dtype, void* y, int y_dtype, int M,
-                                    int N, int K, int bits, int group_size, void* workspace,
-                                    int64_t workspace_bytes, void* stream) {
+                                    const void* biases, int sb_dtype, void* y, int y_dtype,
+                                    const void* residual, int M, int N, int K, int bits, int group_size,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
     if (int rc = check_quant_args("gdn_quantized_matmul", w, scales, biases, sb_dtype, N, K, bits,
                                   group_size))
         return rc;
@@ -1085,19 +1103,24 @@ extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, c
     GDN_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, "gdn_quantized_matmul: x must be 16-byte aligned");
     GDN_REQUIRE(!overlaps(x, int64_t(M) * K * dtype_size(x_dtype), y, int64_t(M) * N * dtype_size(y_dtype)),
                 "gdn_quantized_matmul: y overlaps x");
+    const int64_t y_bytes = int64_t(M) * N * dtype_size(y_dtype);
+    GDN_REQUIRE(!residual || residual == y || !overlaps(residual, y_bytes, y, y_bytes),
+                "gdn_quantized_matmul: residual partially overlaps y");
+    GDN_REQUIRE(!residual || !overlaps(residual, y_bytes, x, int64_t(M) * K * dtype_size(x_dtype)),
+                "gdn_quantized_matmul: residual overlaps x");
     hipStream_t s = as_stream(stream);
     const auto* wp = static_cast<const uint32_t*>(w);
     if (M <= 64 && decode_kernel_fits(x, wp, scales, biases, sb_dtype, N, K, bits, group_size)) {
         if (const int rounds = gemv_rounds(x_f32, M, K, bits))
-            return launch_gemv(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size,
-                               rounds, s);
-        return launch_decode(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, bits, group_size,
-                             workspace, workspace_bytes, s);
+            return launch_gemv(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, bits,
+                               group_size, rounds, s);
+        return launch_decode(x, x_f32, wp, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, bits,
+                             group_size, workspace, workspace_bytes, s);
     }
     if (x_f32)
         return fail(GDN_EUNSUPPORTED, "gdn_quantized_matmul: float32 x needs a shape the decode kernel takes");
-    if (bits == 4) return dispatch_sb<4>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);
-    return dispatch_sb<8>(x, wp, scales, biases, sb_dtype, y, y_dtype, M, N, K, group_size, s);
+    if (bits == 4) return dispatch_sb<4>(x, wp, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, s);
+    return dispatch_sb<8>(x, wp, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, s);
 }
 
 extern "C" int gdn_dequantize(const void* w, const void* scales, const void* biases, int sb_dtype,

@@ -313,11 +313,11 @@ class Qwen3_5LinearAttention:
             return None
         return LinearWeights(concat_quantized(tensors), schemes.pop())
 
-    def _proj(self, rows: torch.Tensor, weights) -> torch.Tensor:
+    def _proj(self, rows: torch.Tensor, weights, residual: torch.Tensor | None = None) -> torch.Tensor:
         tensors, quant = self._scheme_of(weights)
         if quant is None and tensors.dtype != rows.dtype:
             tensors = tensors.to(rows.dtype)
-        return quantized_linear(rows, tensors, quant)
+        return quantized_linear(rows, tensors, quant, residual=residual)
 
     def _project(self, rows: torch.Tensor):
         d = self.linear
@@ -357,9 +357,13 @@ class Qwen3_5LinearAttention:
         out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out_dtype=z.dtype)
         return out.reshape(T, d.value_dim), new_conv, new_ssm
 
-    def __call__(self, x: torch.Tensor, cache: RecurrentCache) -> torch.Tensor:
+    def __call__(self, x: torch.Tensor, cache: RecurrentCache,
+                 residual: torch.Tensor | None = None) -> torch.Tensor:
         """``x``: ``(hidden,)`` for one decode step or ``(L, hidden)`` for a
-        prompt; returns the same rank (linear_attention.py:81-127)."""
+        prompt; returns the same rank (linear_attention.py:81-127). With
+        ``residual`` (x's shape and dtype) the result is ``residual +
+        layer(x)``, the decoder layer's ``h = rows + attention(rms_norm(rows))``
+        (transformer.py:110-112), added in out_proj's store."""
 
         if x.ndim not in (1, 2):
             raise ValueError(f"Qwen3_5LinearAttention expects 1-D or 2-D x, got shape {tuple(x.shape)}")
@@ -378,7 +382,9 @@ class Qwen3_5LinearAttention:
             out, new_conv, new_ssm = self.core(qkv, z, a, b, conv_state[None], ssm_state[None])
             new_conv, new_ssm = new_conv[0], new_ssm[0]
         cache.update(new_conv, new_ssm, advance=L)
-        out = self._proj(out, self.out_proj)
+        if residual is not None and squeeze:
+            residual = residual[None, :]
+        out = self._proj(out, self.out_proj, residual)
         return out[0] if squeeze else out
 
     def _decode_fused(self, qkv, z, a, b, conv_state, ssm_state, in_place: bool,
@@ -388,13 +394,15 @@ class Qwen3_5LinearAttention:
                                  self.linear, conv_out=conv_out,
                                  state_out=ssm_state if in_place else None)
 
-    def decode_batch(self, x: torch.Tensor, pool: RecurrentStatePool, slots=None) -> torch.Tensor:
+    def decode_batch(self, x: torch.Tensor, pool: RecurrentStatePool, slots=None,
+                     residual: torch.Tensor | None = None) -> torch.Tensor:
         """One decode token for each of the pool's sequences: ``x (pool.batch,
         hidden)`` -> ``(pool.batch, hidden)``; or, with ``slots`` (distinct
         pool indices, e.g. the sequences a scheduler has active this step),
         ``x (len(slots), hidden)`` for those slots only. One kernel launch
         updates the slots' ssm tiles in place and rolls their conv state into
-        the other half of the pool's conv buffer."""
+        the other half of the pool's conv buffer. ``residual`` as in
+        ``__call__``."""
 
         d = self.linear
         rows = pool.batch if slots is None else len(slots)
@@ -412,7 +420,7 @@ class Qwen3_5LinearAttention:
             self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_t,
             conv_half=pool.conv_half_dev, conv_arrivals=pool.conv_arrivals)
         pool.advance(slot_list, device_flipped=True)
-        return self._proj(out.reshape(rows, d.value_dim), self.out_proj)
+        return self._proj(out.reshape(rows, d.value_dim), self.out_proj, residual)
 
 
 class DecodeGraph:

@@ -126,19 +126,32 @@ def decode_kernel_takes(M: int, K: int, bits: int, group_size: int, sb_dtype: to
             and gpr <= 64 and gpr % (4 if sb_dtype == torch.float32 else 8) == 0)
 
 
-def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None) -> torch.Tensor:
+def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None, *,
+                     residual: torch.Tensor | None = None) -> torch.Tensor:
     """Linear projection for self-describing, legacy quantized, or dense
     weights (moe_block.py:27-55): ``x @ W.T`` over the last axis of ``x``.
     Quantized weights give ``x``'s dtype; dense ones the promotion of ``x``'s
     and ``W``'s dtypes, as MLX's matmul does (a checkpoint's bf16 dense
-    weights are read widened to float32)."""
+    weights are read widened to float32).
+
+    ``residual`` (the result's shape and dtype) is added to the product
+    rounded to that dtype, as the decoder layer's ``h = x + attention(...)``
+    (transformer.py:110-112) adds two arrays of it; on the quantized
+    kernels the add is part of the store."""
 
     if isinstance(tensors, LinearWeights):
         quant = tensors.quant
         tensors = tensors.tensors
+
+    def with_residual(out: torch.Tensor) -> torch.Tensor:
+        if residual is None:
+            return out
+        _check_residual(residual, out.shape, out.dtype)
+        return out + residual
+
     if isinstance(tensors, torch.Tensor):
         dt = torch.promote_types(x.dtype, tensors.dtype)
-        return x.to(dt) @ tensors.to(dt).T
+        return with_residual(x.to(dt) @ tensors.to(dt).T)
     if quant is None:
         raise ValueError("quantized linear weights require a quantization scheme")
     _kernel_scheme(quant)
@@ -150,16 +163,22 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None)
     x_f32 = (x.dtype == torch.float32 and rows <= 32
              and decode_kernel_takes(rows, K, quant.bits, quant.group_size, scales.dtype))
     if x.dtype != torch.bfloat16 and not x_f32:
-        return x @ dequantize(tensors, quant, x.dtype).T
+        return with_residual(x @ dequantize(tensors, quant, x.dtype).T)
     x2 = _c(x.reshape(-1, K))
     if x2.shape[0] >= _BLAS_ROWS:
         # prefill-sized: the same bf16-rounded weights (gdn_dequantize), one
         # transient copy, and the vendor BLAS for the GEMM itself
-        return (x2 @ dequantize(tensors, quant, torch.bfloat16).T).reshape(*lead, N)
+        return with_residual((x2 @ dequantize(tensors, quant, torch.bfloat16).T).reshape(*lead, N))
     if x2.data_ptr() % 16:
         x2 = x2.clone()
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    r = None
+    if residual is not None:
+        _check_residual(residual, (*lead, N), x.dtype)
+        if residual.device != x.device:
+            raise ValueError("residual must be on the projection's device")
+        r = _c(residual.reshape(M, N))
     w, scales, biases = _c(w), _c(scales), _c(biases)
     ws_bytes = workspace_bytes(x2.dtype, scales.dtype, M, N, K, quant.bits, quant.group_size)
     # a transient from the caching allocator (graph-capture safe); the split
@@ -167,9 +186,15 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     _lib.call("gdn_quantized_matmul", _lib.ptr(x2), _lib.dtype_code(x2.dtype), _lib.ptr(w), _lib.ptr(scales),
               _lib.ptr(biases), _lib.dtype_code(scales.dtype), _lib.ptr(y),
-              _lib.dtype_code(y.dtype), M, N, K, quant.bits, quant.group_size, _lib.ptr(ws),
+              _lib.dtype_code(y.dtype), _lib.ptr(r), M, N, K, quant.bits, quant.group_size, _lib.ptr(ws),
               ws_bytes, _lib.stream_ptr(x.device))
     return y.reshape(*lead, N)
+
+
+def _check_residual(residual: torch.Tensor, shape, dtype: torch.dtype) -> None:
+    if tuple(residual.shape) != tuple(shape) or residual.dtype != dtype:
+        raise ValueError(f"residual must be {tuple(shape)} {dtype}, got {tuple(residual.shape)} "
+                         f"{residual.dtype}")
 
 
 @functools.lru_cache(maxsize=256)

@@ -100,6 +100,6 @@ def test_quantized_matmul_workspace_size():
     assert size(bf, bf, 64, 2048, 4160, 4, 64) == 0                # not whole steps
     # a misaligned workspace is refused before anything runs
     p = ctypes.c_void_p(1 << 30)
-    rc = lib.gdn_quantized_matmul(p, bf, p, p, p, bf, ctypes.c_void_p(1 << 31), bf, 1, 64, 512, 4, 64,
-                                  ctypes.c_void_p((1 << 32) + 8), 1024, None)
+    rc = lib.gdn_quantized_matmul(p, bf, p, p, p, bf, ctypes.c_void_p(1 << 31), bf, None, 1, 64, 512, 4,
+                                  64, ctypes.c_void_p((1 << 32) + 8), 1024, None)
     assert rc == _lib.GDN_EINVAL and "workspace" in _err(lib)

@@ -73,7 +73,7 @@ def test_quantized_matmul_matches_oracle(gpu, M, N, K, bits, gs, sb):
     y32 = torch.empty(M, N, device=gpu)
     _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.GDN_BF16, _lib.ptr(W["weight"]),
               _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
-              _lib.ptr(y32), _lib.GDN_F32, M, N, K, bits, gs, None, 0, _lib.stream_ptr(xt.device))
+              _lib.ptr(y32), _lib.GDN_F32, None, M, N, K, bits, gs, None, 0, _lib.stream_ptr(xt.device))
     err = np.abs(y32.cpu().numpy() - ref).max()
     assert err <= 1e-5 * np.abs(ref).max() + 1e-6, err
 
@@ -100,7 +100,7 @@ def test_float32_activations_on_the_decode_kernel(gpu, M, N, K, bits, gs, sb):
     # more than 32 float32 rows: the C entry declines, quantized_linear dequantizes
     assert _lib.load().gdn_quantized_matmul(
         None, _lib.GDN_F32, _lib.ptr(W["weight"]), _lib.ptr(W["scales"]), _lib.ptr(W["biases"]),
-        _lib.dtype_code(W["scales"].dtype), None, _lib.GDN_F32, 33, N, K, bits, gs,
+        _lib.dtype_code(W["scales"].dtype), None, _lib.GDN_F32, None, 33, N, K, bits, gs,
         None, 0, None) == _lib.GDN_EUNSUPPORTED
 
 
@@ -132,7 +132,7 @@ def test_one_row_runs_the_matrix_vector_kernel_exactly(gpu, N, K, gs, sb, x32):
     y = torch.empty(1, N, device=gpu)
     _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.dtype_code(xt.dtype), _lib.ptr(W["weight"]),
               _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
-              _lib.ptr(y), _lib.GDN_F32, 1, N, K, 4, gs, None, 0, _lib.stream_ptr(gpu))
+              _lib.ptr(y), _lib.GDN_F32, None, 1, N, K, 4, gs, None, 0, _lib.stream_ptr(gpu))
     err = np.abs(y.cpu().numpy() - ref).max()
     assert err <= 1e-5 * np.abs(ref).max() + 1e-6, err
     # a 1-D x through quantized_linear gives the same bits in x's dtype
@@ -174,7 +174,7 @@ def test_split_k_matches_the_unsplit_kernel_and_the_oracle(gpu, M, N, K, bits, g
         y = torch.empty(M, N, device=gpu)
         _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.dtype_code(xdt), _lib.ptr(W["weight"]),
                   _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
-                  _lib.ptr(y), _lib.GDN_F32, M, N, K, bits, gs, w_ptr, w_len, _lib.stream_ptr(gpu))
+                  _lib.ptr(y), _lib.GDN_F32, None, M, N, K, bits, gs, w_ptr, w_len, _lib.stream_ptr(gpu))
         outs.append(y.cpu().numpy())
     tol = (1e-4 if x32 else 1e-5) * np.abs(ref).max() + 1e-6
     for y in outs:
@@ -247,3 +247,38 @@ def test_layer_with_quantized_projections_matches_dense_weights(gpu):
         xt = x[t]
         oq, od = lq(xt, cq), ld(xt, cd)
         assert_bf16_out_close(oq.float().cpu().numpy(), od.float().cpu().numpy().astype(np.float64))
+
+
+@pytest.mark.parametrize("M,N,K,gs,dt", [
+    (1, 2048, 4096, 64, "bf16"),      # the one-row matrix-vector kernel
+    (16, 2048, 4096, 64, "bf16"),     # decode kernel, K split (sum kernel stores)
+    (32, 12352, 2048, 64, "f32"),     # decode kernel, float32 x and result
+    (100, 300, 512, 64, "bf16"),      # tiled kernel
+    (600, 256, 512, 64, "bf16"),      # quantized_linear: dequantize + BLAS, then the add
+])
+def test_residual_is_the_unfused_add(gpu, M, N, K, gs, dt):
+    """residual + x W^T, the product rounded to the result dtype first: bit
+    for bit the unfused add of the two arrays (the decoder layer's
+    h = rows + attention(...))."""
+
+    rng = np.random.default_rng(M + 3 * N)
+    words, s, b = _weights(rng, N, K, 4, gs, "bf16")
+    W = _dev_weights(gpu, words, s, b, "bf16")
+    xdt = _TORCH[dt]
+    x = torch.tensor(rng.standard_normal((M, K)), dtype=torch.float32, device=gpu).to(xdt)
+    r = torch.tensor(rng.standard_normal((M, N)), dtype=torch.float32, device=gpu).to(xdt)
+    scheme = gdn.QuantScheme(4, gs)
+    want = gdn.quantized_linear(x, W, scheme) + r
+    got = gdn.quantized_linear(x, W, scheme, residual=r)
+    assert torch.equal(got, want)
+    if M < 512 and dt == "bf16":
+        # through the C ABI, residual aliasing y: y = x W^T + y
+        y = r.clone()
+        nb = _lib.load().gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, M, N, K, 4, gs)
+        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=gpu)
+        _lib.call("gdn_quantized_matmul", _lib.ptr(x), _lib.GDN_BF16, _lib.ptr(W["weight"]),
+                  _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.GDN_BF16, _lib.ptr(y), _lib.GDN_BF16,
+                  _lib.ptr(y), M, N, K, 4, gs, _lib.ptr(ws), nb, _lib.stream_ptr(gpu))
+        assert torch.equal(y, want)
+    with pytest.raises(ValueError, match="residual"):
+        gdn.quantized_linear(x, W, scheme, residual=r[:, :-1])

@@ -48,6 +48,11 @@ def test_loaded_layer_runs_like_the_decoded_tensors(gpu, tmp_path, act):
     for t in (5, 6):
         torch.testing.assert_close(layer(x[t], c1), direct(x[t], c2), rtol=0, atol=0)
     torch.testing.assert_close(c1.ssm_state, c2.ssm_state, rtol=0, atol=0)
+    # the decoder layer's residual, h = x + layer(x), fused into out_proj's
+    # store: bit for bit the separate add (a prompt chunk and a decode step)
+    for xs in (x[5:7], x[6]):
+        h = layer(xs, c1, residual=xs)
+        assert torch.equal(h, direct(xs, c2) + xs)
 
     # the loaded quantized projection equals x times the oracle's dense weights
     words = u32[f"{PREFIX}.in_proj_z.weight"]
