@@ -13,7 +13,9 @@ Also measured in the same run (reported under "also"):
   prefill:      B=1, T=4096 chunked prefill (bf16 MFMA)
   prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
   decode_slots: B=64 active sequences at random slots of a 256-sequence pool
-  (--workload layer_decode: the whole layer with 4-bit projections, alone,
+  layer_decode: the whole layer's decode step with 4-bit projections, B=64
+  of 256 slots, from HIP graphs
+  (--workload layer_decode: the same alone, with its parts,
   --batch B active sequences, 64 by default)
 
 python bench.py [--steps K] [--warmup W] [--batch B]
@@ -628,8 +630,14 @@ def main(argv=None):
             pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
             pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
             sl = bench_decode_slots(dev, 64, 16, 32, steps=64, warmup=8)
+            ld = bench_layer_decode(dev, 64, steps=64, warmup=8)
             line["also"] = {
                 "decode_slots": sl,
+                "layer_decode": {
+                    "workload": ld["workload"] + ", HIP-graph steps",
+                    "tokens_per_s": ld["graph_tokens_per_s"], "step_us": ld["graph_step_us"],
+                    "input_projection_us": ld["input_projection_us"],
+                    "out_proj_us": ld["out_proj_us"]},
                 "decode_large": {
                     "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
                     "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],
