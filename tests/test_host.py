@@ -107,3 +107,57 @@ def test_decode_slots_are_checked_on_the_host():
         check_slots(torch.zeros(2, 1, dtype=torch.int64), 2, 4)
     with pytest.raises(ValueError, match="integers"):
         check_slots(torch.zeros(2), 2, 4)
+
+
+def test_row_views_are_read_in_place_and_other_layouts_copied():
+    """The decode step reads qkv, z, a and b at a row stride: column slices
+    of one stacked projection output go in as they are (their row stride
+    reported), anything whose rows are not packed is copied."""
+    from mlx_lean_moe_amd.linear_attention import _rows
+
+    stacked = torch.arange(5 * 40, dtype=torch.float32).reshape(5, 40)
+    qkv, z, a = stacked[:, :24], stacked[:, 24:32].reshape(5, 2, 4), stacked[:, 32:36]
+    for t, width in ((qkv, 24), (z, 8), (a, 4)):
+        got, stride = _rows(t)
+        assert got.data_ptr() == t.data_ptr() and stride == 40
+        assert got.stride(0) == 40 and got[0].numel() == width
+    packed, stride = _rows(torch.zeros(3, 6))
+    assert stride == 6
+    # a column view with a non-unit inner stride, or overlapping rows, is copied
+    for t in (stacked[:, ::2], torch.zeros(1, 8).expand(4, 8)):
+        got, stride = _rows(t)
+        assert got.is_contiguous() and stride == t.shape[1] and torch.equal(got, t)
+    one, stride = _rows(stacked[2:3, :7])
+    assert one.data_ptr() == stacked[2:3, :7].data_ptr() and stride == 7
+
+
+def test_conv_half_bits_and_residuals_are_checked_on_the_host():
+    from mlx_lean_moe_amd.linear_attention import check_half_bits
+    from mlx_lean_moe_amd.quant import _check_residual
+
+    assert check_half_bits([0, 1, 1], 3) == [0, 1, 1]
+    for bad in ([0, 2, 1], [0, 1], [-1, 0, 0]):
+        with pytest.raises(ValueError, match="bits"):
+            check_half_bits(bad, 3)
+    _check_residual(torch.zeros(2, 5, dtype=torch.bfloat16), (2, 5), torch.bfloat16)
+    for r in (torch.zeros(2, 4, dtype=torch.bfloat16), torch.zeros(2, 5)):
+        with pytest.raises(ValueError, match="residual"):
+            _check_residual(r, (2, 5), torch.bfloat16)
+
+
+def test_pool_host_bookkeeping_flips_bits_and_sizes():
+    """The pool's host copies of the half bits and sizes (NumPy views of its
+    torch tensors): a decode of some slots flips exactly their bits and adds
+    one token; tokens=-1 undoes it."""
+
+    pool = gdn.RecurrentStatePool.__new__(gdn.RecurrentStatePool)
+    pool.conv_half = torch.zeros(6, dtype=torch.int64)
+    pool.size = torch.zeros(6, dtype=torch.int64)
+    pool._half_np, pool._size_np = pool.conv_half.numpy(), pool.size.numpy()
+    idx = np.array([4, 1])
+    pool.flip_host(idx)
+    assert pool.conv_half.tolist() == [0, 1, 0, 0, 1, 0] and pool.size.tolist() == [0, 1, 0, 0, 1, 0]
+    pool.flip_host(np.array([1, 2]))
+    assert pool.conv_half.tolist() == [0, 0, 1, 0, 1, 0] and pool.size.tolist() == [0, 2, 1, 0, 1, 0]
+    pool.flip_host(np.array([1, 2]), tokens=-1)
+    assert pool.conv_half.tolist() == [0, 1, 0, 0, 1, 0] and pool.size.tolist() == [0, 1, 0, 0, 1, 0]
