@@ -433,16 +433,19 @@ class DecodeGraph:
     The graph reads ``self.x`` and writes ``self.out``; ``step(x)`` copies
     ``x`` into ``self.x`` (skip it by writing ``self.x`` directly), replays
     and keeps the pool's host-side bits and sizes in step with the device.
+    With ``residual_example`` the step adds a residual as ``decode_batch``
+    does, read from ``self.residual`` (``step(x, residual)`` copies it in).
     Shapes, slots and every buffer are fixed at capture; the pool's contents
     may change between steps (e.g. ``pool.load``)."""
 
     def __init__(self, layer: "Qwen3_5LinearAttention", pool: RecurrentStatePool, slots,
-                 x_example: torch.Tensor) -> None:
+                 x_example: torch.Tensor, residual_example: torch.Tensor | None = None) -> None:
         self.layer, self.pool = layer, pool
         self.slots = check_slots(slots, len(slots), pool.batch)
         if x_example.ndim != 2 or x_example.shape[0] != len(self.slots):
             raise ValueError("x_example must be (len(slots), hidden)")
         self.x = x_example.detach().clone()
+        self.residual = None if residual_example is None else residual_example.detach().clone()
         self._idx = np.asarray(self.slots, dtype=np.int64)
         # the slot array must exist before capture (no host copy in the graph)
         side = torch.cuda.Stream(self.x.device)
@@ -453,14 +456,19 @@ class DecodeGraph:
         torch.cuda.synchronize(self.x.device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.out = layer.decode_batch(self.x, pool, slots=self.slots)
+            self.out = layer.decode_batch(self.x, pool, slots=self.slots, residual=self.residual)
         # capture ran decode_batch's host bookkeeping once and none of its
         # device work: undo the former
         pool.flip_host(self._idx, tokens=-1)
 
-    def step(self, x: torch.Tensor | None = None) -> torch.Tensor:
+    def step(self, x: torch.Tensor | None = None, residual: torch.Tensor | None = None) -> torch.Tensor:
         if x is not None and x is not self.x:
             self.x.copy_(x)
+        if residual is not None:
+            if self.residual is None:
+                raise ValueError("this step was captured without a residual")
+            if residual is not self.residual:
+                self.residual.copy_(residual)
         self.graph.replay()
         self.pool.flip_host(self._idx)
         return self.out

@@ -241,3 +241,31 @@ def test_decode_graph_replays_equal_eager_decode(gpu):
     assert torch.equal(graphed.size, eager.size) and torch.equal(graphed.conv_half, eager.conv_half)
     assert torch.equal(graphed.conv_half_dev, eager.conv_half_dev)
     assert graphed.conv_half_dev.cpu().tolist() == graphed.conv_half.tolist()
+
+
+def test_decode_graph_with_a_residual(gpu):
+    """The decoder layer's residual inside the captured step: each replay
+    equals eager decode_batch(..., residual=) on a twin pool."""
+
+    layer, _ = _build(8, DIMS, gpu, dtype=torch.bfloat16)
+    rng = np.random.default_rng(108)
+    P, slots = 4, [3, 1]
+    pools = [gdn.RecurrentStatePool(P, 4, DIMS.conv_dim, DIMS.num_value_heads, 128, 128,
+                                    dtype=torch.bfloat16, device=gpu) for _ in range(2)]
+    for i, n in enumerate((3, 6)):
+        cache = layer.new_cache(torch.bfloat16)
+        layer(torch.tensor(rng.standard_normal((n, HIDDEN)), dtype=torch.bfloat16, device=gpu), cache)
+        for pool in pools:
+            pool.load(slots[i], cache)
+    eager, graphed = pools
+    mk = lambda: torch.tensor(rng.standard_normal((2, HIDDEN)), dtype=torch.bfloat16, device=gpu)
+    step = gdn.DecodeGraph(layer, graphed, slots, mk(), residual_example=mk())
+    for _ in range(3):
+        x, r = mk(), mk()
+        ref = layer.decode_batch(x, eager, slots=slots, residual=r)
+        out = step.step(x, r)
+        assert torch.equal(out, ref)
+        torch.cuda.synchronize()
+    torch.testing.assert_close(graphed.ssm_state, eager.ssm_state, rtol=0, atol=0)
+    with pytest.raises(ValueError, match="without a residual"):
+        gdn.DecodeGraph(layer, graphed, [0], mk()[:1]).step(residual=mk()[:1])
