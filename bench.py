@@ -195,17 +195,14 @@ class SlotDecodeWorkload:
             raise RuntimeError(f"gdn_decode_step failed with {rc}")
 
 
-def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
-    """The whole gated-delta layer (Hk=16, Hv=32, d=128) decoding B active
-    sequences out of a pool of 4 B slots, 4-bit group-64 projections
-    (stacked qkv|z|a|b in, out_proj out) with bf16 activations: one
-    decode_batch call per step, slot sets rotating as in decode_slots. Also
-    times its three launches alone (input projection, fused decode,
-    out_proj) so the per-part figures add up."""
+def quantized_layer(dev, hidden=2048, seed=0):
+    """The gated-delta layer (Hk=16, Hv=32, d=128) with random 4-bit group-64
+    projections (qkv|z|a|b in, out_proj out) and random conv, gate and norm
+    parameters; returns (layer, generator, randn)."""
 
     d = gdn.QWEN3_5_LINEAR
     q = gdn.QuantScheme(4, 64)
-    g = torch.Generator(device=dev).manual_seed(0)
+    g = torch.Generator(device=dev).manual_seed(seed)
 
     def qweights(n, k):
         return gdn.LinearWeights({
@@ -221,6 +218,19 @@ def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
         rnd(d.conv_dim, 4, 1) * 0.2, torch.rand(d.num_value_heads, generator=g, device=dev) * 2.7,
         rnd(d.num_value_heads), torch.rand(d.value_head_dim, generator=g, device=dev) + 0.5,
         qweights(hidden, d.value_dim))
+    return layer, g, rnd
+
+
+def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
+    """The whole gated-delta layer (Hk=16, Hv=32, d=128) decoding B active
+    sequences out of a pool of 4 B slots, 4-bit group-64 projections
+    (stacked qkv|z|a|b in, out_proj out) with bf16 activations: one
+    decode_batch call per step, slot sets rotating as in decode_slots. Also
+    times its three launches alone (input projection, fused decode,
+    out_proj) so the per-part figures add up."""
+
+    d = gdn.QWEN3_5_LINEAR
+    layer, g, rnd = quantized_layer(dev, hidden)
     P = 4 * B
     pool = gdn.RecurrentStatePool(P, 4, d.conv_dim, d.num_value_heads, 128, 128,
                                   dtype=torch.bfloat16, device=dev)
@@ -264,6 +274,33 @@ def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
             "graph_step_us": graph_ms / steps * 1e3,
             "graph_tokens_per_s": B / (graph_ms / steps * 1e-3),
             "input_projection_us": in_us, "out_proj_us": out_us}
+
+
+def bench_layer_prefill(dev, T, steps, warmup, hidden=2048):
+    """The whole gated-delta layer (Hk=16, Hv=32, d=128, 4-bit group-64
+    projections, bf16 activations) over a T-token prompt: one layer(x, cache)
+    call per step, the cache carried from step to step. Also times its
+    three parts alone (input projections, everything between them, out_proj)."""
+
+    d = gdn.QWEN3_5_LINEAR
+    layer, g, rnd = quantized_layer(dev, hidden)
+    cache = layer.new_cache()
+    xs = [rnd(T, hidden).to(torch.bfloat16) for _ in range(2)]
+    total_ms, _ = time_steps(lambda s_: layer(xs[s_ % 2], cache), steps, warmup)
+    x = xs[0]
+    qkv, z, a, b = layer._project(x)
+    conv, ssm = cache.state()
+    o = rnd(T, d.value_dim).to(torch.bfloat16)
+    in_ms, _ = time_steps(lambda s_: layer._project(x), steps, warmup)
+    core_ms, _ = time_steps(lambda s_: layer.core(qkv, z, a, b, conv[None], ssm[None]), steps, warmup)
+    out_ms, _ = time_steps(lambda s_: gdn.quantized_linear(o, layer.out_proj), steps, warmup)
+    ms = total_ms / steps
+    proj_flops = 2 * T * hidden * (d.conv_dim + d.value_dim + 2 * d.num_value_heads + d.value_dim)
+    return {"workload": f"gated-delta layer prefill, T={T}, hidden {hidden}, 4-bit group-64 "
+                        f"projections, bf16 activations",
+            "tokens_per_s": T / (ms * 1e-3), "step_us": ms * 1e3,
+            "input_projection_us": in_ms / steps * 1e3, "core_us": core_ms / steps * 1e3,
+            "out_proj_us": out_ms / steps * 1e3, "projection_flops": proj_flops}
 
 
 def bench_decode_slots(dev, B, Hk, Hv, steps, warmup):
@@ -556,8 +593,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "decode_slots", "layer_decode", "prefill",
-                             "prefill_varlen", "qlinear", "copy"])
+                    choices=["decode", "decode_large", "decode_slots", "layer_decode", "layer_prefill",
+                             "prefill", "prefill_varlen", "qlinear", "copy"])
     ap.add_argument("--batch", type=int, default=64,
                     help="active sequences of the layer_decode workload (pool of 4x as many slots)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -667,6 +704,18 @@ def main(argv=None):
                           "parts_us": {"input_projection": r["input_projection_us"],
                                        "out_proj": r["out_proj_us"],
                                        "note": "each part alone, 20 calls a HIP graph"}}))
+        return 0
+
+    if args.workload == "layer_prefill":
+        r = bench_layer_prefill(dev, 4096, args.steps, args.warmup)
+        print(json.dumps({"metric": "gated-delta layer prefill tokens/s (projections included)",
+                          "value": r["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["step_us"] * 1e-3, "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic", "config": {"workload": r["workload"]},
+                          "parts_us": {"input_projection": r["input_projection_us"],
+                                       "core": r["core_us"], "out_proj": r["out_proj_us"]}}))
         return 0
 
     if args.workload == "decode_slots":

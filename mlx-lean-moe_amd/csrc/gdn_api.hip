@@ -63,6 +63,47 @@ __global__ void gated_rmsnorm_kernel(const void* x, int x_dtype, const void* z, 
     }
 }
 
+// The same for bfloat16 z and out, float32 or bfloat16 x, D = 8 kLanes and
+// 16-byte aligned rows: kLanes lanes a row, 8 elements a lane, 64 / kLanes
+// rows a wave.
+template <int kLanes, bool kXF32>
+__global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(const void* __restrict__ x,
+                                                                const uint16_t* __restrict__ z,
+                                                                const float* __restrict__ w, float eps,
+                                                                uint16_t* __restrict__ out,
+                                                                int64_t rows) {
+    constexpr int D = 8 * kLanes, kRows = kWave / kLanes;
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = (int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * kRows +
+                        lane / kLanes;
+    const bool live = row < rows;
+    const int64_t at = (live ? row : rows - 1) * D + (lane % kLanes) * 8;
+    float v[8];
+    if constexpr (kXF32) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + at);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + at + 4);
+        const float raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = round_bf16(raw[e]);
+    } else {
+        unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + at), v);
+    }
+    float zz[8];
+    unpack8(*reinterpret_cast<const uint4*>(z + at), zz);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + (lane % kLanes) * 8);
+    const float4 w1 = *reinterpret_cast<const float4*>(w + (lane % kLanes) * 8 + 4);
+    const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+    ss = group_sum<kLanes>(ss);
+    const float r = 1.f / sqrtf(ss / float(D) + eps);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = silu(zz[e]) * round_bf16(v[e] * r * ww[e]);
+    if (live) *reinterpret_cast<uint4*>(out + at) = pack8(o);
+}
+
 }  // namespace gdn
 
 using namespace gdn;
@@ -96,6 +137,21 @@ extern "C" int gdn_gated_rmsnorm(const void* x, int x_dtype, const void* z, int 
                 "gdn_gated_rmsnorm: bad dtype");
     if (rows == 0) return 0;
     GDN_REQUIRE(x && z && w && out, "gdn_gated_rmsnorm: null pointer");
+    const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if ((x_dtype == GDN_F32 || x_dtype == GDN_BF16) && z_dtype == GDN_BF16 && out_dtype == GDN_BF16 &&
+        (D == 64 || D == 128 || D == 256) && aligned(x) && aligned(z) && aligned(w) && aligned(out)) {
+        const int64_t per_block = 4 * (kWave / (D / 8));  // rows: four waves
+        const dim3 grid(static_cast<unsigned>((rows + per_block - 1) / per_block));
+        const bool xf = x_dtype == GDN_F32;
+        const auto* zz = static_cast<const uint16_t*>(z);
+        auto* oo = static_cast<uint16_t*>(out);
+        using Kernel = void (*)(const void*, const uint16_t*, const float*, float, uint16_t*, int64_t);
+        const Kernel kern = D == 64  ? (xf ? gated_rmsnorm_vec_kernel<8, true> : gated_rmsnorm_vec_kernel<8, false>)
+                          : D == 128 ? (xf ? gated_rmsnorm_vec_kernel<16, true> : gated_rmsnorm_vec_kernel<16, false>)
+                                     : (xf ? gated_rmsnorm_vec_kernel<32, true> : gated_rmsnorm_vec_kernel<32, false>);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, as_stream(stream), x, zz, w, eps, oo, rows);
+        return check_launch("gdn_gated_rmsnorm");
+    }
     const int waves = 4;
     const int64_t blocks = (rows + waves - 1) / waves;
     hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(unsigned(blocks)), dim3(waves * kWave), 0,

@@ -42,6 +42,37 @@ GDN_DEV uint16_t f32_to_f16_bits(float x) {
     return h;
 }
 
+// Eight bfloat16 values (16 bytes) <-> eight floats, element 0 in the low half
+// of the first dword.
+GDN_DEV void unpack8(uint4 r, float* x) {
+    const uint32_t d[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(d[i] << 16);
+        x[2 * i + 1] = __uint_as_float(d[i] & 0xFFFF0000u);
+    }
+}
+
+// Two floats to two round-to-nearest-even bfloat16 in one dword (one
+// v_cvt_pk_bf16_f32), a in the low half.
+GDN_DEV uint32_t pack_bf16x2(float a, float b) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+// a and b rounded to bfloat16 precision, with one conversion for the pair.
+GDN_DEV void round_bf16x2(float& a, float& b) {
+    const uint32_t u = pack_bf16x2(a, b);
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xFFFF0000u);
+}
+
+GDN_DEV uint4 pack8(const float* x) {
+    return make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]),
+                      pack_bf16x2(x[6], x[7]));
+}
+
 // Load element i of a buffer whose dtype is only known at run time (the
 // branch is uniform across the wave).
 GDN_DEV float load_any(const void* p, int64_t i, int dtype) {
@@ -127,6 +158,22 @@ GDN_DEV float group_sum(float x) {
 #pragma unroll
     for (int off = WIDTH / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
     return x;
+}
+
+// Sum over each row of 16 lanes, in every lane of the row, on DPP moves (no
+// LDS round trip): pairs and quads (quad_perm), then the two quads of each
+// half-row (row_half_mirror) and the two half-rows (row_mirror). Each step
+// adds the same two values in every lane of a pair, so all 16 lanes end
+// with the same bits.
+GDN_DEV float row16_sum(float v) {
+#define GDN_DPP_ADD(CTRL) \
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false))
+    GDN_DPP_ADD(0xB1);   // quad_perm [1, 0, 3, 2]
+    GDN_DPP_ADD(0x4E);   // quad_perm [2, 3, 0, 1]
+    GDN_DPP_ADD(0x141);  // row_half_mirror
+    GDN_DPP_ADD(0x140);  // row_mirror
+#undef GDN_DPP_ADD
+    return v;
 }
 
 // Index of the run that holds token t, given run offsets cu[0..n] (binary

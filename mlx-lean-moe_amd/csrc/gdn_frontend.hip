@@ -1,9 +1,15 @@
 // Prefill front-end: causal depthwise conv + SiLU + conv-state roll, then the
 // q/k scaling, for N packed token runs (linear_attention.py:61-79,103-113).
 //
-// Blocks [0, T_total) each own one token: every channel's K-tap conv goes to
-// LDS, then one wave per q/k head normalises. Blocks [T_total, T_total + N)
-// each write one run's new conv state (the last K-1 rows of
+// Two kernels. The tiled one covers the production shape (Dk = Dv = 128,
+// K = 4, bf16 activations, 16-byte aligned operands): a wave holds four
+// 128-channel groups (q, k or v heads) of one token, 8 channels a lane, and
+// walks a tile of tokens with the previous three input rows in registers, so
+// each qkv row is read once per tile plus a three-row halo, with 16-byte
+// loads and stores; the q/k RMS norm is a 16-lane DPP sum. The general
+// one (any head size and K) gives each token a block: every channel's K-tap
+// conv goes to LDS, then one wave per q/k head normalises. In both, extra
+// blocks each write one run's new conv state (the last K-1 rows of
 // concat(state, tokens)), so conv_state_out must not overlap conv_state_in.
 #include "gdn_common.h"
 #include "gdn_host.h"
@@ -11,6 +17,26 @@
 namespace gdn {
 
 constexpr int kFrontThreads = 256;
+
+// Row j of a run's new conv state is row len + j of concat(state, tokens).
+template <class Act>
+GDN_DEV void write_conv_state(const typename Act::storage* __restrict__ qkv,
+                              const void* __restrict__ cs_in, int conv_dtype,
+                              typename Act::storage* __restrict__ cs_out,
+                              const int32_t* __restrict__ cu, int run, int64_t L_uniform, int C,
+                              int S) {
+    const int64_t start = cu ? cu[run] : run * L_uniform;
+    const int64_t len = cu ? cu[run + 1] - cu[run] : L_uniform;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        for (int j = 0; j < S; ++j) {
+            const int64_t idx = len + j;
+            const float x = idx < S
+                ? Act::round(load_any(cs_in, (int64_t(run) * S + idx) * C + c, conv_dtype))
+                : Act::load(qkv, (start + idx - S) * C + c);
+            Act::store(cs_out, (int64_t(run) * S + j) * C + c, x);
+        }
+    }
+}
 
 template <class Act>
 __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
@@ -26,20 +52,8 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
     const int S = K - 1;  // conv state rows
 
     if (blk >= T) {
-        // New conv state of one run: row j is concat index len + j.
         const int run = int(blk - T);
-        if (run >= N) return;
-        const int64_t start = cu ? cu[run] : run * L_uniform;
-        const int64_t len = cu ? cu[run + 1] - cu[run] : L_uniform;
-        for (int c = tid; c < C; c += kFrontThreads) {
-            for (int j = 0; j < S; ++j) {
-                const int64_t idx = len + j;
-                const float x = idx < S
-                    ? Act::round(load_any(cs_in, (int64_t(run) * S + idx) * C + c, conv_dtype))
-                    : Act::load(qkv, (start + idx - S) * C + c);
-                Act::store(cs_out, (int64_t(run) * S + j) * C + c, x);
-            }
-        }
+        if (run < N) write_conv_state<Act>(qkv, cs_in, conv_dtype, cs_out, cu, run, L_uniform, C, S);
         return;
     }
 
@@ -79,6 +93,191 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
     for (int e = tid; e < Hv * Dv; e += kFrontThreads) Act::store(vo, t * Hv * Dv + e, vsrc[e]);
 }
 
+
+constexpr int kTileTokens = 16;  // tokens a wave walks
+constexpr int kTileWaves = 4;    // waves a block, four channel groups each
+
+constexpr int kStateChunk = kTileWaves * kWave * 8;  // conv-state elements a block writes
+
+// silu(x) = x / (1 + e^-x) on the hardware exp2 and reciprocal (about 1 ulp
+// each; the argument's rounding adds under 2^-20 relative for |x| < 16):
+// five instructions against about twenty-five for libm's expf and an IEEE
+// divide, and within a few float ulp of them, far below the bf16 rounding
+// the result gets next.
+GDN_DEV float silu_hw(float x) {
+    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.44269504088896341f));
+}
+
+// Eight consecutive conv-state values at element `at`, rounded to bf16 (the
+// state may be held in any float dtype; `at` is a multiple of 8, the buffer
+// 16-byte aligned).
+template <int kDt>
+GDN_DEV void load_state8(const void* __restrict__ p, int64_t at, float* x) {
+    if constexpr (kDt == GDN_F32) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + at);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + at + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = round_bf16(v[e]);
+    } else if constexpr (kDt == GDN_BF16) {
+        unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + at), x);
+    } else {
+        const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + at);
+        const uint32_t d[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = round_bf16(f16_bits_to_f32(uint16_t(d[i] & 0xFFFF)));
+            x[2 * i + 1] = round_bf16(f16_bits_to_f32(uint16_t(d[i] >> 16)));
+        }
+    }
+}
+
+// grid (n_state + n_tiles, ceil(G / 16)) for G = 2 Hk + Hv channel groups of
+// 128. The first n_state columns write the runs' new conv states, flattened
+// to N (K-1) C elements, kStateChunk a block (8 independent elements a
+// thread; dispatched first, they overlap the tiles); block (n_state + x, y)
+// covers tokens [16 x, 16 x + 16) of groups [16 y, 16 y + 16).
+//
+// The three-row window holds rows t-3 .. t-1 of concat(run's conv state,
+// run's tokens) for the token t in hand: it is loaded so at the tile's first
+// token and reloaded from the conv state where a run starts inside the tile,
+// and each token shifts itself in.
+template <int kConvDt>
+__global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
+    const uint16_t* __restrict__ qkv, const void* __restrict__ cs_in,
+    uint16_t* __restrict__ cs_out, const float* __restrict__ w, const int32_t* __restrict__ cu,
+    int N, int64_t T, int64_t L_uniform, int n_state, uint16_t* __restrict__ qo,
+    uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, int Hk, int Hv) {
+    constexpr int D = 128, K = 4, S = K - 1;
+    const int G = 2 * Hk + Hv;
+    const int C = G * D;
+    if (int(blockIdx.x) < n_state) {
+        const int64_t total = int64_t(N) * S * C;
+        const int64_t first = (int64_t(blockIdx.x) * gridDim.y + blockIdx.y) * kStateChunk + threadIdx.x;
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // all loads first: they do not wait on each other
+            const int64_t e = first + int64_t(i) * kTileWaves * kWave;
+            if (e < total) {
+                const int run = int(e / (int64_t(S) * C));
+                const int j = int(e / C % S), c = int(e % C);
+                const int64_t start = cu ? cu[run] : run * L_uniform;
+                const int64_t idx = (cu ? cu[run + 1] - cu[run] : L_uniform) + j;  // in concat(state, run)
+                x[i] = idx < S ? round_bf16(load_any(cs_in, (int64_t(run) * S + idx) * C + c, kConvDt))
+                               : ActBF16::load(qkv, (start + idx - S) * C + c);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t e = first + int64_t(i) * kTileWaves * kWave;
+            if (e < total) ActBF16::store(cs_out, e, x[i]);
+        }
+        return;
+    }
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int g0 = (int(blockIdx.y) * kTileWaves + wave) * 4;  // the wave's first group
+    if (g0 >= G) return;  // the whole wave idles; the kernel has no barrier
+    const int g = g0 + lane / 16;
+    const bool live = g < G;
+    const int c0 = (live ? g : G - 1) * D + (lane % 16) * 8;  // this lane's 8 channels
+    const int64_t t0 = (int64_t(blockIdx.x) - n_state) * kTileTokens;
+
+    // the tile's rows, kAhead in flight (the last tile's missing ones repeat
+    // row T-1, unused)
+    constexpr int kAhead = 8;
+    const auto row_at = [&](int i) {
+        const int64_t t = t0 + i < T ? t0 + i : T - 1;
+        return *reinterpret_cast<const uint4*>(qkv + t * C + c0);
+    };
+    uint4 raw[kAhead];
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) raw[i] = row_at(i);
+    int run = cu ? find_run(cu, N, t0) : int(t0 / L_uniform);
+    int64_t start = cu ? cu[run] : run * L_uniform;
+    int64_t next = cu ? cu[run + 1] : start + L_uniform;
+    float win[S][8];
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int64_t row = t0 - S + j;
+        if (row >= start) {
+            unpack8(*reinterpret_cast<const uint4*>(qkv + row * C + c0), win[j]);
+        } else {  // concat index row - start + S of the run's conv state
+            load_state8<kConvDt>(cs_in, (int64_t(run) * S + (row - start + S)) * C + c0, win[j]);
+        }
+    }
+    float wr[8][K];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float4 v4 = *reinterpret_cast<const float4*>(w + int64_t(c0 + e) * K);
+        wr[e][0] = round_bf16(v4.x);
+        wr[e][1] = round_bf16(v4.y);
+        wr[e][2] = round_bf16(v4.z);
+        wr[e][3] = round_bf16(v4.w);
+    }
+
+    const float inv = 1.f / sqrtf(float(D));
+    const float sc = g < Hk ? round_bf16(inv * inv) : round_bf16(inv);
+    const bool is_v = g >= 2 * Hk;
+    // whether the wave holds a q or k head (uniform: a wave may also hold v
+    // heads when Hk is not a multiple of 4; their lanes keep o)
+    const bool qk_wave = __builtin_amdgcn_readfirstlane(int(g0 < 2 * Hk)) != 0;
+    uint16_t* dst = g < Hk ? qo + int64_t(g) * D
+                  : !is_v ? ko + int64_t(g - Hk) * D
+                          : vo + int64_t(g - 2 * Hk) * D;
+    const int64_t dst_row = is_v ? int64_t(Hv) * D : int64_t(Hk) * D;
+    dst += (lane % 16) * 8;
+
+#pragma unroll
+    for (int i = 0; i < kTileTokens; ++i) {
+        const int64_t t = t0 + i;
+        if (t < T && t >= next) {  // a run starts at t (uniform): its conv state is the window
+            run = cu ? find_run(cu, N, t) : int(t / L_uniform);
+            start = t;
+            next = cu ? cu[run + 1] : t + L_uniform;
+#pragma unroll
+            for (int j = 0; j < S; ++j)
+                load_state8<kConvDt>(cs_in, (int64_t(run) * S + j) * C + c0, win[j]);
+        }
+        float x[8];
+        unpack8(raw[i % kAhead], x);
+        if (i + kAhead < kTileTokens) raw[i % kAhead] = row_at(i + kAhead);
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < S; ++j) acc += wr[e][j] * win[j][e];
+            o[e] = acc + wr[e][S] * x[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) round_bf16x2(o[e], o[e + 1]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = silu_hw(o[e]);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) round_bf16x2(o[e], o[e + 1]);
+        if (qk_wave) {  // q and k heads: scaled RMS norm (v lanes keep o)
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += o[e] * o[e];
+            const float r = __builtin_amdgcn_rsqf(row16_sum(ss) / float(D) + 1e-6f);
+            float n[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) n[e] = o[e] * r;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) round_bf16x2(n[e], n[e + 1]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = is_v ? o[e] : sc * n[e];
+        }
+        if (live && t < T) *reinterpret_cast<uint4*>(dst + t * dst_row) = pack8(o);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            win[0][e] = win[1][e];
+            win[1][e] = win[2][e];
+            win[2][e] = x[e];
+        }
+    }
+}
+
 }  // namespace gdn
 
 using namespace gdn;
@@ -109,6 +308,30 @@ extern "C" int gdn_frontend(const void* qkv, const void* conv_state_in, void* co
     GDN_REQUIRE(conv_weight && (T_total == 0 || (qkv && q_out && k_out && v_out)),
                 "gdn_frontend: null pointer");
     const int64_t L_uniform = cu_seqlens ? 0 : T_total / N;
+    const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (act_dtype == GDN_BF16 && Dk == 128 && Dv == 128 && K == 4 && T_total > 0 && aligned(qkv) &&
+        aligned(conv_state_in) && aligned(conv_weight) && aligned(q_out) && aligned(k_out) &&
+        aligned(v_out)) {
+        const int G = 2 * Hk + Hv;
+        const int gy = (G + 4 * kTileWaves - 1) / (4 * kTileWaves);
+        const int64_t n_tiles = (T_total + kTileTokens - 1) / kTileTokens;
+        const int64_t chunks = (int64_t(N) * S * C + kStateChunk - 1) / kStateChunk;
+        const int64_t n_state = (chunks + gy - 1) / gy;
+        const int64_t gx = n_state + n_tiles;
+        GDN_REQUIRE(gx < (1LL << 31) / (kTileWaves * kWave) && gy < 65536,
+                    "gdn_frontend: %lld tokens exceed the grid", (long long)T_total);
+        using Kernel = void (*)(const uint16_t*, const void*, uint16_t*, const float*, const int32_t*,
+                                int, int64_t, int64_t, int, uint16_t*, uint16_t*, uint16_t*, int, int);
+        const Kernel kern = conv_dtype == GDN_F32    ? frontend_tiled_kernel<GDN_F32>
+                            : conv_dtype == GDN_BF16 ? frontend_tiled_kernel<GDN_BF16>
+                                                     : frontend_tiled_kernel<GDN_F16>;
+        hipLaunchKernelGGL(kern, dim3(unsigned(gx), unsigned(gy)), dim3(kTileWaves * kWave), 0,
+                           as_stream(stream), static_cast<const uint16_t*>(qkv), conv_state_in,
+                           static_cast<uint16_t*>(conv_state_out), conv_weight, cu_seqlens, N,
+                           T_total, L_uniform, int(n_state), static_cast<uint16_t*>(q_out),
+                           static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out), Hk, Hv);
+        return check_launch("gdn_frontend");
+    }
     const int64_t blocks = T_total + (S > 0 ? N : 0);
     if (blocks == 0) return 0;
     const size_t lds = size_t(C) * sizeof(float);

@@ -30,7 +30,8 @@ import torch
 from . import _lib
 from .config import LinearAttentionDims
 from .gated_delta import _c, _require_device, _stream, gated_delta_update
-from .quant import LinearWeights, QuantScheme, concat_quantized, quantized_linear
+from .quant import (LinearWeights, QuantScheme, concat_quantized, quantized_linear,
+                    quantized_linear_split)
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
 
 
@@ -323,11 +324,12 @@ class Qwen3_5LinearAttention:
         d = self.linear
         L = rows.shape[0]
         if self._in_stacked is not None:
-            out = quantized_linear(rows, self._in_stacked)
-            qkv, z, a, b = torch.split(out, [d.conv_dim, d.value_dim, d.num_value_heads,
-                                             d.num_value_heads], dim=-1)
-            # column slices of one output: the fused decode reads them in
-            # place, every other consumer copies what it needs packed
+            qkv, z, ab = quantized_linear_split(rows, self._in_stacked,
+                                                [d.conv_dim, d.value_dim, 2 * d.num_value_heads])
+            a, b = torch.split(ab, [d.num_value_heads, d.num_value_heads], dim=-1)
+            # at decode sizes column slices of one output (the fused decode
+            # reads them in place, every other consumer copies what it needs
+            # packed); at prefill sizes qkv and z are packed
             return qkv, z.reshape(L, d.num_value_heads, d.value_head_dim), a, b
         qkv = self._proj(rows, self.in_proj_qkv)
         z = self._proj(rows, self.in_proj_z).reshape(L, d.num_value_heads, d.value_head_dim)

@@ -149,6 +149,79 @@ def test_frontend_matches_oracle_varlen_with_short_runs(gpu):
                                    rtol=2 ** -7, atol=1e-6)
 
 
+def _frontend_vs_oracle(gpu, dims, qkv, conv, w, cu, conv_dev_dtype, pass_cu=True):
+    Hk, Hv, Dk = dims.num_key_heads, dims.num_value_heads, dims.key_head_dim
+    q, k, v, new_conv = gdn.conv_frontend(_t(qkv, gpu, torch.bfloat16), _t(conv, gpu, conv_dev_dtype),
+                                          _t(w, gpu), dims,
+                                          torch.tensor(cu, device=gpu) if pass_cu else None)
+    assert new_conv.dtype == torch.bfloat16
+    qkd = Hk * Dk
+    for i in range(len(cu) - 1):
+        s0, s1 = cu[i], cu[i + 1]
+        out, nc = R.convolve(qkv[s0:s1], conv[i], w, "bf16")
+        np.testing.assert_array_equal(new_conv[i].float().cpu().numpy(), nc)
+        if s1 == s0:
+            continue
+        qe, ke = R.qk_scale(out[:, :qkd].reshape(-1, Hk, Dk), out[:, qkd:2 * qkd].reshape(-1, Hk, Dk),
+                            "bf16")
+        np.testing.assert_allclose(q[s0:s1].float().cpu().numpy(), qe, atol=2e-3, rtol=1e-2)
+        np.testing.assert_allclose(k[s0:s1].float().cpu().numpy(), ke, atol=2e-3, rtol=1e-2)
+        np.testing.assert_allclose(v[s0:s1].float().cpu().numpy(), out[:, 2 * qkd:].reshape(-1, Hv, 128),
+                                   rtol=2 ** -7, atol=1e-6)
+
+
+def test_frontend_production_heads_ragged_runs_match_oracle(gpu):
+    """The tiled front-end (128-wide heads, 4 taps, bf16): runs that are
+    empty, shorter than the conv window, or cross the 16-token tiles, a
+    float32 conv state in, and a partial last tile."""
+
+    rng = np.random.default_rng(8)
+    lens = [0, 1, 2, 3, 16, 0, 37, 5, 70, 1]  # 135 tokens
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T, C = int(cu[-1]), DIMS_PROD.conv_dim
+    qkv = R.bf16_round(rng.standard_normal((T, C)))
+    conv = rng.standard_normal((len(lens), 3, C)).astype(np.float32)
+    w = (rng.standard_normal((C, 4)) * 0.2).astype(np.float32)
+    _frontend_vs_oracle(gpu, DIMS_PROD, qkv, conv, w, cu, torch.float32)
+
+
+def test_frontend_production_heads_equal_runs_match_oracle(gpu):
+    """N equal runs without cu_seqlens (the batched layer), bf16 conv state."""
+
+    rng = np.random.default_rng(9)
+    N, L = 3, 45
+    cu = (np.arange(N + 1) * L).astype(np.int32)
+    C = DIMS_PROD.conv_dim
+    qkv = R.bf16_round(rng.standard_normal((N * L, C)))
+    conv = R.bf16_round(rng.standard_normal((N, 3, C)))
+    w = (rng.standard_normal((C, 4)) * 0.2).astype(np.float32)
+    _frontend_vs_oracle(gpu, DIMS_PROD, qkv, conv, w, cu, torch.bfloat16, pass_cu=False)
+
+
+@pytest.mark.parametrize("D,rows,x_dtype", [(128, 21, torch.float32), (128, 21, torch.bfloat16),
+                                            (64, 13, torch.float32), (256, 7, torch.bfloat16)])
+@pytest.mark.parametrize("misaligned", [False, True])
+def test_gated_rms_norm_row_shapes_match_oracle(gpu, D, rows, x_dtype, misaligned):
+    """bf16 gate and result: 16-byte rows take the vectorised kernel (8
+    elements a lane, several rows a wave, the last wave part empty), a
+    misaligned x the general one; both as the oracle."""
+
+    rng = np.random.default_rng(D + rows)
+    y = rng.standard_normal((rows, D)).astype(np.float32)
+    if x_dtype == torch.bfloat16:
+        y = R.bf16_round(y).astype(np.float32)
+    z = R.bf16_round(rng.standard_normal((rows, D)))
+    w = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    x = _t(y, gpu, x_dtype)
+    if misaligned:
+        buf = torch.empty(rows * D + 1, dtype=x_dtype, device=gpu)
+        buf[1:] = x.reshape(-1)
+        x = buf[1:].view(rows, D)
+    out = gdn.gated_rms_norm(x, _t(z, gpu, torch.bfloat16), _t(w, gpu), 1e-6, out_dtype=torch.bfloat16)
+    expected = R.gated_rms_norm(R.act_round(y, "bf16"), z, w, 1e-6, "bf16")
+    assert_bf16_out_close(out.float().cpu().numpy(), expected)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gated_rms_norm_matches_oracle(gpu, dtype):
     rng = np.random.default_rng(6)

@@ -208,9 +208,35 @@ def test_non_bf16_activations_use_dense_weights(gpu):
     assert np.abs(y.cpu().numpy() - ref).max() < 1e-4
 
 
-def test_layer_with_quantized_projections_matches_dense_weights(gpu):
+@pytest.mark.parametrize("M", [64, 600])
+def test_stacked_projection_blocks_match_the_oracle(gpu, M):
+    """quantized_linear_split: one quantized launch split into column views
+    below 512 rows, one dequantization and a GEMM per block (packed) from
+    512 rows on; either way each block is x @ W_block.T."""
+
+    from mlx_lean_moe_amd.quant import concat_quantized, quantized_linear_split
+
+    rng = np.random.default_rng(M)
+    sizes, K = [96, 64, 16], 512
+    parts = [_weights(rng, n, K, 4, 64, "bf16") for n in sizes]
+    stacked = gdn.LinearWeights(concat_quantized([_dev_weights(gpu, *p, "bf16") for p in parts]),
+                                gdn.QuantScheme(4, 64))
+    x = R.bf16_round(rng.standard_normal((M, K)))
+    xt = torch.tensor(x, dtype=torch.float32, device=gpu).to(torch.bfloat16)
+    blocks = quantized_linear_split(xt, stacked, sizes)
+    exact = _decode_kernel_takes(M, K, 4, 64, "bf16")
+    for blk, (words, s, b), n in zip(blocks, parts, sizes):
+        assert tuple(blk.shape) == (M, n) and blk.dtype == torch.bfloat16
+        assert blk.is_contiguous() == (M >= 512)
+        ref = Q.quantized_matmul(x, words, s, b, 4, 64, w_round="f32" if exact else "bf16")
+        assert_bf16_out_close(blk.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("T", [70, 600])
+def test_layer_with_quantized_projections_matches_dense_weights(gpu, T):
     """The reference's layer test setup: quantized projections against the
-    same layer on the dequantized dense weights, decode and prefill."""
+    same layer on the dequantized dense weights, decode and prefill (600
+    prompt tokens: the stacked input projection as one GEMM per block)."""
 
     dims = gdn.LinearAttentionDims(2, 4, 128, 128, 4)
     dt = (2, 4, 128, 128)
@@ -238,7 +264,7 @@ def test_layer_with_quantized_projections_matches_dense_weights(gpu):
 
     lq, ld = make(quant, scheme), make(dense, None)
     assert lq._in_stacked is not None  # one launch for the four input projections
-    x = torch.tensor(R.bf16_round(rng.standard_normal((70, H))), dtype=torch.float32,
+    x = torch.tensor(R.bf16_round(rng.standard_normal((T, H))), dtype=torch.float32,
                      device=gpu).to(torch.bfloat16)
     cq, cd = lq.new_cache(torch.bfloat16), ld.new_cache(torch.bfloat16)
     oq, od = lq(x, cq), ld(x, cd)

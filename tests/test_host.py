@@ -145,6 +145,16 @@ def test_conv_half_bits_and_residuals_are_checked_on_the_host():
             _check_residual(r, (2, 5), torch.bfloat16)
 
 
+def test_stacked_projection_block_sizes_must_cover_the_rows(no_launch):
+    from mlx_lean_moe_amd.quant import quantized_linear_split
+
+    w = gdn.LinearWeights({"weight": torch.zeros(10, 16, dtype=torch.int32),
+                           "scales": torch.ones(10, 2, dtype=torch.bfloat16),
+                           "biases": torch.zeros(10, 2, dtype=torch.bfloat16)}, gdn.QuantScheme(4, 64))
+    with pytest.raises(ValueError, match="do not add up"):
+        quantized_linear_split(torch.zeros(3, 128, dtype=torch.bfloat16), w, [4, 5])
+
+
 def test_pool_host_bookkeeping_flips_bits_and_sizes():
     """The pool's host copies of the half bits and sizes (NumPy views of its
     torch tensors): a decode of some slots flips exactly their bits and adds
