@@ -17,9 +17,12 @@ Also measured in the same run (reported under "also"):
   of 256 slots, from HIP graphs
   (--workload layer_decode: the same alone, with its parts,
   --batch B active sequences, 64 by default)
+  layer_prefill: the whole layer over a 4096-token prompt, 4-bit
+  projections (--workload layer_prefill: the same alone)
 
 python bench.py [--steps K] [--warmup W] [--batch B]
-                [--workload decode|decode_large|decode_slots|layer_decode|prefill|prefill_varlen|qlinear|copy]
+                [--workload decode|decode_large|decode_slots|layer_decode|layer_prefill|prefill|
+                            prefill_varlen|qlinear|copy]
 """
 
 from __future__ import annotations
@@ -668,6 +671,7 @@ def main(argv=None):
             pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
             sl = bench_decode_slots(dev, 64, 16, 32, steps=64, warmup=8)
             ld = bench_layer_decode(dev, 64, steps=64, warmup=8)
+            lp = bench_layer_prefill(dev, 4096, steps=20, warmup=3)
             line["also"] = {
                 "decode_slots": sl,
                 "layer_decode": {
@@ -675,6 +679,10 @@ def main(argv=None):
                     "tokens_per_s": ld["graph_tokens_per_s"], "step_us": ld["graph_step_us"],
                     "input_projection_us": ld["input_projection_us"],
                     "out_proj_us": ld["out_proj_us"]},
+                "layer_prefill": {
+                    "workload": lp["workload"], "tokens_per_s": lp["tokens_per_s"],
+                    "step_us": lp["step_us"], "input_projection_us": lp["input_projection_us"],
+                    "core_us": lp["core_us"], "out_proj_us": lp["out_proj_us"]},
                 "decode_large": {
                     "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
                     "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],

@@ -225,7 +225,7 @@ def _check_cu_seqlens(cu_seqlens, T: int) -> list[int]:
 
 
 def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=None,
-                       use_kernel: bool = True):
+                       use_kernel: bool = True, y_dtype: torch.dtype | None = None):
     """Gated-delta update with the gates computed from ``a, b`` inside
     (beta = sigmoid(b), g = forget_gate(a, A_log, dt_bias)).
 
@@ -233,7 +233,12 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
     ``a, b (B, L, Hv)``, ``state (B, Hv, Dv, Dk)`` or None (zeros, float32).
     Packed: with ``cu_seqlens`` (N+1 offsets) ``q, k (T, Hk, Dk)``,
     ``v (T, Hv, Dv)``, ``a, b (T, Hv)``, ``state (N, Hv, Dv, Dk)``; each run
-    starts from its own state. Returns ``(y, new_state)``."""
+    starts from its own state. Returns ``(y, new_state)``.
+
+    ``y`` comes in the promotion of the inputs' dtypes (float32 with a
+    float32 state); ``y_dtype`` asks for it rounded to nearest even into that
+    dtype instead, the values of ``y.to(y_dtype)`` without the float32 copy
+    (the layer's output cast, linear_attention.py:122-124)."""
 
     packed = cu_seqlens is not None
     lead = 1 if packed else 2
@@ -264,7 +269,10 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
     cu = (torch.tensor(offsets, dtype=torch.int32, device=device) if packed else None)
     if state is None:
         state = torch.zeros((N, Hv, Dv, Dk), dtype=torch.float32, device=device)
-    y_dtype = _promote(q, k, v, b, state, torch.empty(0, dtype=torch.float32))
+    if y_dtype is None:
+        y_dtype = _promote(q, k, v, b, state, torch.empty(0, dtype=torch.float32))
+    elif y_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"y_dtype must be a float dtype, got {y_dtype}")
     s_dtype = _promote(k, v, b, state, torch.empty(0, dtype=torch.float32))
     qk_dtype = _promote(q, k)
     q, k = q.to(qk_dtype), k.to(qk_dtype)

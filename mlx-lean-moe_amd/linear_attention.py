@@ -349,13 +349,14 @@ class Qwen3_5LinearAttention:
         if cu_seqlens is not None:
             cu_dev = torch.as_tensor(cu_seqlens, dtype=torch.int32).to(qkv.device)
         q, k, v, new_conv = conv_frontend(qkv, conv_state, self.conv1d_weight, d, cu_dev)
+        # y straight in z's dtype: the norm's first step rounds it there
         if cu_seqlens is None:
             y, new_ssm = gated_delta_update(q[None], k[None], v[None], a[None], b[None],
-                                            self.A_log, self.dt_bias, ssm_state)
+                                            self.A_log, self.dt_bias, ssm_state, y_dtype=z.dtype)
             y = y[0]
         else:
             y, new_ssm = gated_delta_update(q, k, v, a, b, self.A_log, self.dt_bias, ssm_state,
-                                            cu_seqlens=cu_seqlens)
+                                            cu_seqlens=cu_seqlens, y_dtype=z.dtype)
         out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out_dtype=z.dtype)
         return out.reshape(T, d.value_dim), new_conv, new_ssm
 

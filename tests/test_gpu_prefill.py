@@ -230,6 +230,24 @@ def test_prefill_full_size_against_c_oracle(gpu):
     assert max_rel(s.cpu().numpy(), s2.cpu().numpy()) < 1e-4
 
 
+@pytest.mark.parametrize("T", [96, 20])  # the chunked kernel; the sequential scan
+def test_update_y_dtype_is_the_rounded_float32_output(gpu, T):
+    """gated_delta_update(..., y_dtype=bf16) gives y.to(bf16) bit for bit
+    (what the layer's norm reads), the state unchanged."""
+
+    arrays = _cfg_inputs(7, T, Hk=2, Hv=4)
+    t = _dev(gpu, arrays)
+    args = (t["q"][None], t["k"][None], t["v"][None], t["a"][None], t["b"][None], t["A_log"],
+            t["dt_bias"], t["state"])
+    y32, s32 = gdn.gated_delta_update(*args)
+    y16, s16 = gdn.gated_delta_update(*args, y_dtype=torch.bfloat16)
+    assert y32.dtype == torch.float32 and y16.dtype == torch.bfloat16
+    assert torch.equal(y16, y32.to(torch.bfloat16))
+    assert torch.equal(s16, s32)
+    with pytest.raises(ValueError, match="y_dtype"):
+        gdn.gated_delta_update(*args, y_dtype=torch.int32)
+
+
 def test_prefill_bf16_output_and_zero_state_pointer(gpu):
     arrays = _cfg_inputs(5, 96, Hk=2, Hv=4)  # zero initial state
     t = _dev(gpu, arrays)
