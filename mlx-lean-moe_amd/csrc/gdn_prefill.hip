@@ -663,12 +663,25 @@ GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassL
         y2 = mfma16(op.pal[s], bh, y2);
     }
     yacc += y2;
-    const int64_t t0 = cx.t0(c);
+    // Stores through a buffer resource that ends at the chunk's last token:
+    // rows past the run fall outside it and the hardware drops them, so the
+    // loop has no branch here (a branch lets the compiler sink the next
+    // chunk's prefetch below it and wait for every outstanding load).
+    using St = typename Y::storage;
     const int len = cx.len(c);
+    const auto yr = __builtin_amdgcn_make_buffer_rsrc(y + cx.t0(c) * cx.Hv * kHD, 0,
+                                                      len * cx.Hv * kHD * int(sizeof(St)), 0x00020000);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tok = 16 * w + 4 * lq + i;
-        if (tok < len) Y::store(y, ((t0 + tok) * cx.Hv + cx.h) * kHD + cx.dv0 + lr, yacc[i]);
+        const int off = ((tok * cx.Hv + cx.h) * kHD + cx.dv0 + lr) * int(sizeof(St));
+        if constexpr (Y::code == GDN_F32) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yacc[i]), yr, off, 0, 0);
+        } else if constexpr (Y::code == GDN_BF16) {
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(yacc[i]), yr, off, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_f16_bits(yacc[i]), yr, off, 0, 0);
+        }
     }
 }
 
@@ -712,11 +725,13 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
         __syncthreads();
         const f32x4 yacc = output_project(sm, w, l);
         fetch_output<kUpper>(on, cx, c + 1 < last ? c + 1 : last, w, l);
+        __builtin_amdgcn_sched_barrier(0);  // the prefetches stay where they are issued
         __syncthreads();
         stage_q(gn, sm, w, l);
         stage_k(gn, sm, buf ^ 1, w, l);
         stage_v(gn, sm, w, l);
         fetch_staged<kUpper>(gf, cx, c + 2 < last ? c + 2 : last, w, l);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         stage_tb_e<kUpper>(gn, sm, w, l);
         output_store<Y, kUpper>(oc, yacc, sm, cx, c, y, w, l);
