@@ -279,11 +279,13 @@ def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
             "input_projection_us": in_us, "out_proj_us": out_us}
 
 
-def bench_layer_prefill(dev, T, steps, warmup, hidden=2048):
+def bench_layer_prefill(dev, T, steps, warmup, hidden=2048, chunk=512):
     """The whole gated-delta layer (Hk=16, Hv=32, d=128, 4-bit group-64
     projections, bf16 activations) over a T-token prompt: one layer(x, cache)
     call per step, the cache carried from step to step. Also times its
-    three parts alone (input projections, everything between them, out_proj)."""
+    three parts alone (input projections, everything between them, out_proj),
+    and a prompt prefilled in `chunk`-token pieces, eager and from a
+    PrefillGraph."""
 
     d = gdn.QWEN3_5_LINEAR
     layer, g, rnd = quantized_layer(dev, hidden)
@@ -297,13 +299,21 @@ def bench_layer_prefill(dev, T, steps, warmup, hidden=2048):
     in_ms, _ = time_steps(lambda s_: layer._project(x), steps, warmup)
     core_ms, _ = time_steps(lambda s_: layer.core(qkv, z, a, b, conv[None], ssm[None]), steps, warmup)
     out_ms, _ = time_steps(lambda s_: gdn.quantized_linear(o, layer.out_proj), steps, warmup)
+    xc = [rnd(chunk, hidden).to(torch.bfloat16) for _ in range(2)]
+    ce, cg = layer.new_cache(), layer.new_cache()
+    chunk_eager_ms, _ = time_steps(lambda s_: layer(xc[s_ % 2], ce), steps, warmup)
+    pg = gdn.PrefillGraph(layer, xc[0])
+    chunk_graph_ms, _ = time_steps(lambda s_: pg.step(cg, xc[s_ % 2]), steps, warmup)
     ms = total_ms / steps
     proj_flops = 2 * T * hidden * (d.conv_dim + d.value_dim + 2 * d.num_value_heads + d.value_dim)
     return {"workload": f"gated-delta layer prefill, T={T}, hidden {hidden}, 4-bit group-64 "
                         f"projections, bf16 activations",
             "tokens_per_s": T / (ms * 1e-3), "step_us": ms * 1e3,
             "input_projection_us": in_ms / steps * 1e3, "core_us": core_ms / steps * 1e3,
-            "out_proj_us": out_ms / steps * 1e3, "projection_flops": proj_flops}
+            "out_proj_us": out_ms / steps * 1e3, "projection_flops": proj_flops,
+            "chunk": chunk, "chunk_eager_us": chunk_eager_ms / steps * 1e3,
+            "chunk_graph_us": chunk_graph_ms / steps * 1e3,
+            "chunk_graph_tokens_per_s": chunk / (chunk_graph_ms / steps * 1e-3)}
 
 
 def bench_decode_slots(dev, B, Hk, Hv, steps, warmup):
@@ -682,7 +692,9 @@ def main(argv=None):
                 "layer_prefill": {
                     "workload": lp["workload"], "tokens_per_s": lp["tokens_per_s"],
                     "step_us": lp["step_us"], "input_projection_us": lp["input_projection_us"],
-                    "core_us": lp["core_us"], "out_proj_us": lp["out_proj_us"]},
+                    "core_us": lp["core_us"], "out_proj_us": lp["out_proj_us"],
+                    "chunk512_eager_us": lp["chunk_eager_us"],
+                    "chunk512_graph_us": lp["chunk_graph_us"]},
                 "decode_large": {
                     "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
                     "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],
@@ -723,7 +735,10 @@ def main(argv=None):
                           "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                           "data": "synthetic", "config": {"workload": r["workload"]},
                           "parts_us": {"input_projection": r["input_projection_us"],
-                                       "core": r["core_us"], "out_proj": r["out_proj_us"]}}))
+                                       "core": r["core_us"], "out_proj": r["out_proj_us"]},
+                          "chunked": {"chunk": r["chunk"], "eager_step_us": r["chunk_eager_us"],
+                                      "graph_step_us": r["chunk_graph_us"],
+                                      "graph_tokens_per_s": r["chunk_graph_tokens_per_s"]}}))
         return 0
 
     if args.workload == "decode_slots":

@@ -10,13 +10,14 @@ hand-written HIP kernels for gfx950 in ``libgdn.so`` (C ABI in
 from .config import QWEN3_5_LINEAR, LinearAttentionDims
 from .gated_delta import (beta_gate, forget_gate, gated_delta_scan, gated_delta_step,
                           gated_delta_update)
-from .linear_attention import (DecodeGraph, Qwen3_5LinearAttention, conv_frontend,
+from .linear_attention import (DecodeGraph, PrefillGraph, Qwen3_5LinearAttention, conv_frontend,
                                fused_decode_step, gated_rms_norm)
 from .quant import LinearWeights, QuantScheme, dequantize, quantized_linear
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
 
 __all__ = [
     "DecodeGraph",
+    "PrefillGraph",
     "LinearAttentionDims",
     "LinearWeights",
     "QuantScheme",

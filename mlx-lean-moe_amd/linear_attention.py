@@ -372,23 +372,28 @@ class Qwen3_5LinearAttention:
             raise ValueError(f"Qwen3_5LinearAttention expects 1-D or 2-D x, got shape {tuple(x.shape)}")
         squeeze = x.ndim == 1
         rows = x[None, :] if squeeze else x
-        L = rows.shape[0]
-        d = self.linear
-        qkv, z, a, b = self._project(rows)
-        conv_state, ssm_state = cache.state()
-        act = qkv.dtype
-        if L == 1 and _fused_decode_ok(d, act):
-            out, new_conv, new_ssm = self._decode_fused(qkv, z, a, b, conv_state[None].to(act),
-                                                        ssm_state[None], in_place=False)
-            out, new_conv, new_ssm = out.reshape(1, d.value_dim), new_conv[0], new_ssm[0]
-        else:
-            out, new_conv, new_ssm = self.core(qkv, z, a, b, conv_state[None], ssm_state[None])
-            new_conv, new_ssm = new_conv[0], new_ssm[0]
-        cache.update(new_conv, new_ssm, advance=L)
         if residual is not None and squeeze:
             residual = residual[None, :]
-        out = self._proj(out, self.out_proj, residual)
+        conv_state, ssm_state = cache.state()
+        out, new_conv, new_ssm = self._rows_step(rows, conv_state, ssm_state, residual)
+        cache.update(new_conv, new_ssm, advance=rows.shape[0])
         return out[0] if squeeze else out
+
+    def _rows_step(self, rows, conv_state, ssm_state, residual=None):
+        """The layer over ``rows (L, hidden)`` of one sequence from
+        ``conv_state (K-1, C)`` and ``ssm_state (Hv, Dv, Dk)``: returns
+        ``(out (L, hidden), new_conv, new_ssm)`` in fresh tensors."""
+
+        d = self.linear
+        qkv, z, a, b = self._project(rows)
+        act = qkv.dtype
+        if rows.shape[0] == 1 and _fused_decode_ok(d, act):
+            out, new_conv, new_ssm = self._decode_fused(qkv, z, a, b, conv_state[None].to(act),
+                                                        ssm_state[None], in_place=False)
+            out = out.reshape(1, d.value_dim)
+        else:
+            out, new_conv, new_ssm = self.core(qkv, z, a, b, conv_state[None], ssm_state[None])
+        return self._proj(out, self.out_proj, residual), new_conv[0], new_ssm[0]
 
     def _decode_fused(self, qkv, z, a, b, conv_state, ssm_state, in_place: bool,
                       conv_out: torch.Tensor | None = None):
@@ -476,3 +481,68 @@ class DecodeGraph:
         self.pool.flip_host(self._idx)
         return self.out
 
+
+
+class PrefillGraph:
+    """One ``layer(x, cache)`` call over a fixed-length chunk of a prompt,
+    captured in a HIP graph: a serving loop that prefills prompts in chunks
+    of ``len(x_example)`` tokens replays the chunk's kernels (projections,
+    front-end, chunked prefill, gated norm, out_proj) without issuing them
+    one by one from Python, which at a few hundred tokens per chunk takes
+    longer than the kernels themselves.
+
+    The graph reads ``self.x`` (and ``self.residual`` when captured with
+    ``residual_example``) and the sequence's state from ``self.conv_state``
+    and ``self.ssm_state``, writes ``self.out`` and leaves the new state in
+    the same two buffers. ``step(cache, x)`` copies ``x`` in, copies the
+    cache's state in unless the cache already holds these buffers, replays,
+    and points the cache at the buffers (``cache.update``): consecutive
+    chunks of one sequence run without copies, and the cache's state tensors
+    then change with every later step of this graph: clone them to keep a
+    snapshot, and before another sequence's step on the same graph. Shapes
+    and buffers are fixed at capture; a prompt's last, shorter chunk runs
+    through ``layer`` as usual."""
+
+    def __init__(self, layer: "Qwen3_5LinearAttention", x_example: torch.Tensor,
+                 residual_example: torch.Tensor | None = None) -> None:
+        if x_example.ndim != 2 or x_example.shape[0] < 2:
+            raise ValueError("x_example must be (chunk, hidden) with at least two tokens")
+        d = layer.linear
+        dev = x_example.device
+        self.layer = layer
+        self.chunk = x_example.shape[0]
+        self.x = x_example.detach().clone()
+        self.residual = None if residual_example is None else residual_example.detach().clone()
+        self.conv_state = torch.zeros((d.conv_kernel_dim - 1, d.conv_dim), dtype=self.x.dtype, device=dev)
+        self.ssm_state = torch.zeros((d.num_value_heads, d.value_head_dim, d.key_head_dim),
+                                     dtype=torch.float32, device=dev)
+        # one eager call first: lazily built operands (dequantized weights'
+        # workspace sizes, BLAS handles) exist before capture
+        layer._rows_step(self.x, self.conv_state, self.ssm_state, self.residual)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out, new_conv, new_ssm = layer._rows_step(self.x, self.conv_state, self.ssm_state,
+                                                           self.residual)
+            self.conv_state.copy_(new_conv)
+            self.ssm_state.copy_(new_ssm)
+
+    def step(self, cache: RecurrentCache, x: torch.Tensor | None = None,
+             residual: torch.Tensor | None = None) -> torch.Tensor:
+        if x is not None and x is not self.x:
+            if tuple(x.shape) != tuple(self.x.shape):
+                raise ValueError(f"x must be {tuple(self.x.shape)}, got {tuple(x.shape)}")
+            self.x.copy_(x)
+        if residual is not None:
+            if self.residual is None:
+                raise ValueError("this chunk was captured without a residual")
+            if residual is not self.residual:
+                self.residual.copy_(residual)
+        conv, ssm = cache.state()
+        if conv is not self.conv_state:
+            self.conv_state.copy_(conv)
+        if ssm is not self.ssm_state:
+            self.ssm_state.copy_(ssm)
+        self.graph.replay()
+        cache.update(self.conv_state, self.ssm_state, advance=self.chunk)
+        return self.out
