@@ -33,8 +33,22 @@ _KERNEL_BITS = {4, 8}
 # From this many rows on, quantized_linear dequantizes the weights to bf16
 # once and multiplies on the vendor BLAS (measured at hidden 2048 -> 12352:
 # 73 vs 103 us at 1024 rows, 242 vs 336 us at 4096; even at 512 rows);
-# below it gdn_quantized_matmul's kernels run directly.
+# below it gdn_quantized_matmul's kernels run directly, see _dense_rows.
 _BLAS_ROWS = 512
+
+
+def _dense_rows(rows: int, N: int, K: int) -> bool:
+    """Whether ``rows`` bf16 rows times a quantized ``(N, K)`` weight run on
+    dequantized weights and the vendor BLAS rather than the quantized
+    kernels. Above 64 rows the quantized tiled kernel takes 128 x 128 tiles
+    with no K split, so a narrow or deep weight leaves the GPU idle: for
+    4096 -> 2048 (out_proj) it takes 73-76 us from 65 to 1024 rows against
+    23-34 us dense; for 2048 -> 12352 it wins up to ~400 rows (41-44 us
+    against 45-57 us, device time from graphs)."""
+
+    if rows >= _BLAS_ROWS:
+        return True
+    return rows > 64 and (N < 4096 or K >= 4096)
 
 
 @dataclass(frozen=True)
@@ -165,9 +179,9 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None,
     if x.dtype != torch.bfloat16 and not x_f32:
         return with_residual(x @ dequantize(tensors, quant, x.dtype).T)
     x2 = _c(x.reshape(-1, K))
-    if x2.shape[0] >= _BLAS_ROWS:
-        # prefill-sized: the same bf16-rounded weights (gdn_dequantize), one
-        # transient copy, and the vendor BLAS for the GEMM itself
+    if _dense_rows(x2.shape[0], N, K):
+        # the same bf16-rounded weights as the tiled kernel (gdn_dequantize),
+        # one transient copy, and the vendor BLAS for the GEMM itself
         return with_residual((x2 @ dequantize(tensors, quant, torch.bfloat16).T).reshape(*lead, N))
     if x2.data_ptr() % 16:
         x2 = x2.clone()
@@ -197,9 +211,9 @@ def quantized_linear_split(x: torch.Tensor, weights: LinearWeights, sizes) -> li
     (which sum to ``W``'s rows): what :func:`quantized_linear` of each
     projection would give, in one launch where that pays.
 
-    At prefill sizes (bf16 ``x`` of ``_BLAS_ROWS`` rows or more) ``W`` is
-    dequantized once and each block is its own GEMM on the vendor BLAS with a
-    packed output: for hidden 2048 -> 8192|4096|64 at 4096 rows the blocks
+    Where the dense path runs (bf16 ``x``, :func:`_dense_rows`: prefill
+    sizes) ``W`` is dequantized once and each block is its own GEMM on the
+    vendor BLAS with a packed output: for hidden 2048 -> 8192|4096|64 at 4096 rows the blocks
     take 159 us together against 246 us for one 12352-column product (the
     library tiles that N poorly). Below it one quantized launch computes all
     columns and the blocks are column views of its output."""
@@ -211,7 +225,8 @@ def quantized_linear_split(x: torch.Tensor, weights: LinearWeights, sizes) -> li
                          f"stacked rows")
     K = x.shape[-1]
     rows = x.reshape(-1, K).shape[0]
-    if x.dtype == torch.bfloat16 and rows >= _BLAS_ROWS and x.device.type == "cuda":
+    if (x.dtype == torch.bfloat16 and x.device.type == "cuda"
+            and _dense_rows(rows, tensors["weight"].shape[0], K)):
         _kernel_scheme(quant)
         _check_quantized(tensors, quant, K)
         lead = x.shape[:-1]

@@ -155,6 +155,17 @@ def test_stacked_projection_block_sizes_must_cover_the_rows(no_launch):
         quantized_linear_split(torch.zeros(3, 128, dtype=torch.bfloat16), w, [4, 5])
 
 
+def test_dense_path_choice_follows_the_measured_crossovers():
+    from mlx_lean_moe_amd.quant import _dense_rows
+
+    assert not _dense_rows(64, 2048, 4096)       # decode sizes: quantized kernels
+    assert _dense_rows(65, 2048, 4096)           # out_proj above 64 rows: dense
+    assert not _dense_rows(300, 12352, 2048)     # the stacked input projection: tiled kernel
+    assert _dense_rows(512, 12352, 2048)         # prefill sizes: dense for every shape
+    assert _dense_rows(200, 12352, 4096)         # deep weights
+    assert _dense_rows(100, 300, 512)            # narrow weights
+
+
 def test_pool_host_bookkeeping_flips_bits_and_sizes():
     """The pool's host copies of the half bits and sizes (NumPy views of its
     torch tensors): a decode of some slots flips exactly their bits and adds
