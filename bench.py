@@ -394,7 +394,7 @@ class PrefillWorkload:
 
         self._fn = _lib.load().gdn_prefill_chunked
         self._args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.a.data_ptr(),
-                      self.b.data_ptr(), _lib.GDN_BF16, self.A_log.data_ptr(),
+                      self.b.data_ptr(), _lib.GDN_BF16, Hv, self.A_log.data_ptr(),
                       self.dt_bias.data_ptr(), 0,
                       None if self.state_in is None else self.state_in.data_ptr(),
                       self.state_out.data_ptr(), self.y.data_ptr(), _lib.GDN_BF16,

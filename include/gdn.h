@@ -49,7 +49,7 @@ typedef enum {
  * slots, 4 its conv rows, 5 replaces the conv rows with the pool's half bits,
  * adds input row strides and gdn_pool_advance, 6 the quantized matmul's
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
- * residual). */
+ * residual, 8 the prefill's gate row stride). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -183,6 +183,9 @@ int gdn_pool_advance(const int32_t *slots, int B, int32_t *conv_half, int pool, 
  *   gate_mode 0: ga = a, gb = b, both (T_total, Hv) in gb_dtype, with A_log and
  *                dt_bias (Hv) float32 (gates computed in-kernel, beta held in gb_dtype)
  *   gate_mode 1: ga = g (T_total, Hv) float32, gb = beta (T_total, Hv) gb_dtype
+ *   gate_stride: elements between consecutive tokens' rows of ga and gb (>= Hv;
+ *                Hv when packed), so a and b may be column slices of one
+ *                projection output
  *   state_in: (N, Hv, Dv, Dk) float32 or NULL (zero state); state_out: (N, Hv, Dv, Dk),
  *             not aliasing state_in
  *   q, k, states and workspace 16-byte aligned, v 8-byte aligned
@@ -194,7 +197,7 @@ int gdn_pool_advance(const int32_t *slots, int B, int32_t *conv_half, int pool, 
  */
 int64_t gdn_prefill_workspace_size(int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv);
 int gdn_prefill_chunked(const void *q, const void *k, const void *v, const void *ga,
-                        const void *gb, int gb_dtype, const float *A_log,
+                        const void *gb, int gb_dtype, int64_t gate_stride, const float *A_log,
                         const float *dt_bias, int gate_mode, const float *state_in,
                         float *state_out, void *y, int y_dtype, const int32_t *cu_seqlens,
                         int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv, void *workspace,

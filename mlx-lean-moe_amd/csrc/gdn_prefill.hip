@@ -235,7 +235,7 @@ GDN_DEV void offdiag_inverse(float* As, float* Ts, int w, int l) {
 // but the first read that chunk's K and Q from the XCD's L2.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_chunk_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const void* __restrict__ ga,
-    const void* __restrict__ gb, int gb_dtype, const float* __restrict__ A_log,
+    const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
     int Hk, int Hv) {
     // K/Q tiles first; once K K^T and K Q^T are in registers the same bytes
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     // (exp2 of differences gives the decays).
     if (w == 0) {
         const int lc = l < pos.len ? l : pos.len - 1;
-        const int64_t i = (pos.t0 + lc) * Hv + hv;
+        const int64_t i = (pos.t0 + lc) * gate_stride + hv;
         float lg, beta;
         if (gate_mode == 0) {
             lg = log_forget_gate(load_any(ga, i, gb_dtype), A_log[hv], dt_bias[hv]);
@@ -833,7 +833,7 @@ extern "C" int64_t gdn_prefill_workspace_size(int N, int64_t T_total, int Hk, in
 }
 
 extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* ga,
-                                   const void* gb, int gb_dtype, const float* A_log,
+                                   const void* gb, int gb_dtype, int64_t gate_stride, const float* A_log,
                                    const float* dt_bias, int gate_mode, const float* state_in,
                                    float* state_out, void* y, int y_dtype,
                                    const int32_t* cu_seqlens, int N, int64_t T_total, int Hk,
@@ -844,6 +844,8 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     if (Dk != kHD || Dv != kHD)
         return fail(GDN_EUNSUPPORTED, "gdn_prefill_chunked: specialised for Dk=Dv=128 (got %d, %d)", Dk, Dv);
     GDN_REQUIRE(gate_mode == 0 || gate_mode == 1, "gdn_prefill_chunked: gate_mode must be 0 or 1");
+    GDN_REQUIRE(gate_stride >= Hv, "gdn_prefill_chunked: gate_stride %lld below Hv=%d",
+                (long long)gate_stride, Hv);
     GDN_REQUIRE(valid_dtype(gb_dtype) && valid_dtype(y_dtype), "gdn_prefill_chunked: bad dtype");
     GDN_REQUIRE(gate_mode == 1 || (A_log && dt_bias), "gdn_prefill_chunked: gate_mode 0 needs A_log, dt_bias");
     GDN_REQUIRE(cu_seqlens || T_total % N == 0, "gdn_prefill_chunked: T_total not divisible by N");
@@ -883,7 +885,7 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     const int64_t items = (nchunks * Hk + 7) / 8 * 8;
     hipLaunchKernelGGL(prefill_chunk_kernel, dim3(unsigned(items * (Hv / Hk))), dim3(256), 0, s,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), ga, gb,
-                       gb_dtype, A_log, dt_bias, gate_mode, rl, records, Hk, Hv);
+                       gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl, records, Hk, Hv);
     if (int rc = check_launch("gdn_prefill_chunked/chunk")) return rc;
     const dim3 sgrid(unsigned(int64_t(N) * Hv * kSlices));
 #define GDN_STATE_LAUNCH(YT)                                                                      \

@@ -138,12 +138,13 @@ def prefill_workspace_bytes(N: int, T: int, Hk: int, Hv: int, Dk: int, Dv: int) 
 
 
 def _launch_prefill(q, k, v, ga, gb, A_log, dt_bias, gate_mode, state_in, state_out, y, cu, N, T,
-                    Hk, Hv, Dk, Dv, device, workspace=None):
+                    Hk, Hv, Dk, Dv, device, workspace=None, gate_stride=None):
     nbytes = prefill_workspace_bytes(N, T, Hk, Hv, Dk, Dv)
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
     _lib.call("gdn_prefill_chunked", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(ga),
-              _lib.ptr(gb), _lib.dtype_code(gb.dtype), _lib.ptr(A_log), _lib.ptr(dt_bias),
+              _lib.ptr(gb), _lib.dtype_code(gb.dtype), Hv if gate_stride is None else gate_stride,
+              _lib.ptr(A_log), _lib.ptr(dt_bias),
               gate_mode, _lib.ptr(state_in), _lib.ptr(state_out), _lib.ptr(y),
               _lib.dtype_code(y.dtype), _lib.ptr(cu), N, T, Hk, Hv, Dk, Dv,
               _lib.ptr(workspace), workspace.numel(), _stream(device))
@@ -276,17 +277,23 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
     s_dtype = _promote(k, v, b, state, torch.empty(0, dtype=torch.float32))
     qk_dtype = _promote(q, k)
     q, k = q.to(qk_dtype), k.to(qk_dtype)
-    q, k, v, a, b = (_c(t.reshape((T,) + tuple(t.shape[lead:]))) for t in (q, k, v, a, b))
+    q, k, v = (_c(t.reshape((T,) + tuple(t.shape[lead:]))) for t in (q, k, v))
+    a, b = a.reshape(T, Hv), b.reshape(T, Hv)
+    # a and b may be column slices of one projection output: the chunked
+    # prefill reads them with their row stride, every other path packs them
+    rows_ok = a.stride() == b.stride() and a.stride(1) == 1 and a.stride(0) >= Hv
     state_in = _c(state.to(s_dtype))
     y = torch.empty((T, Hv, Dv), dtype=y_dtype, device=device)
     state_out = torch.empty((N, Hv, Dv, Dk), dtype=s_dtype, device=device)
     if T > 0:
         if (use_kernel and s_dtype == torch.float32 and a.dtype == b.dtype == torch.bfloat16
                 and _prefill_eligible(q, k, v, mean_run)):
+            if not rows_ok:
+                a, b = _c(a), _c(b)
             _launch_prefill(q, k, v, a, b, _c(A_log.float()), _c(dt_bias.float()), 0, state_in,
-                            state_out, y, cu, N, T, Hk, Hv, Dk, Dv, device)
+                            state_out, y, cu, N, T, Hk, Hv, Dk, Dv, device, gate_stride=a.stride(0))
         else:
-            g, beta = _gates(a, b, A_log, dt_bias)
+            g, beta = _gates(_c(a), _c(b), A_log, dt_bias)
             name = "gdn_scan" if use_kernel and Dk in (32, 64, 128, 256) else "gdn_scan_reference"
             _launch_scan(name, q, k, v, g, beta, state_in, state_out, y, cu, N, T, Hk, Hv, Dk, Dv,
                          device)

@@ -67,6 +67,10 @@ def test_invalid_arguments_return_einval_without_launching():
                                  128, 128, 4, 1, slots, 4, slots, (ctypes.c_int64 * 4)(*strides), None,
                                  None)
         assert rc == _lib.GDN_EINVAL and what in _err(lib), (what, _err(lib))
+    # a gate row stride below Hv
+    rc = lib.gdn_prefill_chunked(*fake[:5], 1, 3, *fake[5:7], 0, None, fake[7], fake[8], 0, None, 1, 64,
+                                 2, 4, 128, 128, fake[9], 1 << 30, None)
+    assert rc == _lib.GDN_EINVAL and "gate_stride" in _err(lib), _err(lib)
     # overlapping conv state buffers are rejected
     p = ctypes.c_void_p(4096)
     rc = lib.gdn_frontend(p, p, p, 1, p, None, 1, 1, p, p, p, 1, 2, 32, 32, 4, 1, None)

@@ -230,6 +230,39 @@ def test_prefill_full_size_against_c_oracle(gpu):
     assert max_rel(s.cpu().numpy(), s2.cpu().numpy()) < 1e-4
 
 
+@pytest.mark.parametrize("packed", [False, True])
+def test_gates_as_column_slices_of_one_projection(gpu, packed):
+    """a and b as column views of one (T, 2 Hv) projection output (the
+    layer's a||b block): the chunked prefill reads them with their row
+    stride, bit for bit the packed call; the scan path packs them."""
+
+    T, Hv = 200, 4
+    arrays = _cfg_inputs(9, T, Hk=2, Hv=Hv)
+    t = _dev(gpu, arrays)
+    ab = torch.cat([t["a"], t["b"]], dim=-1)
+    a, b = ab[:, :Hv], ab[:, Hv:]
+    assert a.stride() == (2 * Hv, 1)
+    if packed:
+        cu = [0, 70, 70, 200]
+        state = torch.zeros(3, Hv, 128, 128, device=gpu)
+        run = lambda a_, b_: gdn.gated_delta_update(t["q"], t["k"], t["v"], a_, b_, t["A_log"],
+                                                    t["dt_bias"], state, cu_seqlens=cu)
+    else:
+        run = lambda a_, b_: gdn.gated_delta_update(t["q"][None], t["k"][None], t["v"][None],
+                                                    a_[None], b_[None], t["A_log"], t["dt_bias"],
+                                                    t["state"])
+    y1, s1 = run(a, b)
+    y2, s2 = run(a.contiguous(), b.contiguous())
+    assert torch.equal(y1, y2) and torch.equal(s1, s2)
+    # the scan path (runs under 64 tokens) with the same views
+    y3, s3 = gdn.gated_delta_update(t["q"][None, :20], t["k"][None, :20], t["v"][None, :20],
+                                    a[None, :20], b[None, :20], t["A_log"], t["dt_bias"], t["state"])
+    y4, s4 = gdn.gated_delta_update(t["q"][None, :20], t["k"][None, :20], t["v"][None, :20],
+                                    a[None, :20].contiguous(), b[None, :20].contiguous(), t["A_log"],
+                                    t["dt_bias"], t["state"])
+    assert torch.equal(y3, y4) and torch.equal(s3, s4)
+
+
 @pytest.mark.parametrize("T", [96, 20])  # the chunked kernel; the sequential scan
 def test_update_y_dtype_is_the_rounded_float32_output(gpu, T):
     """gated_delta_update(..., y_dtype=bf16) gives y.to(bf16) bit for bit
