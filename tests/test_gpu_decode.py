@@ -170,19 +170,23 @@ def _frontend_vs_oracle(gpu, dims, qkv, conv, w, cu, conv_dev_dtype, pass_cu=Tru
                                    rtol=2 ** -7, atol=1e-6)
 
 
-def test_frontend_production_heads_ragged_runs_match_oracle(gpu):
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (3, 6), (1, 1)])
+def test_frontend_production_heads_ragged_runs_match_oracle(gpu, Hk, Hv):
     """The tiled front-end (128-wide heads, 4 taps, bf16): runs that are
     empty, shorter than the conv window, or cross the 16-token tiles, a
-    float32 conv state in, and a partial last tile."""
+    float32 conv state in, and a partial last tile. Three key heads put k
+    and v heads in one wave (the v lanes skip the norm); one of each leaves
+    a wave's fourth group of lanes idle."""
 
-    rng = np.random.default_rng(8)
+    dims = gdn.LinearAttentionDims(Hk, Hv, 128, 128, 4)
+    rng = np.random.default_rng(8 + Hk)
     lens = [0, 1, 2, 3, 16, 0, 37, 5, 70, 1]  # 135 tokens
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
-    T, C = int(cu[-1]), DIMS_PROD.conv_dim
+    T, C = int(cu[-1]), dims.conv_dim
     qkv = R.bf16_round(rng.standard_normal((T, C)))
     conv = rng.standard_normal((len(lens), 3, C)).astype(np.float32)
     w = (rng.standard_normal((C, 4)) * 0.2).astype(np.float32)
-    _frontend_vs_oracle(gpu, DIMS_PROD, qkv, conv, w, cu, torch.float32)
+    _frontend_vs_oracle(gpu, dims, qkv, conv, w, cu, torch.float32)
 
 
 def test_frontend_production_heads_equal_runs_match_oracle(gpu):
