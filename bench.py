@@ -479,7 +479,9 @@ def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None):
     total_ms, isolated_ms = time_steps(w.step, steps, warmup)
     call_ms = total_ms / steps  # one gdn_prefill_chunked call per step
     tflops = w.flops / (call_ms * 1e-3) / 1e12
+    extra = {} if lens is None else {"continuation": bench_continuation(dev, w, Hk, Hv)}
     return {
+        **extra,
         "tokens_per_s": w.T * steps / (total_ms * 1e-3),
         "ms_per_step": call_ms,
         "call_us": call_ms * 1e3,
@@ -488,6 +490,60 @@ def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None):
         "tflops": tflops,
         "mfma_frac": tflops / BF16_PEAK_TFLOPS,
     }
+
+
+def bench_continuation(dev, w, Hk, Hv, steps=128, warmup=8):
+    """The packed prefill's sequences decoding `steps` tokens each from its
+    final states: one fused decode launch (conv roll, gated RMSNorm) per
+    token for all of them, the states updated in place and two conv-state
+    buffers alternating."""
+
+    d = gdn.LinearAttentionDims(Hk, Hv, 128, 128, 4)
+    B, C = w.state_out.shape[0], d.conv_dim
+    g = torch.Generator(device=dev).manual_seed(1)
+    bf = torch.bfloat16
+    rnd = lambda *s_: torch.randn(*s_, generator=g, device=dev)
+    state = w.state_out.clone()
+    convs = [rnd(B, 3, C).to(bf), torch.empty(B, 3, C, dtype=bf, device=dev)]
+    n_in = 8
+    qkv = [rnd(B, C).to(bf) for _ in range(n_in)]
+    z = [rnd(B, Hv, 128).to(bf) for _ in range(n_in)]
+    a = [rnd(B, Hv).to(bf) for _ in range(n_in)]
+    b = [rnd(B, Hv).to(bf) for _ in range(n_in)]
+    conv_w = rnd(C, 4) * 0.2
+    norm_w = torch.rand(128, generator=g, device=dev) + 0.5
+
+    def step(s_):
+        i = s_ % n_in
+        gdn.fused_decode_step(qkv[i], z[i], a[i], b[i], convs[s_ % 2], state, conv_w, w.A_log,
+                              w.dt_bias, norm_w, 1e-6, d, conv_out=convs[(s_ + 1) % 2],
+                              state_out=state)
+
+    # eight steps a HIP graph (the conv buffers back at their start), replayed
+    # steps / 8 times: device time, not Python's launch rate
+    for s_ in range(warmup):
+        step(s_)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for s_ in range(8):
+            step(s_)
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps // 8):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (steps // 8 * 8)
+    _, _, nbytes = decode_bytes(B, Hk, Hv, 128, 4, True)
+    return {"workload": f"{steps} decode steps of the {B} sequences from the packed prefill's "
+                        f"states (fused decode in place, from HIP graphs; the "
+                        f"{B * Hv * 128 * 128 * 4 >> 20} MiB of state stay in the 256 MB Infinity "
+                        f"Cache)",
+            "tokens_per_s": B / (ms * 1e-3), "step_us": ms * 1e3,
+            "gbs": nbytes / (ms * 1e-3) / 1e9}
 
 
 def cpu_baseline_prefill(Hk, Hv, budget_s=10.0):
@@ -708,7 +764,8 @@ def main(argv=None):
                     "workload": "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 "
                                 "Hv=32, nonzero initial states",
                     "tokens_per_s": pv["tokens_per_s"], "call_us": pv["call_us"],
-                    "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"]}}
+                    "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"],
+                    "continuation": pv["continuation"]}}
         print(json.dumps(line))
         return 0
 
@@ -803,7 +860,8 @@ def main(argv=None):
                                        "kernel": "gdn_prefill_chunked (3 launches)",
                                        "call_us": r["call_us"]},
                           **({} if args.no_cpu_baseline or varlen else
-                             {"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)})}))
+                             {"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)}),
+                          **({"continuation": r["continuation"]} if varlen else {})}))
         return 0
 
     raise SystemExit(f"workload {args.workload} is not available in this build")
