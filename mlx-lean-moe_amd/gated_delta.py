@@ -56,6 +56,21 @@ def _c(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+def _check_out(out: torch.Tensor, shape, dtype: torch.dtype, device, src: torch.Tensor, name: str):
+    """A caller-provided output buffer: the shape and dtype the call would
+    allocate, contiguous, on the call's device, and not overlapping ``src``
+    (the kernels read their inputs while they write their outputs)."""
+
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or not out.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous {tuple(shape)} {dtype} tensor")
+    if out.device != device:
+        raise ValueError(f"{name} must be on {device}")
+    a0, a1 = out.data_ptr(), out.data_ptr() + out.numel() * out.element_size()
+    b0, b1 = src.data_ptr(), src.data_ptr() + src.numel() * src.element_size()
+    if a0 < b1 and b0 < a1:
+        raise ValueError(f"{name} must not overlap its input")
+
+
 def _stream(device: torch.device):
     return _lib.stream_ptr(device)
 
@@ -226,7 +241,8 @@ def _check_cu_seqlens(cu_seqlens, T: int) -> list[int]:
 
 
 def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=None,
-                       use_kernel: bool = True, y_dtype: torch.dtype | None = None):
+                       use_kernel: bool = True, y_dtype: torch.dtype | None = None,
+                       state_out: torch.Tensor | None = None):
     """Gated-delta update with the gates computed from ``a, b`` inside
     (beta = sigmoid(b), g = forget_gate(a, A_log, dt_bias)).
 
@@ -239,7 +255,9 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
     ``y`` comes in the promotion of the inputs' dtypes (float32 with a
     float32 state); ``y_dtype`` asks for it rounded to nearest even into that
     dtype instead, the values of ``y.to(y_dtype)`` without the float32 copy
-    (the layer's output cast, linear_attention.py:122-124)."""
+    (the layer's output cast, linear_attention.py:122-124). ``state_out``
+    receives the new state instead of a fresh tensor (its shape and dtype,
+    contiguous, not overlapping ``state``) and is returned."""
 
     packed = cu_seqlens is not None
     lead = 1 if packed else 2
@@ -284,7 +302,10 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
     rows_ok = a.stride() == b.stride() and a.stride(1) == 1 and a.stride(0) >= Hv
     state_in = _c(state.to(s_dtype))
     y = torch.empty((T, Hv, Dv), dtype=y_dtype, device=device)
-    state_out = torch.empty((N, Hv, Dv, Dk), dtype=s_dtype, device=device)
+    if state_out is None:
+        state_out = torch.empty((N, Hv, Dv, Dk), dtype=s_dtype, device=device)
+    else:
+        _check_out(state_out, (N, Hv, Dv, Dk), s_dtype, device, state_in, "state_out")
     if T > 0:
         if (use_kernel and s_dtype == torch.float32 and a.dtype == b.dtype == torch.bfloat16
                 and _prefill_eligible(q, k, v, mean_run)):

@@ -29,7 +29,7 @@ import torch
 
 from . import _lib
 from .config import LinearAttentionDims
-from .gated_delta import _c, _require_device, _stream, gated_delta_update
+from .gated_delta import _c, _check_out, _require_device, _stream, gated_delta_update
 from .quant import (LinearWeights, QuantScheme, concat_quantized, quantized_linear,
                     quantized_linear_split)
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
@@ -57,14 +57,16 @@ def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, ep
 
 
 def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torch.Tensor,
-                  dims: LinearAttentionDims, cu_seqlens: torch.Tensor | None = None):
+                  dims: LinearAttentionDims, cu_seqlens: torch.Tensor | None = None,
+                  conv_out: torch.Tensor | None = None):
     """Conv + SiLU + roll and q/k scaling for N packed runs
     (linear_attention.py:61-79,103-113).
 
     ``qkv (T, C)`` in the activation dtype; ``conv_state (N, K-1, C)`` (any
     float dtype); ``conv_weight (C, K)``; ``cu_seqlens`` device int32 offsets
     or None for N equal runs. Returns ``q, k (T, Hk, Dk)``, ``v (T, Hv, Dv)``
-    and the new conv state ``(N, K-1, C)`` in the activation dtype."""
+    and the new conv state ``(N, K-1, C)`` in the activation dtype (written
+    into ``conv_out`` if given: contiguous, not overlapping ``conv_state``)."""
 
     device = _require_device(qkv, conv_state, conv_weight)
     T, C = qkv.shape
@@ -80,7 +82,11 @@ def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torc
     q = torch.empty((T, dims.num_key_heads, dims.key_head_dim), dtype=act, device=device)
     k = torch.empty_like(q)
     v = torch.empty((T, dims.num_value_heads, dims.value_head_dim), dtype=act, device=device)
-    new_conv = torch.empty((N, K - 1, C), dtype=act, device=device)
+    if conv_out is None:
+        new_conv = torch.empty((N, K - 1, C), dtype=act, device=device)
+    else:
+        _check_out(conv_out, (N, K - 1, C), act, device, conv_state, "conv_out")
+        new_conv = conv_out
     _lib.call("gdn_frontend", _lib.ptr(qkv), _lib.ptr(conv_state), _lib.ptr(new_conv),
               _lib.dtype_code(conv_state.dtype), _lib.ptr(w), _lib.ptr(cu_seqlens), N, T,
               _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), dims.num_key_heads, dims.num_value_heads,
@@ -337,26 +343,31 @@ class Qwen3_5LinearAttention:
         b = self._proj(rows, self.in_proj_b)
         return qkv, z, a, b
 
-    def core(self, qkv, z, a, b, conv_state, ssm_state, cu_seqlens=None):
+    def core(self, qkv, z, a, b, conv_state, ssm_state, cu_seqlens=None, conv_out=None,
+             ssm_out=None):
         """Everything between the projections for N packed runs (one run if
         ``cu_seqlens`` is None): ``qkv (T, C)``, ``z (T, Hv, Dv)``,
         ``a, b (T, Hv)``, ``conv_state (N, K-1, C)``, ``ssm_state (N, Hv, Dv, Dk)``.
-        Returns ``(out (T, Hv*Dv), new_conv, new_ssm)``."""
+        Returns ``(out (T, Hv*Dv), new_conv, new_ssm)``, the new states in
+        ``conv_out`` and ``ssm_out`` when given."""
 
         d = self.linear
         T = qkv.shape[0]
         cu_dev = None
         if cu_seqlens is not None:
             cu_dev = torch.as_tensor(cu_seqlens, dtype=torch.int32).to(qkv.device)
-        q, k, v, new_conv = conv_frontend(qkv, conv_state, self.conv1d_weight, d, cu_dev)
+        q, k, v, new_conv = conv_frontend(qkv, conv_state, self.conv1d_weight, d, cu_dev,
+                                          conv_out=conv_out)
         # y straight in z's dtype: the norm's first step rounds it there
         if cu_seqlens is None:
             y, new_ssm = gated_delta_update(q[None], k[None], v[None], a[None], b[None],
-                                            self.A_log, self.dt_bias, ssm_state, y_dtype=z.dtype)
+                                            self.A_log, self.dt_bias, ssm_state, y_dtype=z.dtype,
+                                            state_out=ssm_out)
             y = y[0]
         else:
             y, new_ssm = gated_delta_update(q, k, v, a, b, self.A_log, self.dt_bias, ssm_state,
-                                            cu_seqlens=cu_seqlens, y_dtype=z.dtype)
+                                            cu_seqlens=cu_seqlens, y_dtype=z.dtype,
+                                            state_out=ssm_out)
         out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out_dtype=z.dtype)
         return out.reshape(T, d.value_dim), new_conv, new_ssm
 
@@ -379,20 +390,25 @@ class Qwen3_5LinearAttention:
         cache.update(new_conv, new_ssm, advance=rows.shape[0])
         return out[0] if squeeze else out
 
-    def _rows_step(self, rows, conv_state, ssm_state, residual=None):
+    def _rows_step(self, rows, conv_state, ssm_state, residual=None, conv_out=None, ssm_out=None):
         """The layer over ``rows (L, hidden)`` of one sequence from
         ``conv_state (K-1, C)`` and ``ssm_state (Hv, Dv, Dk)``: returns
-        ``(out (L, hidden), new_conv, new_ssm)`` in fresh tensors."""
+        ``(out (L, hidden), new_conv, new_ssm)``, the new states in fresh
+        tensors, or in ``conv_out`` and ``ssm_out`` when given."""
 
         d = self.linear
         qkv, z, a, b = self._project(rows)
         act = qkv.dtype
-        if rows.shape[0] == 1 and _fused_decode_ok(d, act):
+        outs = conv_out is not None or ssm_out is not None
+        if rows.shape[0] == 1 and _fused_decode_ok(d, act) and not outs:
             out, new_conv, new_ssm = self._decode_fused(qkv, z, a, b, conv_state[None].to(act),
                                                         ssm_state[None], in_place=False)
             out = out.reshape(1, d.value_dim)
         else:
-            out, new_conv, new_ssm = self.core(qkv, z, a, b, conv_state[None], ssm_state[None])
+            out, new_conv, new_ssm = self.core(
+                qkv, z, a, b, conv_state[None], ssm_state[None],
+                conv_out=None if conv_out is None else conv_out[None],
+                ssm_out=None if ssm_out is None else ssm_out[None])
         return self._proj(out, self.out_proj, residual), new_conv[0], new_ssm[0]
 
     def _decode_fused(self, qkv, z, a, b, conv_state, ssm_state, in_place: bool,
@@ -492,16 +508,18 @@ class PrefillGraph:
     longer than the kernels themselves.
 
     The graph reads ``self.x`` (and ``self.residual`` when captured with
-    ``residual_example``) and the sequence's state from ``self.conv_state``
-    and ``self.ssm_state``, writes ``self.out`` and leaves the new state in
-    the same two buffers. ``step(cache, x)`` copies ``x`` in, copies the
-    cache's state in unless the cache already holds these buffers, replays,
-    and points the cache at the buffers (``cache.update``): consecutive
-    chunks of one sequence run without copies, and the cache's state tensors
-    then change with every later step of this graph: clone them to keep a
-    snapshot, and before another sequence's step on the same graph. Shapes
-    and buffers are fixed at capture; a prompt's last, shorter chunk runs
-    through ``layer`` as usual."""
+    ``residual_example``) and writes ``self.out``. The sequence's state lives
+    in two buffer sets the chunks alternate between (the kernels read one
+    and write the other; two graphs over one memory pool). ``step(cache,
+    x)`` copies ``x`` in, copies the cache's state into the first set unless
+    the cache already holds one of the sets, replays, and points the cache
+    at the set just written (``cache.update``): consecutive chunks of one
+    sequence run without copies, and the cache's state tensors are then
+    overwritten two steps later on this graph: clone them to keep a
+    snapshot, and before another sequence's step on the same graph. The
+    returned output holds until the next step. Shapes and buffers are fixed
+    at capture; a prompt's last, shorter chunk runs through ``layer`` as
+    usual."""
 
     def __init__(self, layer: "Qwen3_5LinearAttention", x_example: torch.Tensor,
                  residual_example: torch.Tensor | None = None) -> None:
@@ -513,19 +531,24 @@ class PrefillGraph:
         self.chunk = x_example.shape[0]
         self.x = x_example.detach().clone()
         self.residual = None if residual_example is None else residual_example.detach().clone()
-        self.conv_state = torch.zeros((d.conv_kernel_dim - 1, d.conv_dim), dtype=self.x.dtype, device=dev)
-        self.ssm_state = torch.zeros((d.num_value_heads, d.value_head_dim, d.key_head_dim),
-                                     dtype=torch.float32, device=dev)
-        # one eager call first: lazily built operands (dequantized weights'
-        # workspace sizes, BLAS handles) exist before capture
-        layer._rows_step(self.x, self.conv_state, self.ssm_state, self.residual)
+        self._conv = [torch.zeros((d.conv_kernel_dim - 1, d.conv_dim), dtype=self.x.dtype, device=dev)
+                      for _ in range(2)]
+        self._ssm = [torch.zeros((d.num_value_heads, d.value_head_dim, d.key_head_dim),
+                                 dtype=torch.float32, device=dev) for _ in range(2)]
+        # one eager call first: lazily built operands (workspace sizes, BLAS
+        # handles) exist before capture
+        layer._rows_step(self.x, self._conv[0], self._ssm[0], self.residual)
         torch.cuda.synchronize(dev)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.out, new_conv, new_ssm = layer._rows_step(self.x, self.conv_state, self.ssm_state,
-                                                           self.residual)
-            self.conv_state.copy_(new_conv)
-            self.ssm_state.copy_(new_ssm)
+        self._graphs, self._outs = [], []
+        for i in (0, 1):
+            graph = torch.cuda.CUDAGraph()
+            pool = self._graphs[0].pool() if self._graphs else None
+            with torch.cuda.graph(graph, pool=pool):
+                out, _, _ = layer._rows_step(self.x, self._conv[i], self._ssm[i], self.residual,
+                                             conv_out=self._conv[1 - i], ssm_out=self._ssm[1 - i])
+            self._graphs.append(graph)
+            self._outs.append(out)
+        self.out = self._outs[0]
 
     def step(self, cache: RecurrentCache, x: torch.Tensor | None = None,
              residual: torch.Tensor | None = None) -> torch.Tensor:
@@ -539,10 +562,12 @@ class PrefillGraph:
             if residual is not self.residual:
                 self.residual.copy_(residual)
         conv, ssm = cache.state()
-        if conv is not self.conv_state:
-            self.conv_state.copy_(conv)
-        if ssm is not self.ssm_state:
-            self.ssm_state.copy_(ssm)
-        self.graph.replay()
-        cache.update(self.conv_state, self.ssm_state, advance=self.chunk)
+        held = [i for i in (0, 1) if conv is self._conv[i] and ssm is self._ssm[i]]
+        i = held[0] if held else 0
+        if not held:
+            self._conv[0].copy_(conv)
+            self._ssm[0].copy_(ssm)
+        self._graphs[i].replay()
+        cache.update(self._conv[1 - i], self._ssm[1 - i], advance=self.chunk)
+        self.out = self._outs[i]
         return self.out

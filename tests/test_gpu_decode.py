@@ -189,6 +189,20 @@ def test_frontend_production_heads_ragged_runs_match_oracle(gpu, Hk, Hv):
     _frontend_vs_oracle(gpu, dims, qkv, conv, w, cu, torch.float32)
 
 
+def test_frontend_writes_a_given_conv_out(gpu):
+    rng = np.random.default_rng(10)
+    C = DIMS_PROD.conv_dim
+    qkv = _t(R.bf16_round(rng.standard_normal((40, C))), gpu, torch.bfloat16)
+    conv = _t(rng.standard_normal((1, 3, C)), gpu, torch.bfloat16)
+    w = _t(rng.standard_normal((C, 4)) * 0.2, gpu)
+    q1, k1, v1, c1 = gdn.conv_frontend(qkv, conv, w, DIMS_PROD)
+    out = torch.empty_like(c1)
+    q2, k2, v2, c2 = gdn.conv_frontend(qkv, conv, w, DIMS_PROD, conv_out=out)
+    assert c2 is out and torch.equal(c2, c1) and torch.equal(q2, q1) and torch.equal(v2, v1)
+    with pytest.raises(ValueError, match="overlap"):
+        gdn.conv_frontend(qkv, conv, w, DIMS_PROD, conv_out=conv)
+
+
 def test_frontend_production_heads_equal_runs_match_oracle(gpu):
     """N equal runs without cu_seqlens (the batched layer), bf16 conv state."""
 

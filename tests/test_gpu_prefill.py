@@ -281,6 +281,22 @@ def test_update_y_dtype_is_the_rounded_float32_output(gpu, T):
         gdn.gated_delta_update(*args, y_dtype=torch.int32)
 
 
+@pytest.mark.parametrize("T", [96, 20])
+def test_update_writes_a_given_state_out(gpu, T):
+    arrays = _cfg_inputs(11, T, Hk=2, Hv=4, state_scale=0.05)
+    t = _dev(gpu, arrays)
+    args = (t["q"][None], t["k"][None], t["v"][None], t["a"][None], t["b"][None], t["A_log"],
+            t["dt_bias"], t["state"])
+    y1, s1 = gdn.gated_delta_update(*args)
+    out = torch.full_like(s1, float("nan"))
+    y2, s2 = gdn.gated_delta_update(*args, state_out=out)
+    assert s2 is out and torch.equal(s2, s1) and torch.equal(y2, y1)
+    with pytest.raises(ValueError, match="overlap"):
+        gdn.gated_delta_update(*args, state_out=t["state"])
+    with pytest.raises(ValueError, match="state_out"):
+        gdn.gated_delta_update(*args, state_out=out[..., :64])
+
+
 def test_prefill_bf16_output_and_zero_state_pointer(gpu):
     arrays = _cfg_inputs(5, 96, Hk=2, Hv=4)  # zero initial state
     t = _dev(gpu, arrays)
