@@ -304,6 +304,10 @@ def bench_layer_prefill(dev, T, steps, warmup, hidden=2048, chunk=512):
     chunk_eager_ms, _ = time_steps(lambda s_: layer(xc[s_ % 2], ce), steps, warmup)
     pg = gdn.PrefillGraph(layer, xc[0])
     chunk_graph_ms, _ = time_steps(lambda s_: pg.step(cg, xc[s_ % 2]), steps, warmup)
+    # the same with the projections' bf16 dequantization kept
+    layer.keep_dense_weights()
+    pgd, cd = gdn.PrefillGraph(layer, xc[0]), layer.new_cache()
+    chunk_dense_ms, _ = time_steps(lambda s_: pgd.step(cd, xc[s_ % 2]), steps, warmup)
     ms = total_ms / steps
     proj_flops = 2 * T * hidden * (d.conv_dim + d.value_dim + 2 * d.num_value_heads + d.value_dim)
     return {"workload": f"gated-delta layer prefill, T={T}, hidden {hidden}, 4-bit group-64 "
@@ -313,7 +317,8 @@ def bench_layer_prefill(dev, T, steps, warmup, hidden=2048, chunk=512):
             "out_proj_us": out_ms / steps * 1e3, "projection_flops": proj_flops,
             "chunk": chunk, "chunk_eager_us": chunk_eager_ms / steps * 1e3,
             "chunk_graph_us": chunk_graph_ms / steps * 1e3,
-            "chunk_graph_tokens_per_s": chunk / (chunk_graph_ms / steps * 1e-3)}
+            "chunk_graph_tokens_per_s": chunk / (chunk_graph_ms / steps * 1e-3),
+            "chunk_graph_dense_us": chunk_dense_ms / steps * 1e3}
 
 
 def bench_decode_slots(dev, B, Hk, Hv, steps, warmup):
@@ -795,6 +800,7 @@ def main(argv=None):
                                        "core": r["core_us"], "out_proj": r["out_proj_us"]},
                           "chunked": {"chunk": r["chunk"], "eager_step_us": r["chunk_eager_us"],
                                       "graph_step_us": r["chunk_graph_us"],
+                                      "graph_dense_weights_step_us": r["chunk_graph_dense_us"],
                                       "graph_tokens_per_s": r["chunk_graph_tokens_per_s"]}}))
         return 0
 

@@ -72,10 +72,24 @@ class QuantScheme:
 @dataclass(frozen=True)
 class LinearWeights:
     """A loaded linear projection with its own storage scheme; ``quant`` is
-    ``None`` for an ordinary floating-point matrix (moe_block.py:13-20)."""
+    ``None`` for an ordinary floating-point matrix (moe_block.py:13-20).
+
+    ``dense``, for quantized weights, optionally holds their bf16
+    dequantization (``dequantize(tensors, quant, bfloat16)``, see
+    :meth:`with_dense`): the prefill-sized products, which multiply on
+    exactly those values, then skip converting the weights on every call, at
+    the cost of keeping the copy (2 bytes per weight)."""
 
     tensors: object
     quant: QuantScheme | None
+    dense: torch.Tensor | None = None
+
+    def with_dense(self) -> "LinearWeights":
+        """These weights with their bf16 dequantization kept alongside."""
+
+        if self.quant is None:
+            return self
+        return LinearWeights(self.tensors, self.quant, dequantize(self.tensors, self.quant, torch.bfloat16))
 
 
 def _kernel_scheme(quant: QuantScheme) -> None:
@@ -153,8 +167,9 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None,
     (transformer.py:110-112) adds two arrays of it; on the quantized
     kernels the add is part of the store."""
 
+    dense = None
     if isinstance(tensors, LinearWeights):
-        quant = tensors.quant
+        quant, dense = tensors.quant, tensors.dense
         tensors = tensors.tensors
 
     def with_residual(out: torch.Tensor) -> torch.Tensor:
@@ -182,7 +197,8 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None,
     if _dense_rows(x2.shape[0], N, K):
         # the same bf16-rounded weights as the tiled kernel (gdn_dequantize),
         # one transient copy, and the vendor BLAS for the GEMM itself
-        return with_residual((x2 @ dequantize(tensors, quant, torch.bfloat16).T).reshape(*lead, N))
+        wd = dense if dense is not None else dequantize(tensors, quant, torch.bfloat16)
+        return with_residual((x2 @ wd.T).reshape(*lead, N))
     if x2.data_ptr() % 16:
         x2 = x2.clone()
     M = x2.shape[0]
@@ -231,7 +247,7 @@ def quantized_linear_split(x: torch.Tensor, weights: LinearWeights, sizes) -> li
         _check_quantized(tensors, quant, K)
         lead = x.shape[:-1]
         x2 = _c(x.reshape(-1, K))
-        wd = dequantize(tensors, quant, torch.bfloat16)
+        wd = weights.dense if weights.dense is not None else dequantize(tensors, quant, torch.bfloat16)
         return [(x2 @ blk.T).reshape(*lead, blk.shape[0]) for blk in torch.split(wd, sizes)]
     return list(torch.split(quantized_linear(x, weights), sizes, dim=-1))
 

@@ -99,3 +99,24 @@ def _detached(cache):
     out = gdn.RecurrentCache.__new__(gdn.RecurrentCache)
     out.conv_state, out.ssm_state, out.size = cache.conv_state.clone(), cache.ssm_state.clone(), cache.size
     return out
+
+
+def test_kept_dense_weights_change_no_result(gpu):
+    """keep_dense_weights: the prompt-sized products use the kept bf16
+    copies instead of dequantizing per call; eager calls (dense and
+    quantized-kernel sizes) and graph chunks are bit-identical."""
+
+    plain, dense = _quantized_layer(21, gpu), _quantized_layer(21, gpu)
+    dense.keep_dense_weights()
+    assert dense._in_stacked.dense is not None and dense.out_proj.dense is not None
+    rng = np.random.default_rng(22)
+    c1, c2 = plain.new_cache(), dense.new_cache()
+    for n in (600, 70, 1):
+        x = _x(rng, n, gpu)
+        assert torch.equal(plain(x if n > 1 else x[0], c1), dense(x if n > 1 else x[0], c2))
+    assert torch.equal(c1.ssm_state, c2.ssm_state)
+    step = gdn.PrefillGraph(dense, _x(rng, 512, gpu))
+    for _ in range(2):
+        x = _x(rng, 512, gpu)
+        assert torch.equal(step.step(c2, x), plain(x, c1))
+        torch.cuda.synchronize()
