@@ -49,7 +49,7 @@ typedef enum {
  * slots, 4 its conv rows, 5 replaces the conv rows with the pool's half bits,
  * adds input row strides and gdn_pool_advance, 6 the quantized matmul's
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
- * residual, 8 the prefill's gate row stride). */
+ * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -71,7 +71,9 @@ int gdn_gates(const void *a, const void *b, int ab_dtype, const float *A_log,
 /*
  * gdn_frontend - causal depthwise conv (K taps) + SiLU + conv-state roll and
  * q/k scaling for a batch of token runs.
- *   qkv:            (T_total, C) act_dtype, C = 2*Hk*Dk + Hv*Dv, channel order [q; k; v]
+ *   qkv:            (T_total, C) act_dtype, C = 2*Hk*Dk + Hv*Dv, channel order [q; k; v],
+ *                   rows qkv_stride elements apart (>= C; C when packed: qkv may be
+ *                   the first columns of a stacked projection output)
  *   conv_state_in:  (N, K-1, C) conv_dtype
  *   conv_state_out: (N, K-1, C) act_dtype (the reference keeps the rolled state in
  *                   the activation dtype); must not overlap conv_state_in
@@ -83,7 +85,7 @@ int gdn_gates(const void *a, const void *b, int ab_dtype, const float *A_log,
  * Replaces Qwen3_5LinearAttention._convolve and the split/scale
  * (linear_attention.py:61-79,103-113).
  */
-int gdn_frontend(const void *qkv, const void *conv_state_in, void *conv_state_out,
+int gdn_frontend(const void *qkv, int64_t qkv_stride, const void *conv_state_in, void *conv_state_out,
                  int conv_dtype, const float *conv_weight, const int32_t *cu_seqlens, int N,
                  int64_t T_total, void *q_out, void *k_out, void *v_out, int Hk, int Hv, int Dk,
                  int Dv, int K, int act_dtype, void *stream);

@@ -16,7 +16,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgdn.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 GDN_F32, GDN_BF16, GDN_F16 = 0, 1, 2
 GDN_EINVAL, GDN_EUNSUPPORTED = -1, -2
@@ -35,7 +35,7 @@ _SIGNATURES = {
     "gdn_last_error": (ctypes.c_char_p, []),
     "gdn_gates": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p,
                            _c_void_p, _c_int, _c_i64, _c_int, _c_void_p]),
-    "gdn_frontend": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
+    "gdn_frontend": (_c_int, [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
                               _c_int, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
                               _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "gdn_scan_reference": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p,

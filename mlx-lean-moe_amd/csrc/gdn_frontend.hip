@@ -20,7 +20,7 @@ constexpr int kFrontThreads = 256;
 
 // Row j of a run's new conv state is row len + j of concat(state, tokens).
 template <class Act>
-GDN_DEV void write_conv_state(const typename Act::storage* __restrict__ qkv,
+GDN_DEV void write_conv_state(const typename Act::storage* __restrict__ qkv, int64_t qs,
                               const void* __restrict__ cs_in, int conv_dtype,
                               typename Act::storage* __restrict__ cs_out,
                               const int32_t* __restrict__ cu, int run, int64_t L_uniform, int C,
@@ -32,7 +32,7 @@ GDN_DEV void write_conv_state(const typename Act::storage* __restrict__ qkv,
             const int64_t idx = len + j;
             const float x = idx < S
                 ? Act::round(load_any(cs_in, (int64_t(run) * S + idx) * C + c, conv_dtype))
-                : Act::load(qkv, (start + idx - S) * C + c);
+                : Act::load(qkv, (start + idx - S) * qs + c);
             Act::store(cs_out, (int64_t(run) * S + j) * C + c, x);
         }
     }
@@ -40,7 +40,7 @@ GDN_DEV void write_conv_state(const typename Act::storage* __restrict__ qkv,
 
 template <class Act>
 __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
-    const typename Act::storage* __restrict__ qkv, const void* __restrict__ cs_in,
+    const typename Act::storage* __restrict__ qkv, int64_t qs, const void* __restrict__ cs_in,
     int conv_dtype, typename Act::storage* __restrict__ cs_out, const float* __restrict__ w,
     const int32_t* __restrict__ cu, int N, int64_t T, int64_t L_uniform,
     typename Act::storage* __restrict__ qo, typename Act::storage* __restrict__ ko,
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
 
     if (blk >= T) {
         const int run = int(blk - T);
-        if (run < N) write_conv_state<Act>(qkv, cs_in, conv_dtype, cs_out, cu, run, L_uniform, C, S);
+        if (run < N) write_conv_state<Act>(qkv, qs, cs_in, conv_dtype, cs_out, cu, run, L_uniform, C, S);
         return;
     }
 
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
             const int64_t idx = pos + j;  // index into concat(state, run tokens)
             const float x = idx < S
                 ? Act::round(load_any(cs_in, (int64_t(run) * S + idx) * C + c, conv_dtype))
-                : Act::load(qkv, (start + idx - S) * C + c);
+                : Act::load(qkv, (start + idx - S) * qs + c);
             acc += Act::round(w[int64_t(c) * K + j]) * x;
         }
         acc = Act::round(acc);
@@ -144,7 +144,7 @@ GDN_DEV void load_state8(const void* __restrict__ p, int64_t at, float* x) {
 // and each token shifts itself in.
 template <int kConvDt>
 __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
-    const uint16_t* __restrict__ qkv, const void* __restrict__ cs_in,
+    const uint16_t* __restrict__ qkv, int64_t qs, const void* __restrict__ cs_in,
     uint16_t* __restrict__ cs_out, const float* __restrict__ w, const int32_t* __restrict__ cu,
     int N, int64_t T, int64_t L_uniform, int n_state, uint16_t* __restrict__ qo,
     uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, int Hk, int Hv) {
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
                 const int64_t start = cu ? cu[run] : run * L_uniform;
                 const int64_t idx = (cu ? cu[run + 1] - cu[run] : L_uniform) + j;  // in concat(state, run)
                 x[i] = idx < S ? round_bf16(load_any(cs_in, (int64_t(run) * S + idx) * C + c, kConvDt))
-                               : ActBF16::load(qkv, (start + idx - S) * C + c);
+                               : ActBF16::load(qkv, (start + idx - S) * qs + c);
             }
         }
 #pragma unroll
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
     constexpr int kAhead = 8;
     const auto row_at = [&](int i) {
         const int64_t t = t0 + i < T ? t0 + i : T - 1;
-        return *reinterpret_cast<const uint4*>(qkv + t * C + c0);
+        return *reinterpret_cast<const uint4*>(qkv + t * qs + c0);
     };
     uint4 raw[kAhead];
 #pragma unroll
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
     for (int j = 0; j < S; ++j) {
         const int64_t row = t0 - S + j;
         if (row >= start) {
-            unpack8(*reinterpret_cast<const uint4*>(qkv + row * C + c0), win[j]);
+            unpack8(*reinterpret_cast<const uint4*>(qkv + row * qs + c0), win[j]);
         } else {  // concat index row - start + S of the run's conv state
             load_state8<kConvDt>(cs_in, (int64_t(run) * S + (row - start + S)) * C + c0, win[j]);
         }
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
 
 using namespace gdn;
 
-extern "C" int gdn_frontend(const void* qkv, const void* conv_state_in, void* conv_state_out,
+extern "C" int gdn_frontend(const void* qkv, int64_t qkv_stride, const void* conv_state_in, void* conv_state_out,
                             int conv_dtype, const float* conv_weight, const int32_t* cu_seqlens,
                             int N, int64_t T_total, void* q_out, void* k_out, void* v_out, int Hk,
                             int Hv, int Dk, int Dv, int K, int act_dtype, void* stream) {
@@ -297,6 +297,8 @@ extern "C" int gdn_frontend(const void* qkv, const void* conv_state_in, void* co
                 (long long)T_total, N);
     const int64_t C = 2LL * Hk * Dk + int64_t(Hv) * Dv;
     GDN_REQUIRE(C * 4 <= 64 * 1024, "gdn_frontend: conv_dim %lld exceeds the LDS tile", (long long)C);
+    GDN_REQUIRE(qkv_stride >= C, "gdn_frontend: qkv_stride %lld below conv_dim %lld",
+                (long long)qkv_stride, (long long)C);
     const int64_t S = K - 1;
     if (S > 0) {
         GDN_REQUIRE(conv_state_in && conv_state_out, "gdn_frontend: null conv state");
@@ -310,6 +312,7 @@ extern "C" int gdn_frontend(const void* qkv, const void* conv_state_in, void* co
     const int64_t L_uniform = cu_seqlens ? 0 : T_total / N;
     const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (act_dtype == GDN_BF16 && Dk == 128 && Dv == 128 && K == 4 && T_total > 0 && aligned(qkv) &&
+        qkv_stride % 8 == 0 &&
         aligned(conv_state_in) && aligned(conv_weight) && aligned(q_out) && aligned(k_out) &&
         aligned(v_out)) {
         const int G = 2 * Hk + Hv;
@@ -320,13 +323,13 @@ extern "C" int gdn_frontend(const void* qkv, const void* conv_state_in, void* co
         const int64_t gx = n_state + n_tiles;
         GDN_REQUIRE(gx < (1LL << 31) / (kTileWaves * kWave) && gy < 65536,
                     "gdn_frontend: %lld tokens exceed the grid", (long long)T_total);
-        using Kernel = void (*)(const uint16_t*, const void*, uint16_t*, const float*, const int32_t*,
+        using Kernel = void (*)(const uint16_t*, int64_t, const void*, uint16_t*, const float*, const int32_t*,
                                 int, int64_t, int64_t, int, uint16_t*, uint16_t*, uint16_t*, int, int);
         const Kernel kern = conv_dtype == GDN_F32    ? frontend_tiled_kernel<GDN_F32>
                             : conv_dtype == GDN_BF16 ? frontend_tiled_kernel<GDN_BF16>
                                                      : frontend_tiled_kernel<GDN_F16>;
         hipLaunchKernelGGL(kern, dim3(unsigned(gx), unsigned(gy)), dim3(kTileWaves * kWave), 0,
-                           as_stream(stream), static_cast<const uint16_t*>(qkv), conv_state_in,
+                           as_stream(stream), static_cast<const uint16_t*>(qkv), qkv_stride, conv_state_in,
                            static_cast<uint16_t*>(conv_state_out), conv_weight, cu_seqlens, N,
                            T_total, L_uniform, int(n_state), static_cast<uint16_t*>(q_out),
                            static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out), Hk, Hv);
@@ -337,14 +340,14 @@ extern "C" int gdn_frontend(const void* qkv, const void* conv_state_in, void* co
     const size_t lds = size_t(C) * sizeof(float);
     if (act_dtype == GDN_F32) {
         hipLaunchKernelGGL(frontend_kernel<ActF32>, dim3(unsigned(blocks)), dim3(kFrontThreads),
-                           lds, as_stream(stream), static_cast<const float*>(qkv), conv_state_in,
+                           lds, as_stream(stream), static_cast<const float*>(qkv), qkv_stride, conv_state_in,
                            conv_dtype, static_cast<float*>(conv_state_out), conv_weight,
                            cu_seqlens, N, T_total, L_uniform, static_cast<float*>(q_out),
                            static_cast<float*>(k_out), static_cast<float*>(v_out), Hk, Hv, Dk,
                            Dv, K);
     } else {
         hipLaunchKernelGGL(frontend_kernel<ActBF16>, dim3(unsigned(blocks)), dim3(kFrontThreads),
-                           lds, as_stream(stream), static_cast<const uint16_t*>(qkv),
+                           lds, as_stream(stream), static_cast<const uint16_t*>(qkv), qkv_stride,
                            conv_state_in, conv_dtype, static_cast<uint16_t*>(conv_state_out),
                            conv_weight, cu_seqlens, N, T_total, L_uniform,
                            static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out),

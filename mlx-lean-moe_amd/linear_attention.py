@@ -77,7 +77,11 @@ def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torc
     act = qkv.dtype
     if act not in (torch.float32, torch.bfloat16):
         raise ValueError(f"activations must be float32 or bfloat16, got {act}")
-    qkv, conv_state = _c(qkv), _c(conv_state)
+    # qkv may be the first columns of a stacked projection output: read in
+    # place with its row stride
+    if not (qkv.stride(1) == 1 and qkv.stride(0) >= C):
+        qkv = qkv.contiguous()
+    conv_state = _c(conv_state)
     w = _c(conv_weight.float().reshape(C, K))
     q = torch.empty((T, dims.num_key_heads, dims.key_head_dim), dtype=act, device=device)
     k = torch.empty_like(q)
@@ -87,7 +91,7 @@ def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torc
     else:
         _check_out(conv_out, (N, K - 1, C), act, device, conv_state, "conv_out")
         new_conv = conv_out
-    _lib.call("gdn_frontend", _lib.ptr(qkv), _lib.ptr(conv_state), _lib.ptr(new_conv),
+    _lib.call("gdn_frontend", _lib.ptr(qkv), qkv.stride(0), _lib.ptr(conv_state), _lib.ptr(new_conv),
               _lib.dtype_code(conv_state.dtype), _lib.ptr(w), _lib.ptr(cu_seqlens), N, T,
               _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), dims.num_key_heads, dims.num_value_heads,
               dims.key_head_dim, dims.value_head_dim, K, _lib.dtype_code(act), _stream(device))

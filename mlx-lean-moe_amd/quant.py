@@ -35,6 +35,11 @@ _KERNEL_BITS = {4, 8}
 # 73 vs 103 us at 1024 rows, 242 vs 336 us at 4096; even at 512 rows);
 # below it gdn_quantized_matmul's kernels run directly, see _dense_rows.
 _BLAS_ROWS = 512
+# quantized_linear_split multiplies per block from this many rows on (one
+# product of the stacked 2048 -> 12352 weight: 32.7 us at 512 rows against
+# 45.9 us per block, 53.9 against 62.1 at 1024, even at 2048, 246 against
+# 159 at 4096)
+_SPLIT_ROWS = 2048
 
 
 def _dense_rows(rows: int, N: int, K: int) -> bool:
@@ -228,11 +233,13 @@ def quantized_linear_split(x: torch.Tensor, weights: LinearWeights, sizes) -> li
     projection would give, in one launch where that pays.
 
     Where the dense path runs (bf16 ``x``, :func:`_dense_rows`: prefill
-    sizes) ``W`` is dequantized once and each block is its own GEMM on the
-    vendor BLAS with a packed output: for hidden 2048 -> 8192|4096|64 at 4096 rows the blocks
-    take 159 us together against 246 us for one 12352-column product (the
-    library tiles that N poorly). Below it one quantized launch computes all
-    columns and the blocks are column views of its output."""
+    sizes) ``W`` is dequantized once (or its kept copy used); from
+    ``_SPLIT_ROWS`` rows on each block is its own GEMM on the vendor BLAS
+    with a packed output: for hidden 2048 -> 8192|4096|64 at 4096 rows the
+    blocks take 159 us together against 246 us for one 12352-column product
+    (the library tiles that N poorly at that size), while below 2048 rows the
+    one product is faster and the blocks are column views of it, as they are
+    of the one quantized launch at decode sizes."""
 
     tensors, quant = weights.tensors, weights.quant
     sizes = [int(n) for n in sizes]
@@ -248,6 +255,9 @@ def quantized_linear_split(x: torch.Tensor, weights: LinearWeights, sizes) -> li
         lead = x.shape[:-1]
         x2 = _c(x.reshape(-1, K))
         wd = weights.dense if weights.dense is not None else dequantize(tensors, quant, torch.bfloat16)
+        if rows < _SPLIT_ROWS:
+            # one product; the blocks are column views of it
+            return list(torch.split((x2 @ wd.T).reshape(*lead, -1), sizes, dim=-1))
         return [(x2 @ blk.T).reshape(*lead, blk.shape[0]) for blk in torch.split(wd, sizes)]
     return list(torch.split(quantized_linear(x, weights), sizes, dim=-1))
 

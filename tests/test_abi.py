@@ -73,8 +73,12 @@ def test_invalid_arguments_return_einval_without_launching():
     assert rc == _lib.GDN_EINVAL and "gate_stride" in _err(lib), _err(lib)
     # overlapping conv state buffers are rejected
     p = ctypes.c_void_p(4096)
-    rc = lib.gdn_frontend(p, p, p, 1, p, None, 1, 1, p, p, p, 1, 2, 32, 32, 4, 1, None)
+    rc = lib.gdn_frontend(p, 128, p, p, 1, p, None, 1, 1, p, p, p, 1, 2, 32, 32, 4, 1, None)
     assert rc == _lib.GDN_EINVAL and "overlaps" in _err(lib)
+    # a qkv row stride below conv_dim
+    rc = lib.gdn_frontend(p, 127, p, ctypes.c_void_p(1 << 30), 1, p, None, 1, 1, p, p, p, 1, 2, 32, 32,
+                          4, 1, None)
+    assert rc == _lib.GDN_EINVAL and "qkv_stride" in _err(lib)
 
 
 def test_empty_work_is_a_no_op():

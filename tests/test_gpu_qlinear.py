@@ -208,11 +208,12 @@ def test_non_bf16_activations_use_dense_weights(gpu):
     assert np.abs(y.cpu().numpy() - ref).max() < 1e-4
 
 
-@pytest.mark.parametrize("M", [64, 600])
+@pytest.mark.parametrize("M", [64, 600, 2100])
 def test_stacked_projection_blocks_match_the_oracle(gpu, M):
     """quantized_linear_split: one quantized launch split into column views
-    below 512 rows, one dequantization and a GEMM per block (packed) from
-    512 rows on; either way each block is x @ W_block.T."""
+    below 512 rows, one dequantized product split into views below 2048,
+    a GEMM per block (packed) from 2048 rows on; either way each block is
+    x @ W_block.T."""
 
     from mlx_lean_moe_amd.quant import concat_quantized, quantized_linear_split
 
@@ -227,7 +228,7 @@ def test_stacked_projection_blocks_match_the_oracle(gpu, M):
     exact = _decode_kernel_takes(M, K, 4, 64, "bf16")
     for blk, (words, s, b), n in zip(blocks, parts, sizes):
         assert tuple(blk.shape) == (M, n) and blk.dtype == torch.bfloat16
-        assert blk.is_contiguous() == (M >= 512)
+        assert blk.is_contiguous() == (M >= 2048)
         ref = Q.quantized_matmul(x, words, s, b, 4, 64, w_round="f32" if exact else "bf16")
         assert_bf16_out_close(blk.float().cpu().numpy(), ref)
 
