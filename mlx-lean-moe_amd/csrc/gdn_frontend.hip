@@ -4,13 +4,15 @@
 // Two kernels. The tiled one covers the production shape (Dk = Dv = 128,
 // K = 4, bf16 activations, 16-byte aligned operands): a wave holds four
 // 128-channel groups (q, k or v heads) of one token, 8 channels a lane, and
-// walks a tile of tokens with the previous three input rows in registers, so
+// walks a tile of 4-16 tokens with the previous three input rows in registers, so
 // each qkv row is read once per tile plus a three-row halo, with 16-byte
 // loads and stores; the q/k RMS norm is a 16-lane DPP sum. The general
 // one (any head size and K) gives each token a block: every channel's K-tap
 // conv goes to LDS, then one wave per q/k head normalises. In both, extra
 // blocks each write one run's new conv state (the last K-1 rows of
 // concat(state, tokens)), so conv_state_out must not overlap conv_state_in.
+#include <type_traits>
+
 #include "gdn_common.h"
 #include "gdn_host.h"
 
@@ -94,7 +96,7 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
 }
 
 
-constexpr int kTileTokens = 16;  // tokens a wave walks
+constexpr int kMaxTileTokens = 16;  // tokens a wave walks, at most
 constexpr int kTileWaves = 4;    // waves a block, four channel groups each
 
 constexpr int kStateChunk = kTileWaves * kWave * 8;  // conv-state elements a block writes
@@ -132,17 +134,18 @@ GDN_DEV void load_state8(const void* __restrict__ p, int64_t at, float* x) {
     }
 }
 
+// Tiles of kTileTokens = TT tokens (16, or 8 or 4 for short inputs).
 // grid (n_state + n_tiles, ceil(G / 16)) for G = 2 Hk + Hv channel groups of
 // 128. The first n_state columns write the runs' new conv states, flattened
 // to N (K-1) C elements, kStateChunk a block (8 independent elements a
 // thread; dispatched first, they overlap the tiles); block (n_state + x, y)
-// covers tokens [16 x, 16 x + 16) of groups [16 y, 16 y + 16).
+// covers tokens [TT x, TT x + TT) of groups [16 y, 16 y + 16).
 //
 // The three-row window holds rows t-3 .. t-1 of concat(run's conv state,
 // run's tokens) for the token t in hand: it is loaded so at the tile's first
 // token and reloaded from the conv state where a run starts inside the tile,
 // and each token shifts itself in.
-template <int kConvDt>
+template <int kConvDt, int kTileTokens>
 __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
     const uint16_t* __restrict__ qkv, int64_t qs, const void* __restrict__ cs_in,
     uint16_t* __restrict__ cs_out, const float* __restrict__ w, const int32_t* __restrict__ cu,
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
 
     // the tile's rows, kAhead in flight (the last tile's missing ones repeat
     // row T-1, unused)
-    constexpr int kAhead = 8;
+    constexpr int kAhead = kTileTokens < 8 ? kTileTokens : 8;
     const auto row_at = [&](int i) {
         const int64_t t = t0 + i < T ? t0 + i : T - 1;
         return *reinterpret_cast<const uint4*>(qkv + t * qs + c0);
@@ -317,7 +320,11 @@ extern "C" int gdn_frontend(const void* qkv, int64_t qkv_stride, const void* con
         aligned(v_out)) {
         const int G = 2 * Hk + Hv;
         const int gy = (G + 4 * kTileWaves - 1) / (4 * kTileWaves);
-        const int64_t n_tiles = (T_total + kTileTokens - 1) / kTileTokens;
+        // tiles of 16 tokens, or of 8 or 4 where that leaves under 1024
+        // workgroups (a wave walks its tile's tokens one after another)
+        int tile = kMaxTileTokens;
+        while (tile > 4 && (T_total + tile - 1) / tile * gy < 1024) tile /= 2;
+        const int64_t n_tiles = (T_total + tile - 1) / tile;
         const int64_t chunks = (int64_t(N) * S * C + kStateChunk - 1) / kStateChunk;
         const int64_t n_state = (chunks + gy - 1) / gy;
         const int64_t gx = n_state + n_tiles;
@@ -325,9 +332,15 @@ extern "C" int gdn_frontend(const void* qkv, int64_t qkv_stride, const void* con
                     "gdn_frontend: %lld tokens exceed the grid", (long long)T_total);
         using Kernel = void (*)(const uint16_t*, int64_t, const void*, uint16_t*, const float*, const int32_t*,
                                 int, int64_t, int64_t, int, uint16_t*, uint16_t*, uint16_t*, int, int);
-        const Kernel kern = conv_dtype == GDN_F32    ? frontend_tiled_kernel<GDN_F32>
-                            : conv_dtype == GDN_BF16 ? frontend_tiled_kernel<GDN_BF16>
-                                                     : frontend_tiled_kernel<GDN_F16>;
+        const auto pick = [&](auto tt) -> Kernel {
+            constexpr int TT = decltype(tt)::value;
+            return conv_dtype == GDN_F32    ? frontend_tiled_kernel<GDN_F32, TT>
+                   : conv_dtype == GDN_BF16 ? frontend_tiled_kernel<GDN_BF16, TT>
+                                            : frontend_tiled_kernel<GDN_F16, TT>;
+        };
+        const Kernel kern = tile == 16 ? pick(std::integral_constant<int, 16>{})
+                            : tile == 8 ? pick(std::integral_constant<int, 8>{})
+                                        : pick(std::integral_constant<int, 4>{});
         hipLaunchKernelGGL(kern, dim3(unsigned(gx), unsigned(gy)), dim3(kTileWaves * kWave), 0,
                            as_stream(stream), static_cast<const uint16_t*>(qkv), qkv_stride, conv_state_in,
                            static_cast<uint16_t*>(conv_state_out), conv_weight, cu_seqlens, N,

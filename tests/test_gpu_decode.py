@@ -203,11 +203,12 @@ def test_frontend_writes_a_given_conv_out(gpu):
         gdn.conv_frontend(qkv, conv, w, DIMS_PROD, conv_out=conv)
 
 
-def test_frontend_production_heads_equal_runs_match_oracle(gpu):
-    """N equal runs without cu_seqlens (the batched layer), bf16 conv state."""
+@pytest.mark.parametrize("N,L", [(3, 45), (1, 2100), (2, 2050)])
+def test_frontend_production_heads_equal_runs_match_oracle(gpu, N, L):
+    """N equal runs without cu_seqlens (the batched layer), bf16 conv state;
+    the token counts take the 4-, 8- and 16-token tiles (partial last tile)."""
 
-    rng = np.random.default_rng(9)
-    N, L = 3, 45
+    rng = np.random.default_rng(9 + L)
     cu = (np.arange(N + 1) * L).astype(np.int32)
     C = DIMS_PROD.conv_dim
     qkv = R.bf16_round(rng.standard_normal((N * L, C)))
