@@ -130,3 +130,17 @@ def test_decode_batch_matches_per_sequence_layer_calls(gpu):
     for i in range(B):
         torch.testing.assert_close(pool.ssm_state[i], caches[i].ssm_state, rtol=0, atol=0)
         torch.testing.assert_close(pool.conv_state[i], caches[i].conv_state, rtol=0, atol=0)
+
+
+def test_launch_stream_is_the_current_stream(gpu):
+    """Kernels go to torch's current stream of the tensors' device, also
+    inside a stream context."""
+
+    from mlx_lean_moe_amd import _lib
+
+    side = torch.cuda.Stream(gpu)
+    assert _lib.stream_ptr(gpu) == torch.cuda.current_stream(gpu).cuda_stream
+    assert _lib.stream_ptr(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
+    with torch.cuda.stream(side):
+        assert _lib.stream_ptr(gpu) == side.cuda_stream
+    assert _lib.stream_ptr(gpu) != side.cuda_stream
