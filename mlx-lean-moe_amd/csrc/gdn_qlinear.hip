@@ -776,15 +776,6 @@ __global__ __launch_bounds__(256) void qlinear_gemv_kernel(
     int n0 = kC * wave;
     if (n0 < N) fetch(n0);
 
-    // x staged in LDS once per workgroup: every wave reads all of it, and
-    // thousands of waves reading the same bytes from L2 cost ~1.5 us at
-    // N=12352, K=2048 (x is at most 16 KB: one row, K <= 4096)
-    __shared__ __attribute__((aligned(16))) u32x4 x_lds[kM * 4096 * 4 / 16];
-    const int x_vecs = M * K * esx / 16;
-    for (int i = int(threadIdx.x); i < x_vecs; i += int(blockDim.x))
-        x_lds[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * i, 0, 0);
-    __syncthreads();
-
     // x of the chunks and their sums; rows >= M and inactive chunks hold 0
     uint32_t xq[kM][kR][kXRegs];
     float xs[kM][kR];
@@ -799,7 +790,7 @@ __global__ __launch_bounds__(256) void qlinear_gemv_kernel(
                 const int off = (m * K + kCodes * (64 * r + lane)) * esx;
 #pragma unroll
                 for (int c = 0; c < kCodes * esx / 16; ++c) {
-                    const u32x4 d = x_lds[off / 16 + c];
+                    const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * c, 0, 0);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         if constexpr (kXF32) {
