@@ -49,7 +49,8 @@ typedef enum {
  * slots, 4 its conv rows, 5 replaces the conv rows with the pool's half bits,
  * adds input row strides and gdn_pool_advance, 6 the quantized matmul's
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
- * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride). */
+ * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride,
+ * 10 the gated norm's z layout). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -209,12 +210,17 @@ int gdn_prefill_chunked(const void *q, const void *k, const void *v, const void 
  * gdn_gated_rmsnorm - out = silu(z) * rms_norm(x, w, eps) with x first rounded
  * to out_dtype and the normalised value held in out_dtype; the product is
  * taken in float32 and stored in out_dtype.
- *   x: (rows, D) x_dtype; z: (rows, D) z_dtype; w: (D) float32; out: (rows, D) out_dtype
+ *   x: (rows, D) x_dtype; w: (D) float32; out: (rows, D) out_dtype
+ *   z: rows of D z_dtype elements, row r at element (r / heads) * z_stride +
+ *      (r % heads) * D (heads = 1, z_stride = D when packed; the layer's
+ *      (T, Hv, D) column view of a stacked projection output: heads = Hv and
+ *      z_stride its token stride); rows % heads == 0, z_stride >= heads * D
  * Replaces _gated_rms_norm (linear_attention.py:22-32); with out_dtype = z's
  * dtype it includes its call site's y.astype(z.dtype) (linear_attention.py:122-124).
  */
-int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, const float *w,
-                      float eps, void *out, int out_dtype, int64_t rows, int D, void *stream);
+int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, int64_t z_stride,
+                      int heads, const float *w, float eps, void *out, int out_dtype, int64_t rows,
+                      int D, void *stream);
 
 /*
  * gdn_quantized_matmul - y = x W^T for an affine-quantized W in MLX's packing,

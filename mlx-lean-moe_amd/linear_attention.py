@@ -45,13 +45,21 @@ def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, ep
         raise ValueError("gate must match x and weight its last axis")
     device = _require_device(x, gate, weight)
     out_dtype = x.dtype if out_dtype is None else out_dtype
-    x, gate = _c(x), _c(gate)
+    x = _c(x)
     w = _c(weight.float())
     D = x.shape[-1]
     rows = x.numel() // D if D else 0
+    # the gate may be a (T, H, D) column view of a stacked projection output,
+    # read in place: row r at (r / H) * stride(0) + (r % H) * D
+    if (gate.dim() == 3 and gate.stride(2) == 1 and gate.stride(1) == D
+            and gate.stride(0) >= gate.shape[1] * D and not gate.is_contiguous()):
+        heads, z_stride = gate.shape[1], gate.stride(0)
+    else:
+        gate = _c(gate)
+        heads, z_stride = 1, D
     out = torch.empty(x.shape, dtype=out_dtype, device=device)
     _lib.call("gdn_gated_rmsnorm", _lib.ptr(x), _lib.dtype_code(x.dtype), _lib.ptr(gate),
-              _lib.dtype_code(gate.dtype), _lib.ptr(w), float(eps), _lib.ptr(out),
+              _lib.dtype_code(gate.dtype), z_stride, heads, _lib.ptr(w), float(eps), _lib.ptr(out),
               _lib.dtype_code(out_dtype), rows, D, _stream(device))
     return out
 

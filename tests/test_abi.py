@@ -84,7 +84,11 @@ def test_invalid_arguments_return_einval_without_launching():
 def test_empty_work_is_a_no_op():
     lib = _lib.load()
     assert lib.gdn_gates(None, None, 0, None, None, None, None, 0, 0, 4, None) == 0
-    assert lib.gdn_gated_rmsnorm(None, 0, None, 0, None, 1e-6, None, 0, 0, 8, None) == 0
+    assert lib.gdn_gated_rmsnorm(None, 0, None, 0, 8, 1, None, 1e-6, None, 0, 0, 8, None) == 0
+    # a z layout that does not fit the rows
+    p = ctypes.c_void_p(4096)
+    assert lib.gdn_gated_rmsnorm(p, 0, p, 0, 8, 3, p, 1e-6, p, 0, 4, 8, None) == _lib.GDN_EINVAL
+    assert lib.gdn_gated_rmsnorm(p, 0, p, 0, 15, 2, p, 1e-6, p, 0, 4, 8, None) == _lib.GDN_EINVAL
 
 
 def test_quantized_matmul_workspace_size():

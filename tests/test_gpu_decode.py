@@ -241,6 +241,24 @@ def test_gated_rms_norm_row_shapes_match_oracle(gpu, D, rows, x_dtype, misaligne
     assert_bf16_out_close(out.float().cpu().numpy(), expected)
 
 
+@pytest.mark.parametrize("zdt", [torch.bfloat16, torch.float32])
+def test_gated_rms_norm_reads_a_column_view_of_z(gpu, zdt):
+    """z as the (T, H, D) column view of a stacked projection output, read
+    in place (bf16: the vectorised kernel; float32: the general one): bit
+    for bit the packed z."""
+
+    rng = np.random.default_rng(12)
+    T, H, D = 37, 4, 128
+    y = _t(rng.standard_normal((T, H, D)), gpu, torch.bfloat16)
+    stacked = _t(R.bf16_round(rng.standard_normal((T, 8 + H * D + 24))), gpu, zdt)
+    z = stacked[:, 8:8 + H * D].reshape(T, H, D)
+    assert not z.is_contiguous() and z.stride() == (8 + H * D + 24, D, 1)
+    w = _t(rng.uniform(0.5, 1.5, D), gpu)
+    a = gdn.gated_rms_norm(y, z, w, 1e-6, out_dtype=torch.bfloat16)
+    b = gdn.gated_rms_norm(y, z.contiguous(), w, 1e-6, out_dtype=torch.bfloat16)
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gated_rms_norm_matches_oracle(gpu, dtype):
     rng = np.random.default_rng(6)
