@@ -544,9 +544,10 @@ class PrefillGraph:
     sequence run without copies, and the cache's state tensors are then
     overwritten two steps later on this graph: clone them to keep a
     snapshot, and before another sequence's step on the same graph. The
-    returned output holds until the next step. Shapes and buffers are fixed
-    at capture; a prompt's last, shorter chunk runs through ``layer`` as
-    usual."""
+    returned output holds until the next step. Writing the chunk straight
+    into ``self.x`` (and calling ``step(cache)``) skips its copy. Shapes and
+    buffers are fixed at capture; a prompt's last, shorter chunk runs through
+    ``layer`` as usual."""
 
     def __init__(self, layer: "Qwen3_5LinearAttention", x_example: torch.Tensor,
                  residual_example: torch.Tensor | None = None) -> None:
