@@ -189,6 +189,25 @@ def test_frontend_production_heads_ragged_runs_match_oracle(gpu, Hk, Hv):
     _frontend_vs_oracle(gpu, dims, qkv, conv, w, cu, torch.float32)
 
 
+@pytest.mark.parametrize("dims", [gdn.LinearAttentionDims(2, 4, 32, 32, 4), DIMS_PROD])
+def test_frontend_reads_qkv_as_a_column_view(gpu, dims):
+    """qkv as the first columns of a stacked projection output, read with
+    its row stride (general kernel for 32-wide heads, tiled for 128): bit
+    for bit the packed qkv, with packed runs and a float32 conv state."""
+
+    rng = np.random.default_rng(13)
+    C = dims.conv_dim
+    cu = torch.tensor([0, 5, 5, 40, 77], dtype=torch.int32, device=gpu)
+    stacked = _t(R.bf16_round(rng.standard_normal((77, C + 40))), gpu, torch.bfloat16)
+    qkv = stacked[:, :C]
+    conv = _t(rng.standard_normal((4, 3, C)), gpu)
+    w = _t(rng.standard_normal((C, 4)) * 0.2, gpu)
+    a = gdn.conv_frontend(qkv, conv, w, dims, cu)
+    b = gdn.conv_frontend(qkv.contiguous(), conv, w, dims, cu)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
 def test_frontend_writes_a_given_conv_out(gpu):
     rng = np.random.default_rng(10)
     C = DIMS_PROD.conv_dim
