@@ -224,6 +224,56 @@ def quantized_layer(dev, hidden=2048, seed=0):
     return layer, g, rnd
 
 
+def bench_layer_stack_decode(dev, B, layers, steps, warmup, hidden=2048):
+    """`layers` gated-delta layers (each with its own 4-bit weights and a
+    pool of 4 B slots) decoding B sequences, chained through the decoder's
+    residual (h = h + layer(h)), all captured in one HIP graph: the per-layer
+    cost of a decode step when the host's launch work is amortised over the
+    stack, as in a whole-model graph."""
+
+    d = gdn.QWEN3_5_LINEAR
+    P = 4 * B
+    stack, pools = [], []
+    for i in range(layers):
+        layer, g, rnd = quantized_layer(dev, hidden, seed=100 + i)
+        pool = gdn.RecurrentStatePool(P, 4, d.conv_dim, d.num_value_heads, 128, 128,
+                                      dtype=torch.bfloat16, device=dev)
+        pool.ssm_state.normal_(0, 0.05, generator=g)
+        stack.append(layer)
+        pools.append(pool)
+    slots = list(range(B))
+    x = torch.randn(B, hidden, device=dev).to(torch.bfloat16)
+
+    def run():
+        h = x
+        for layer, pool in zip(stack, pools):
+            h = layer.decode_batch(h, pool, slots=slots, residual=h)
+        return h
+
+    for _ in range(max(warmup, 1)):
+        run()
+    torch.cuda.synchronize()
+    for pool in pools:  # the slot arrays exist before capture
+        pool.device_slots(slots)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        run()
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = e0.elapsed_time(e1) * 1e3 / steps
+    return {"workload": f"{layers} gated-delta layers decoding B={B} (each of 4 B slots, 4-bit "
+                        f"projections, hidden {hidden}) chained through the residual, one HIP graph",
+            "layers": layers, "step_us": step_us, "per_layer_us": step_us / layers,
+            "tokens_per_s": B / (step_us * 1e-6)}
+
+
 def bench_layer_decode(dev, B, steps, warmup, hidden=2048):
     """The whole gated-delta layer (Hk=16, Hv=32, d=128) decoding B active
     sequences out of a pool of 4 B slots, 4-bit group-64 projections
@@ -669,6 +719,8 @@ def main(argv=None):
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode_large", "decode_slots", "layer_decode", "layer_prefill",
                              "prefill", "prefill_varlen", "qlinear", "copy"])
+    ap.add_argument("--layers", type=int, default=1,
+                    help="layer_decode: also time this many layers chained in one graph")
     ap.add_argument("--batch", type=int, default=64,
                     help="active sequences of the layer_decode workload (pool of 4x as many slots)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -776,6 +828,8 @@ def main(argv=None):
 
     if args.workload == "layer_decode":
         r = bench_layer_decode(dev, args.batch, args.steps, args.warmup)
+        stack = (bench_layer_stack_decode(dev, args.batch, args.layers, args.steps, args.warmup)
+                 if args.layers > 1 else None)
         print(json.dumps({"metric": "gated-delta layer decode tokens/s (projections included)",
                           "value": r["graph_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup,
@@ -785,7 +839,8 @@ def main(argv=None):
                           "eager_step_us": r["step_us"],
                           "parts_us": {"input_projection": r["input_projection_us"],
                                        "out_proj": r["out_proj_us"],
-                                       "note": "each part alone, 20 calls a HIP graph"}}))
+                                       "note": "each part alone, 20 calls a HIP graph"},
+                          **({"stack": stack} if stack else {})}))
         return 0
 
     if args.workload == "layer_prefill":
