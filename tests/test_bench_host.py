@@ -24,7 +24,7 @@ def test_more_than_one_gpu_exits_with_a_message():
 def test_decode_bytes_of_the_measured_workloads():
     # B=64, Hk=16, Hv=32, d=128, 4 taps (pooled decode): the state tiles read
     # and written once (8 Hv d^2 bytes a sequence) are ~97 % of the bytes, the
-    # conv state (read and written in float32 terms) and the inputs the rest
+    # conv state (3 C bf16 values read and written) and the inputs the rest
     per_token, per_step, total = bench.decode_bytes(64, 16, 32, 128, 4, False)
     assert total == 276_439_296
     assert 0.96 < 8 * 32 * 128 * 128 / per_token < 0.98
