@@ -1,16 +1,19 @@
 """Benchmark of the gated-delta path on one MI355X.
 
-Default workload (the headline line): batched single-token decode, B=64
-sequences, Hk=16 key heads, Hv=32 value heads, d=128, K=4 conv taps, bf16
-activations, float32 recurrent state; one step = one fused decode launch
-(conv + SiLU + roll, q/k scaling, gates, recurrence) for all 64 sequences.
-The float32 state rotates through four 128 MiB buffers (step s reads buffer
-s % 4 and writes (s + 1) % 4), so the 512 MiB working set exceeds the 256 MB
-Infinity Cache and the bandwidth figure is HBM's, not the cache's.
+Default workload (the headline line): batched single-token decode, B=256
+sequences, Hk=16 key heads, Hv=64 value heads, d=128, K=4 conv taps, bf16
+activations, float32 recurrent state (1 GiB), the z gate and gated RMSNorm
+fused; one step = one fused decode launch (conv + SiLU + roll, q/k scaling,
+gates, recurrence, gated norm) for all 256 sequences. The state rotates
+through four buffers: step s reads buffer s % 4 and writes (s + 2) % 4, so
+no step reads what the step before it wrote, and the working set (4 GiB)
+exceeds the 256 MB Infinity Cache: the bandwidth figure is HBM's.
 
 Also measured in the same run (reported under "also"):
-  decode_large: B=256, Hv=64, fused conv roll + gated RMSNorm (1 GiB state)
-  prefill:      B=1, T=4096 chunked prefill (bf16 MFMA)
+  decode_b64:   B=64, Hv=32, no gate (128 MiB state, four rotating buffers
+                as above: 512 MiB)
+  prefill:      B=1, T=4096 chunked prefill (bf16 MFMA), with its roofline
+                and CPU baseline
   prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
   decode_slots: B=64 active sequences at random slots of a 256-sequence pool
   layer_decode: the whole layer's decode step with 4-bit projections, B=64
@@ -21,8 +24,9 @@ Also measured in the same run (reported under "also"):
   projections (--workload layer_prefill: the same alone)
 
 python bench.py [--steps K] [--warmup W] [--batch B]
-                [--workload decode|decode_large|decode_slots|layer_decode|layer_prefill|prefill|
+                [--workload decode|decode_b64|decode_slots|layer_decode|layer_prefill|prefill|
                             prefill_varlen|qlinear|copy]
+(--workload decode_large is the default decode workload under its older name.)
 """
 
 from __future__ import annotations
@@ -96,13 +100,15 @@ class DecodeWorkload:
         stream = torch.cuda.current_stream().cuda_stream
         n_s, n_i = len(self.states), len(self.qkv)
         phases = []
+        # step s reads state buffer s % n_s and writes (s + 2) % n_s: the
+        # buffer a step reads was last written two steps earlier
         for s in range(np.lcm(np.lcm(n_s, n_i), 2)):
             phases.append((
                 self.qkv[s % n_i].data_ptr(), self.convs[s % 2].data_ptr(),
                 self.convs[(s + 1) % 2].data_ptr(), self.conv_w.data_ptr(),
                 self.a[s % n_i].data_ptr(), self.b[s % n_i].data_ptr(), self.A_log.data_ptr(),
                 self.dt_bias.data_ptr(), self.states[s % n_s].data_ptr(),
-                self.states[(s + 1) % n_s].data_ptr(),
+                self.states[(s + 2) % n_s].data_ptr(),
                 self.z[s % n_i].data_ptr() if self.with_z else None,
                 self.norm_w.data_ptr() if self.with_z else None, 1e-6, self.out.data_ptr(),
                 _lib.GDN_BF16, self.B, d.num_key_heads, d.num_value_heads, 128, 128, 4,
@@ -633,10 +639,10 @@ def cpu_baseline_prefill(Hk, Hv, budget_s=10.0):
     }
 
 
-def cpu_baseline_decode(B, Hk, Hv, budget_s=10.0):
+def cpu_baseline_decode(B, Hk, Hv, with_z, budget_s=10.0):
     """The C restatement of the reference's decode path (fused front-end +
-    recurrence, float32, OpenMP over (sequence, head)) timed on the host on a
-    bounded number of steps of the same workload."""
+    recurrence [+ gated RMSNorm], float32, OpenMP over (sequence, head))
+    timed on the host on a bounded number of steps of the same workload."""
 
     from oracle import cref
 
@@ -646,16 +652,18 @@ def cpu_baseline_decode(B, Hk, Hv, budget_s=10.0):
     conv_w = (rng.standard_normal((C, K)) * 0.2).astype(np.float32)
     A_log = rng.uniform(0, np.log(16), Hv).astype(np.float32)
     dt_bias = rng.uniform(-1, 1, Hv).astype(np.float32)
-    state = (rng.standard_normal((B, Hv, d, d)) * 0.05).astype(np.float32)
-    conv = rng.standard_normal((B, K - 1, C)).astype(np.float32)
-    qkv = rng.standard_normal((B, C)).astype(np.float32)
-    a = rng.standard_normal((B, Hv)).astype(np.float32)
-    b = rng.standard_normal((B, Hv)).astype(np.float32)
-    cref.decode_step(qkv, conv, conv_w, a, b, A_log, dt_bias, state, None, None, 1e-6,
+    norm_w = rng.uniform(0.5, 1.5, d).astype(np.float32) if with_z else None
+    state = rng.standard_normal((B, Hv, d, d), dtype=np.float32) * np.float32(0.05)
+    conv = rng.standard_normal((B, K - 1, C), dtype=np.float32)
+    qkv = rng.standard_normal((B, C), dtype=np.float32)
+    a = rng.standard_normal((B, Hv), dtype=np.float32)
+    b = rng.standard_normal((B, Hv), dtype=np.float32)
+    z = rng.standard_normal((B, Hv, d), dtype=np.float32) if with_z else None
+    cref.decode_step(qkv, conv, conv_w, a, b, A_log, dt_bias, state, z, norm_w, 1e-6,
                      (Hk, Hv, d, d), True, state_out=state)
     steps, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < budget_s:
-        _, conv, _ = cref.decode_step(qkv, conv, conv_w, a, b, A_log, dt_bias, state, None, None,
+        _, conv, _ = cref.decode_step(qkv, conv, conv_w, a, b, A_log, dt_bias, state, z, norm_w,
                                       1e-6, (Hk, Hv, d, d), True, state_out=state)
         steps += 1
     dt = time.perf_counter() - t0
@@ -666,7 +674,8 @@ def cpu_baseline_decode(B, Hk, Hv, budget_s=10.0):
         "cores": min(threads, len(os.sched_getaffinity(0))),
         "kind": "port",
         "sample": f"{steps} fused decode steps of the B={B}, Hv={Hv} workload "
-                  f"({B * steps} tokens, {dt:.1f} s), float32 C/OpenMP restatement",
+                  f"{'with the gated RMSNorm ' if with_z else ''}({B * steps} tokens, {dt:.1f} s), "
+                  f"float32 C/OpenMP restatement",
     }
 
 
@@ -711,13 +720,90 @@ def load_traffic(name):
         return None
 
 
+DECODE_WORKLOADS = {
+    False: "decode B=256 Hk=16 Hv=64 d=128 K=4, fused conv roll + gated RMSNorm",
+    True: "decode B=64 Hk=16 Hv=32 d=128 K=4, fused conv roll",
+}
+
+
+def decode_roofline(r, small):
+    return {
+        "bound": "hbm",
+        "achieved": r["hbm_gbs"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": r["hbm_frac"],
+        "traffic": load_traffic(f"gdn_decode_step_{'b64_hv32' if small else 'b256_hv64'}_traffic.json"),
+        "kernel": "gdn_decode_step",
+        "kernel_us": r["kernel_us"],
+        "isolated_launch_us": r["isolated_launch_us"],
+        "algorithmic_bytes_per_launch": r["bytes_per_step"],
+    }
+
+
+def prefill_roofline(r):
+    return {
+        "bound": "mfma",
+        "achieved": r["tflops"],
+        "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": r["mfma_frac"],
+        "traffic": load_traffic("gdn_prefill_chunked_t4096_traffic.json"),
+        "kernel": "gdn_prefill_chunked (one call: all its launches)",
+        "kernel_us": r["call_us"],
+        "isolated_launch_us": r["isolated_call_us"],
+        "algorithmic_flops_per_launch": r["flops_per_call"],
+    }
+
+
+def bench_also(dev, cpu=True):
+    """The secondary workloads of the default run."""
+
+    sm = bench_decode(dev, 64, 16, 32, False, steps=64, warmup=8)
+    pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
+    pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
+    sl = bench_decode_slots(dev, 64, 16, 32, steps=64, warmup=8)
+    ld = bench_layer_decode(dev, 64, steps=64, warmup=8)
+    lp = bench_layer_prefill(dev, 4096, steps=20, warmup=3)
+    return {
+        "decode_b64": {
+            "workload": DECODE_WORKLOADS[True], "tokens_per_s": sm["tokens_per_s"],
+            "roofline": decode_roofline(sm, True),
+            **({"cpu_baseline": cpu_baseline_decode(64, 16, 32, False, budget_s=5.0)} if cpu else {})},
+        "prefill": {
+            "workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64, bf16 MFMA",
+            "tokens_per_s": pf["tokens_per_s"], "call_us": pf["call_us"],
+            "roofline": prefill_roofline(pf),
+            **({"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)} if cpu else {})},
+        "prefill_varlen": {
+            "workload": "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 "
+                        "Hv=32, nonzero initial states",
+            "tokens_per_s": pv["tokens_per_s"], "call_us": pv["call_us"],
+            "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"],
+            "continuation": pv["continuation"]},
+        "decode_slots": sl,
+        "layer_decode": {
+            "workload": ld["workload"] + ", HIP-graph steps",
+            "tokens_per_s": ld["graph_tokens_per_s"], "step_us": ld["graph_step_us"],
+            "input_projection_us": ld["input_projection_us"],
+            "out_proj_us": ld["out_proj_us"]},
+        "layer_prefill": {
+            "workload": lp["workload"], "tokens_per_s": lp["tokens_per_s"],
+            "step_us": lp["step_us"], "input_projection_us": lp["input_projection_us"],
+            "core_us": lp["core_us"], "out_proj_us": lp["out_proj_us"],
+            "chunk512_eager_us": lp["chunk_eager_us"],
+            "chunk512_graph_us": lp["chunk_graph_us"]},
+    }
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "decode_slots", "layer_decode", "layer_prefill",
+                    choices=["decode", "decode_large", "decode_b64", "decode_slots", "layer_decode",
+                             "layer_prefill",
                              "prefill", "prefill_varlen", "qlinear", "copy"])
     ap.add_argument("--layers", type=int, default=1,
                     help="layer_decode: also time this many layers chained in one graph")
@@ -749,11 +835,10 @@ def main(argv=None):
                           "gbs": nbytes / (copy_ms * 1e-3) / 1e9}))
         return 0
 
-    if args.workload in ("decode", "decode_large"):
-        big = args.workload == "decode_large"
-        B, Hk, Hv, with_z = (256, 16, 64, True) if big else (64, 16, 32, False)
+    if args.workload in ("decode", "decode_large", "decode_b64"):
+        small = args.workload == "decode_b64"
+        B, Hk, Hv, with_z = (64, 16, 32, False) if small else (256, 16, 64, True)
         r = bench_decode(dev, B, Hk, Hv, with_z, args.steps, args.warmup)
-        kernel = "gdn_decode_step"
         line = {
             "metric": METRIC,
             "value": r["tokens_per_s"],
@@ -768,61 +853,16 @@ def main(argv=None):
             "dtype": "bf16",
             "data": "synthetic",
             "config": {
-                "workload": ("decode B=256 Hk=16 Hv=64 d=128 K=4, fused conv roll + gated RMSNorm"
-                             if big else "decode B=64 Hk=16 Hv=32 d=128 K=4, fused conv roll"),
+                "workload": DECODE_WORKLOADS[small],
                 "batch": B, "tokens_per_step": B, "key_heads": Hk, "value_heads": Hv,
-                "head_dim": 128, "state": "float32, 4 rotating buffers",
+                "head_dim": 128, "state": "float32, 4 buffers: step s reads s % 4, writes (s + 2) % 4",
             },
-            "roofline": {
-                "bound": "hbm",
-                "achieved": r["hbm_gbs"],
-                "peak": HBM_PEAK_GBS,
-                "unit": "GB/s",
-                "frac": r["hbm_frac"],
-                "traffic": load_traffic(f"{kernel}_{'b256_hv64' if big else 'b64_hv32'}_traffic.json"),
-                "kernel": kernel,
-                "kernel_us": r["kernel_us"],
-                "isolated_launch_us": r["isolated_launch_us"],
-                "algorithmic_bytes_per_launch": r["bytes_per_step"],
-            },
+            "roofline": decode_roofline(r, small),
         }
         if not args.no_cpu_baseline:
-            line["cpu_baseline"] = cpu_baseline_decode(B, Hk, Hv, budget_s=10.0)
-        if not args.no_also and not big:
-            lg = bench_decode(dev, 256, 16, 64, True, steps=64, warmup=8)
-            pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
-            pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
-            sl = bench_decode_slots(dev, 64, 16, 32, steps=64, warmup=8)
-            ld = bench_layer_decode(dev, 64, steps=64, warmup=8)
-            lp = bench_layer_prefill(dev, 4096, steps=20, warmup=3)
-            line["also"] = {
-                "decode_slots": sl,
-                "layer_decode": {
-                    "workload": ld["workload"] + ", HIP-graph steps",
-                    "tokens_per_s": ld["graph_tokens_per_s"], "step_us": ld["graph_step_us"],
-                    "input_projection_us": ld["input_projection_us"],
-                    "out_proj_us": ld["out_proj_us"]},
-                "layer_prefill": {
-                    "workload": lp["workload"], "tokens_per_s": lp["tokens_per_s"],
-                    "step_us": lp["step_us"], "input_projection_us": lp["input_projection_us"],
-                    "core_us": lp["core_us"], "out_proj_us": lp["out_proj_us"],
-                    "chunk512_eager_us": lp["chunk_eager_us"],
-                    "chunk512_graph_us": lp["chunk_graph_us"]},
-                "decode_large": {
-                    "workload": "decode B=256 Hk=16 Hv=64 d=128, fused conv roll + gated RMSNorm",
-                    "tokens_per_s": lg["tokens_per_s"], "kernel_us": lg["kernel_us"],
-                    "hbm_gbs": lg["hbm_gbs"], "hbm_frac": lg["hbm_frac"]},
-                "prefill": {
-                    "workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64, bf16 MFMA",
-                    "tokens_per_s": pf["tokens_per_s"], "call_us": pf["call_us"],
-                    "tflops": pf["tflops"], "mfma_frac": pf["mfma_frac"],
-                    "flops_per_call": pf["flops_per_call"]},
-                "prefill_varlen": {
-                    "workload": "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 "
-                                "Hv=32, nonzero initial states",
-                    "tokens_per_s": pv["tokens_per_s"], "call_us": pv["call_us"],
-                    "tflops": pv["tflops"], "mfma_frac": pv["mfma_frac"],
-                    "continuation": pv["continuation"]}}
+            line["cpu_baseline"] = cpu_baseline_decode(B, Hk, Hv, with_z, budget_s=10.0)
+        if not args.no_also and not small:
+            line["also"] = bench_also(dev, cpu=not args.no_cpu_baseline)
         print(json.dumps(line))
         return 0
 
@@ -915,11 +955,8 @@ def main(argv=None):
                               "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 Hv=32 "
                               "d=128 chunk 64" if varlen else
                               "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64")},
-                          "roofline": {"bound": "mfma", "achieved": r["tflops"],
-                                       "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                       "frac": r["mfma_frac"], "traffic": None,
-                                       "kernel": "gdn_prefill_chunked (3 launches)",
-                                       "call_us": r["call_us"]},
+                          "roofline": ({**prefill_roofline(r), "traffic": None} if varlen
+                                       else prefill_roofline(r)),
                           **({} if args.no_cpu_baseline or varlen else
                              {"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)}),
                           **({"continuation": r["continuation"]} if varlen else {})}))

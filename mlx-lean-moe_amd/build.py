@@ -30,14 +30,31 @@ def sources() -> list[str]:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile all kernels into ``libgdn.so`` (always recompiles)."""
+    """Compile all kernels into ``libgdn.so`` (always recompiles): one hipcc
+    process per source file, run in parallel, then one link."""
+
+    import concurrent.futures
+    import tempfile
 
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB_PATH + f".tmp{os.getpid()}"
-    cmd = [hipcc, *HIPCC_FLAGS, *sources(), "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="gdn_build_") as tmpdir:
+        jobs = []
+        for src in sources():
+            obj = os.path.join(tmpdir, os.path.basename(src) + ".o")
+            jobs.append(([hipcc, *compile_flags, "-c", src, "-o", obj], obj))
+        workers = min(len(jobs), max(1, min(os.cpu_count() or 1, 8)))
+
+        def run(cmd):
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            subprocess.run(cmd, check=True)
+
+        with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+            for f in [pool.submit(run, cmd) for cmd, _ in jobs]:
+                f.result()
+        tmp = LIB_PATH + f".tmp{os.getpid()}"
+        run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for _, o in jobs], "-o", tmp])
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -27,7 +27,8 @@ class LinearAttentionDims:
 
     @property
     def conv_dim(self) -> int:
-        """The convolution runs over q, k and v concatenated."""
+        """Channels of the depthwise conv: the q, k and v projections side by
+        side (two key_dim blocks, then value_dim)."""
         return self.key_dim * 2 + self.value_dim
 
 

@@ -34,7 +34,7 @@ __global__ void gates_kernel(const void* a, const void* b, int ab_dtype, const f
     if (i >= n) return;
     const int h = int(i % Hv);
     if (g) g[i] = expf(log_forget_gate(load_any(a, i, ab_dtype), A_log[h], dt_bias[h]));
-    if (beta) store_any(beta, i, beta_dtype, sigmoid(load_any(b, i, ab_dtype)));
+    if (beta) store_any(beta, i, beta_dtype, beta_of(load_any(b, i, ab_dtype), beta_dtype));
 }
 
 // One wave per row: out = silu(z) * rms_norm(x held in out's dtype, w, eps),

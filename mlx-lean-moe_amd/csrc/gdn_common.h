@@ -95,6 +95,25 @@ GDN_DEV float round_to(float x, int dtype) {
     return dtype == GDN_BF16 ? round_bf16(x) : f16_bits_to_f32(f32_to_f16_bits(x));
 }
 
+// One rounding of a double to what `dtype` holds: round to nearest even,
+// as if from the exact value. float32 directly; bfloat16 and float16 through
+// float32 rounded to odd (truncated, with the last bit set if anything was
+// dropped), which keeps enough of the dropped bits for the second rounding
+// to nearest to land where one rounding of the double would.
+GDN_DEV float round_once(double x, int dtype) {
+    if (dtype == GDN_F32) return float(x);
+    float f = __double2float_rz(x);
+    if (double(f) != x) f = __uint_as_float(__float_as_uint(f) | 1u);
+    return round_to(f, dtype);
+}
+
+// beta = sigmoid(b) held in `dtype` (linear_attention.py:116), evaluated in
+// double and rounded once: the value the exact sigmoid rounds to, so the
+// decision at a rounding boundary does not depend on float32 error.
+GDN_DEV float beta_of(float b, int dtype) {
+    return round_once(1.0 / (1.0 + exp(-double(b))), dtype);
+}
+
 // Compile-time activation formats for the specialised kernels.
 struct ActF32 {
     using storage = float;
@@ -155,6 +174,13 @@ GDN_DEV float mask_select(uint32_t m, float a, float b) {
 
 template <int WIDTH>
 GDN_DEV float group_sum(float x) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+    return x;
+}
+
+template <int WIDTH>
+GDN_DEV double group_sum(double x) {
 #pragma unroll
     for (int off = WIDTH / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
     return x;

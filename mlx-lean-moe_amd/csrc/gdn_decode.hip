@@ -174,18 +174,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
         roll_taps<Act>(t2, cso, C, c2);
     } else if (tid == kD) {
         gate_g = expf(log_forget_gate(av, alog, dtb));
-        gate_beta = Act::round(sigmoid(bv));
+        gate_beta = beta_of(bv, Act::code);
     }
     __syncthreads();
     if (w < 2) {
+        // rms_norm(x, 1e-6) rounded once from its exact value: the sum of
+        // squares (exact in double for activation-dtype inputs), the
+        // reciprocal root and the products in double; then the scale, whose
+        // product with a 16-bit value is exact in float32
         float* arr = w == 0 ? qs : ks;
         const float x0 = arr[l], x1 = arr[l + 64];
-        const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
-        const float rr = 1.f / sqrtf(ss / float(kD) + 1e-6f);
+        const double ss = group_sum<kWave>(double(x0) * x0 + double(x1) * x1);
+        const double rr = 1.0 / sqrt(ss / kD + 1e-6);
         const float inv = 1.f / sqrtf(float(kD));
         const float sc = Act::round(w == 0 ? inv * inv : inv);
-        arr[l] = Act::round(sc * Act::round(x0 * rr));
-        arr[l + 64] = Act::round(sc * Act::round(x1 * rr));
+        arr[l] = Act::round(sc * round_once(x0 * rr, Act::code));
+        arr[l + 64] = Act::round(sc * round_once(x1 * rr, Act::code));
     }
     __syncthreads();
 

@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         float lg, beta;
         if (gate_mode == 0) {
             lg = log_forget_gate(load_any(ga, i, gb_dtype), A_log[hv], dt_bias[hv]);
-            beta = round_to(sigmoid(load_any(gb, i, gb_dtype)), gb_dtype);
+            beta = beta_of(load_any(gb, i, gb_dtype), gb_dtype);
         } else {
             const float gv = static_cast<const float*>(ga)[i];
             lg = gv > 0.f ? logf(gv) : kLogGateFloor;

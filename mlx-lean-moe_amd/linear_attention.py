@@ -29,7 +29,8 @@ import torch
 
 from . import _lib
 from .config import LinearAttentionDims
-from .gated_delta import _c, _check_out, _require_device, _stream, gated_delta_update
+from .gated_delta import (_c, _check_cu_seqlens, _check_out, _require_device, _stream,
+                          gated_delta_update)
 from .quant import (LinearWeights, QuantScheme, concat_quantized, quantized_linear,
                     quantized_linear_split)
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
@@ -71,10 +72,14 @@ def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torc
     (linear_attention.py:61-79,103-113).
 
     ``qkv (T, C)`` in the activation dtype; ``conv_state (N, K-1, C)`` (any
-    float dtype); ``conv_weight (C, K)``; ``cu_seqlens`` device int32 offsets
-    or None for N equal runs. Returns ``q, k (T, Hk, Dk)``, ``v (T, Hv, Dv)``
-    and the new conv state ``(N, K-1, C)`` in the activation dtype (written
-    into ``conv_out`` if given: contiguous, not overlapping ``conv_state``)."""
+    float dtype); ``conv_weight (C, K)``; ``cu_seqlens`` the N+1 int32
+    offsets of the runs (a host sequence, or a device tensor, which is read
+    back to the host once for the check below), or None for N equal runs.
+    The offsets are checked before anything is launched: N+1 of them,
+    from 0 to T, non-decreasing (``ValueError`` otherwise). Returns
+    ``q, k (T, Hk, Dk)``, ``v (T, Hv, Dv)`` and the new conv state
+    ``(N, K-1, C)`` in the activation dtype (written into ``conv_out`` if
+    given: contiguous, not overlapping ``conv_state``)."""
 
     device = _require_device(qkv, conv_state, conv_weight)
     T, C = qkv.shape
@@ -82,6 +87,7 @@ def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torc
     K = dims.conv_kernel_dim
     if C != dims.conv_dim or tuple(conv_state.shape[1:]) != (K - 1, C):
         raise ValueError("qkv/conv_state do not match the layer's conv_dim and kernel")
+    cu_seqlens = _runs_on_device(cu_seqlens, N, T, device)
     act = qkv.dtype
     if act not in (torch.float32, torch.bfloat16):
         raise ValueError(f"activations must be float32 or bfloat16, got {act}")
@@ -104,6 +110,24 @@ def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torc
               _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), dims.num_key_heads, dims.num_value_heads,
               dims.key_head_dim, dims.value_head_dim, K, _lib.dtype_code(act), _stream(device))
     return q, k, v, new_conv
+
+
+def _runs_on_device(cu_seqlens, N: int, T: int, device) -> torch.Tensor | None:
+    """Checked run offsets as an int32 device tensor (None: N equal runs,
+    T a multiple of N)."""
+
+    if cu_seqlens is None:
+        if N <= 0 or T % N:
+            raise ValueError(f"{T} tokens do not split into {N} equal runs; pass cu_seqlens")
+        return None
+    offsets = _check_cu_seqlens(cu_seqlens, T)
+    if len(offsets) != N + 1:
+        raise ValueError(f"cu_seqlens must hold {N + 1} offsets (one more than the "
+                         f"{N} conv states), got {len(offsets)}")
+    if (isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device == device
+            and cu_seqlens.dtype == torch.int32 and cu_seqlens.is_contiguous()):
+        return cu_seqlens
+    return torch.tensor(offsets, dtype=torch.int32).to(device)
 
 
 def _fused_decode_ok(dims: LinearAttentionDims, act: torch.dtype) -> bool:
@@ -380,10 +404,11 @@ class Qwen3_5LinearAttention:
 
         d = self.linear
         T = qkv.shape[0]
-        cu_dev = None
+        # the offsets are read to the host once and checked there before
+        # the first launch (each launch below checks the host list again)
         if cu_seqlens is not None:
-            cu_dev = torch.as_tensor(cu_seqlens, dtype=torch.int32).to(qkv.device)
-        q, k, v, new_conv = conv_frontend(qkv, conv_state, self.conv1d_weight, d, cu_dev,
+            cu_seqlens = _check_cu_seqlens(cu_seqlens, T)
+        q, k, v, new_conv = conv_frontend(qkv, conv_state, self.conv1d_weight, d, cu_seqlens,
                                           conv_out=conv_out)
         # y straight in z's dtype: the norm's first step rounds it there
         if cu_seqlens is None:
@@ -498,11 +523,13 @@ class DecodeGraph:
         self.x = x_example.detach().clone()
         self.residual = None if residual_example is None else residual_example.detach().clone()
         self._idx = np.asarray(self.slots, dtype=np.int64)
-        # the slot array must exist before capture (no host copy in the graph)
+        # the slot array must exist before capture (no host copy in the
+        # graph), and the graph holds it: the pool's cache of slot arrays may
+        # drop it later, and a replay must not read freed (reused) memory
         side = torch.cuda.Stream(self.x.device)
         side.wait_stream(torch.cuda.current_stream(self.x.device))
         with torch.cuda.stream(side):
-            pool.device_slots(self.slots)
+            self._slot_t = pool.device_slots(self.slots)
         torch.cuda.current_stream(self.x.device).wait_stream(side)
         torch.cuda.synchronize(self.x.device)
         self.graph = torch.cuda.CUDAGraph()

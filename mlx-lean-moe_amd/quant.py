@@ -76,8 +76,9 @@ class QuantScheme:
 
 @dataclass(frozen=True)
 class LinearWeights:
-    """A loaded linear projection with its own storage scheme; ``quant`` is
-    ``None`` for an ordinary floating-point matrix (moe_block.py:13-20).
+    """One projection's weights as read: a dense matrix (``quant`` None) or
+    the packed codes with their per-group scales and biases under
+    ``quant`` (the reference's type, moe_block.py:13-20).
 
     ``dense``, for quantized weights, optionally holds their bf16
     dequantization (``dequantize(tensors, quant, bfloat16)``, see

@@ -6,7 +6,7 @@ The reference indexes a checkpoint's shards by byte range
 (``weights/expert_loader.py:164-180``), decodes them
 (``expert_loader.py:53-85``: BF16 is widened exactly to float32, except the
 quantization ``scales``/``biases``, which keep their stored bf16 width),
-validates each projection's packed layout (``expert_loader.py:95-141``) and
+checks each projection's packed layout (``expert_loader.py:95-141``) and
 reads it as dense or quantized weights (``expert_loader.py:144-161``); the
 decoder layer pulls the linear-attention tensors by name
 (``model/qwen3_5/transformer.py:52-65``) and the HF config supplies the shapes
@@ -19,61 +19,69 @@ from __future__ import annotations
 
 import json
 import os
-import struct
 from dataclasses import dataclass
 from pathlib import Path
+from typing import Iterator, NamedTuple
 
 import torch
 
 from .config import LinearAttentionDims
 from .quant import LinearWeights, QuantScheme
 
-_INDEX_FILENAME = "model.safetensors.index.json"
-_SINGLE_FILENAME = "model.safetensors"
 
+class TensorSpan(NamedTuple):
+    """One tensor inside a shard file: the safetensors dtype tag ("BF16",
+    "F32", "U32", ...), its shape, and the absolute byte range
+    ``[begin, end)`` of its data in that file."""
 
-@dataclass(frozen=True)
-class TensorLocation:
-    """Where one tensor's raw bytes live (safetensors_index.py:18-24)."""
-
-    shard: str  # file name, relative to the checkpoint directory
-    dtype: str  # safetensors dtype string: "BF16", "F32", "U32", ...
+    shard: str
+    dtype: str
     shape: tuple[int, ...]
-    offset: int  # absolute byte offset in the shard
-    length: int  # byte length of the raw data
+    begin: int
+    end: int
+
+    @property
+    def nbytes(self) -> int:
+        return self.end - self.begin
 
 
-def _shard_header(path: Path) -> tuple[dict, int]:
+def _read_header(path: Path) -> Iterator[tuple[str, str, tuple[int, ...], int, int]]:
+    """The entries of one safetensors file: a little-endian u64 header
+    length, that many bytes of JSON, then the data, which each entry's
+    ``data_offsets`` address relative to the data's first byte."""
+
     with path.open("rb") as f:
-        (header_len,) = struct.unpack("<Q", f.read(8))
-        header = json.loads(f.read(header_len))
-    return header, 8 + header_len
+        size = int.from_bytes(f.read(8), "little")
+        entries = json.loads(f.read(size))
+    base = 8 + size
+    for key, meta in entries.items():
+        if key != "__metadata__":
+            lo, hi = meta["data_offsets"]
+            yield key, meta["dtype"], tuple(meta["shape"]), base + lo, base + hi
 
 
-def _shards(model_dir: Path) -> list[str]:
-    index_json = model_dir / _INDEX_FILENAME
-    if index_json.exists():
-        return sorted(set(json.loads(index_json.read_text())["weight_map"].values()))
-    if (model_dir / _SINGLE_FILENAME).exists():
-        return [_SINGLE_FILENAME]
-    raise FileNotFoundError(f"no {_INDEX_FILENAME} or {_SINGLE_FILENAME} found under {model_dir}")
+def _shard_files(model_dir: Path) -> list[str]:
+    """Shard file names of a checkpoint: the ones the HF sharding index
+    ``model.safetensors.index.json`` maps tensors to, else the lone
+    ``model.safetensors``."""
+
+    sharded = model_dir / "model.safetensors.index.json"
+    if sharded.is_file():
+        mapping = json.loads(sharded.read_text())["weight_map"]
+        return sorted(set(mapping.values()))
+    if (model_dir / "model.safetensors").is_file():
+        return ["model.safetensors"]
+    raise FileNotFoundError(f"{model_dir} holds neither a sharding index "
+                            f"(model.safetensors.index.json) nor model.safetensors")
 
 
-def build_index(model_dir: str | Path) -> dict[str, TensorLocation]:
-    """Tensor name -> location over every shard of a checkpoint (the shards
-    an index file names, or the single ``model.safetensors``)."""
+def build_index(model_dir: str | Path) -> dict[str, TensorSpan]:
+    """Tensor name -> :class:`TensorSpan` over every shard of a checkpoint."""
 
     model_dir = Path(model_dir)
-    index: dict[str, TensorLocation] = {}
-    for shard in _shards(model_dir):
-        header, data_start = _shard_header(model_dir / shard)
-        for name, meta in header.items():
-            if name == "__metadata__":
-                continue
-            start, end = meta["data_offsets"]
-            index[name] = TensorLocation(shard, meta["dtype"], tuple(meta["shape"]),
-                                         data_start + start, end - start)
-    return index
+    return {key: TensorSpan(shard, dtype, shape, lo, hi)
+            for shard in _shard_files(model_dir)
+            for key, dtype, shape, lo, hi in _read_header(model_dir / shard)}
 
 
 # safetensors dtype -> the torch dtype holding the same bytes (unsigned
@@ -85,14 +93,16 @@ _TORCH_DTYPES = {
     "U64": torch.int64, "U32": torch.int32, "U16": torch.int16, "U8": torch.uint8,
     "BOOL": torch.bool,
 }
-# Fields kept at their stored width: the quantization metadata. Norm weights,
-# A_log, dt_bias and the conv kernel are bf16 on disk too and feed float32
-# arithmetic, so they widen (expert_loader.py:53-59).
-_STORED_WIDTH_FIELDS = ("scales", "biases")
 
 
-def keeps_stored_width(name: str) -> bool:
-    return name.rpartition(".")[2] in _STORED_WIDTH_FIELDS
+def is_quant_metadata(name: str) -> bool:
+    """Whether a tensor is a quantized projection's per-group ``scales`` or
+    ``biases``: those are handed to the matmul at their stored width. Every
+    other bf16 tensor on this path (conv kernel, ``A_log``, ``dt_bias``,
+    norm weight) feeds float32 arithmetic and is widened on read
+    (expert_loader.py:53-59)."""
+
+    return name.split(".")[-1] in ("scales", "biases")
 
 
 def decode_tensor(raw: bytes, dtype: str, shape: tuple[int, ...], *,
@@ -120,7 +130,7 @@ class CheckpointReader:
     (expert_loader.py:164-180): one ``os.pread`` per tensor, one descriptor
     per shard."""
 
-    def __init__(self, model_dir: str | Path, index: dict[str, TensorLocation] | None = None):
+    def __init__(self, model_dir: str | Path, index: dict[str, TensorSpan] | None = None):
         self.model_dir = Path(model_dir)
         self.index = index if index is not None else build_index(self.model_dir)
         self._fds: dict[str, int] = {}
@@ -132,11 +142,16 @@ class CheckpointReader:
         return fd
 
     def read_tensor(self, name: str) -> torch.Tensor:
-        loc = self.index[name]
-        raw = os.pread(self._fd(loc.shard), loc.length, loc.offset)
-        if len(raw) != loc.length:
-            raise ValueError(f"{name}: shard {loc.shard} is truncated")
-        return decode_tensor(raw, loc.dtype, loc.shape, stored_width=keeps_stored_width(name))
+        span = self.index[name]
+        raw = os.pread(self._fd(span.shard), span.nbytes, span.begin)
+        if len(raw) != span.nbytes:
+            raise ValueError(f"{name}: shard {span.shard} is truncated")
+        return decode_tensor(raw, span.dtype, span.shape, stored_width=is_quant_metadata(name))
+
+    def read_fields(self, name: str, fields) -> dict[str, torch.Tensor]:
+        """``{field: tensor}`` for each ``name.field`` the checkpoint holds."""
+
+        return {f: self.read_tensor(f"{name}.{f}") for f in fields if f"{name}.{f}" in self.index}
 
     def close(self) -> None:
         for fd in self._fds.values():
@@ -150,42 +165,59 @@ class CheckpointReader:
         self.close()
 
 
-def validate_linear_layout(index: dict[str, TensorLocation], name: str, quant: QuantScheme) -> bool:
-    """Check a projection's fields and packed shape; return whether it is
-    quantized (expert_loader.py:95-141, same conditions)."""
+class LayoutError(ValueError):
+    """A projection's tensors in a checkpoint do not fit together under its
+    quantization scheme."""
 
-    weight_name, scale_name, bias_name = f"{name}.weight", f"{name}.scales", f"{name}.biases"
-    if weight_name not in index:
-        raise KeyError(f"no weight tensor for {name}")
-    has_scales, has_biases = scale_name in index, bias_name in index
-    if not has_scales:
-        if has_biases:
-            raise ValueError(f"{name} has biases but no scales")
+
+def projection_is_quantized(index: dict[str, TensorSpan], name: str, scheme: QuantScheme) -> bool:
+    """Whether projection ``name`` is stored quantized (``name.scales``, and
+    ``name.biases`` where the scheme has them, beside the packed
+    ``name.weight``) or as a plain matrix (``name.weight`` alone).
+
+    A missing weight raises ``KeyError``. Otherwise every inconsistency is
+    collected and reported together in one :class:`LayoutError`: biases
+    stored without scales; an affine scheme without biases; biases not
+    shaped like the scales; weight and scales disagreeing in their leading
+    (row) dimensions; a packed row width other than the scale groups'
+    ``groups * group_size * bits / 32`` words. These are the conditions the
+    reference's loader enforces (expert_loader.py:95-141)."""
+
+    weight = index.get(f"{name}.weight")
+    scales = index.get(f"{name}.scales")
+    biases = index.get(f"{name}.biases")
+    if weight is None:
+        raise KeyError(f"{name}.weight is not in the checkpoint")
+    if scales is None and biases is None:
         return False
-    if quant.mode == "affine" and not has_biases:
-        raise ValueError(f"affine-quantized {name} has no biases")
-    weight, scales = index[weight_name], index[scale_name]
-    if weight.shape[:-1] != scales.shape[:-1]:
-        raise ValueError(f"{name} weight shape {weight.shape} is incompatible with scales shape "
-                         f"{scales.shape}")
-    if has_biases and index[bias_name].shape != scales.shape:
-        raise ValueError(f"{name} biases shape {index[bias_name].shape} does not match scales "
-                         f"shape {scales.shape}")
-    packed = scales.shape[-1] * quant.group_size * quant.bits // 32
-    if weight.shape[-1] != packed:
-        raise ValueError(f"{name} weight shape {weight.shape} does not match bits={quant.bits}, "
-                         f"group_size={quant.group_size}; expected packed width {packed}")
+    problems = []
+    if scales is None:
+        problems.append("per-group biases are stored without the scales they pair with")
+    else:
+        if biases is None and scheme.mode == "affine":
+            problems.append("the affine scheme dequantizes with per-group biases; none are stored")
+        if biases is not None and biases.shape != scales.shape:
+            problems.append(f"biases {biases.shape} and scales {scales.shape} differ in shape")
+        if weight.shape[:-1] != scales.shape[:-1]:
+            problems.append(f"weight {weight.shape} and scales {scales.shape} differ in their "
+                            f"leading dimensions")
+        words = scales.shape[-1] * scheme.group_size * scheme.bits // 32
+        if weight.shape[-1] != words:
+            problems.append(f"{scales.shape[-1]} groups of {scheme.group_size} {scheme.bits}-bit "
+                            f"codes pack into {words} words a row; weight {weight.shape} has "
+                            f"{weight.shape[-1]}")
+    if problems:
+        raise LayoutError(f"{name}: " + "; ".join(problems))
     return True
 
 
-def read_linear(reader: CheckpointReader, name: str, quant: QuantScheme) -> LinearWeights:
-    """A projection as dense weights (``quant`` None) or its quantized fields
-    (expert_loader.py:144-161)."""
+def read_projection(reader: CheckpointReader, name: str, scheme: QuantScheme) -> LinearWeights:
+    """Projection ``name`` as a plain matrix (``quant`` None) or as its
+    quantized fields under ``scheme`` (expert_loader.py:144-161)."""
 
-    if not validate_linear_layout(reader.index, name, quant):
-        return LinearWeights(reader.read_tensor(f"{name}.weight"), None)
-    fields = [f for f in ("weight", "scales", "biases") if f"{name}.{f}" in reader.index]
-    return LinearWeights({f: reader.read_tensor(f"{name}.{f}") for f in fields}, quant)
+    if projection_is_quantized(reader.index, name, scheme):
+        return LinearWeights(reader.read_fields(name, ("weight", "scales", "biases")), scheme)
+    return LinearWeights(reader.read_tensor(f"{name}.weight"), None)
 
 
 @dataclass(frozen=True)
@@ -258,7 +290,7 @@ def load_linear_attention(model_dir: str | Path, layer_index: int, *, device="cu
     eps = float(hf_config.get("text_config", hf_config).get("rms_norm_eps", 1e-6))
     prefix = f"{tensor_prefix}.layers.{layer_index}.linear_attn"
     with CheckpointReader(model_dir) as reader:
-        proj = {p: _to_device(read_linear(reader, f"{prefix}.{p}", quant.quant_for(f"{prefix}.{p}")),
+        proj = {p: _to_device(read_projection(reader, f"{prefix}.{p}", quant.quant_for(f"{prefix}.{p}")),
                               device) for p in _PROJECTIONS}
         conv = reader.read_tensor(f"{prefix}.conv1d.weight")
         A_log = reader.read_tensor(f"{prefix}.A_log")

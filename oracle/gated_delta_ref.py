@@ -27,7 +27,7 @@ Arithmetic runs in ``dtype`` (float64 by default, float32 for the timed
 op-for-op CPU comparator).  ``act="bf16"`` additionally rounds to bfloat16 at
 the points where the reference holds bfloat16 activations (conv output, SiLU,
 q/k scaling, ``sigmoid(b)``, the y cast before the gated norm, the gated-norm
-output).  Those rounding points follow the reference's dtype flow; where they
+output); in float64 each of these is the exact value's one rounding.  Those rounding points follow the reference's dtype flow; where they
 depend on MLX's internal bf16 kernels (``mx.fast.rms_norm``, ``mx.conv1d``,
 Python-scalar promotion) they are a best restatement and parity is unpinned
 at the bit level, which the bf16 tolerance (2e-2 max-abs) absorbs.
@@ -52,8 +52,19 @@ EPS_QK = 1e-6  # hard-coded q/k eps, model/qwen3_5/linear_attention.py:109-113
 
 
 def bf16_round(x) -> np.ndarray:
-    """Round to the nearest bfloat16 (ties to even); returns float32 values."""
+    """Round to the nearest bfloat16 (ties to even), once, from the value as
+    given; returns float32 values. float64 input is rounded on its own bits
+    (8 significant bits kept), not through float32, whose own rounding would
+    otherwise decide values within a float32 ulp of a bf16 tie."""
 
+    x = np.asarray(x)
+    if x.dtype == np.float64:
+        u = np.ascontiguousarray(x).view(np.uint64)
+        drop = np.uint64(45)  # 52 - 7 stored mantissa bits
+        half = np.uint64((1 << 44) - 1)
+        keep = np.uint64(0xFFFF_FFFF_FFFF_FFFF ^ ((1 << 45) - 1))
+        u = (u + half + ((u >> drop) & np.uint64(1))) & keep
+        return u.view(np.float64).astype(np.float32)
     x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
     u = x.view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000

@@ -13,7 +13,9 @@
  * The decode step adds the layer's front-end and epilogue
  * (src/mlx_lean_moe/model/qwen3_5/linear_attention.py:22-32,61-79,109-124).
  * With act_bf16 != 0 values are rounded to bfloat16 where the reference holds
- * bf16 activations (same points as oracle/gated_delta_ref.py).
+ * bf16 activations (same points as oracle/gated_delta_ref.py). The decode
+ * step's front-end and gated norm evaluate each such value in double and
+ * round it once; the recurrence itself runs in float32.
  */
 #include <math.h>
 #include <stdint.h>
@@ -29,13 +31,28 @@ static float bf16r(float x) {
 
 static float rnd(float x, int act_bf16) { return act_bf16 ? bf16r(x) : x; }
 
+/* One rounding of a double to the activation dtype: float32 by the cast;
+ * bfloat16 by rounding the double's own mantissa to 8 significant bits
+ * (nearest, ties to even), after which the cast to float is exact. The
+ * front-end below evaluates each value the reference rounds to bf16 in
+ * double and rounds it once, so a float32 error never decides a rounding
+ * boundary (the float64 restatement in gated_delta_ref.py does the same). */
+static float rnd_d(double x, int act_bf16) {
+    if (!act_bf16) return (float)x;
+    uint64_t u;
+    memcpy(&u, &x, 8);
+    u = (u + ((1ull << 44) - 1) + ((u >> 45) & 1)) & ~((1ull << 45) - 1);
+    memcpy(&x, &u, 8);
+    return (float)x;
+}
+
+static double sigmoid_d(double x) { return 1.0 / (1.0 + exp(-x)); }
+
 static float softplusf(float x) {
     /* logaddexp(x, 0) */
     float m = x > 0.f ? x : 0.f;
     return m + log1pf(expf(-fabsf(x)));
 }
-
-static float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
 
 /* Sequential scan over L tokens for B sequences (uniform length).
  * q,k: (B, L, Hk, Dk); v: (B, L, Hv, Dv); g, beta: (B, L, Hv);
@@ -102,13 +119,13 @@ void gdn_ref_decode_f32(const float *qkv, const float *conv_in, float *conv_out,
                 float *dst = part == 0 ? qv : part == 1 ? kv : vv;
                 for (int i = 0; i < n; ++i) {
                     const int c = base + i;
-                    float acc = 0.f;
+                    double acc = 0.0;
                     for (int j = 0; j < K; ++j) {
                         const float in = j < K - 1 ? rnd(cs[(size_t)j * C + c], act_bf16) : rnd(x[c], act_bf16);
-                        acc += rnd(conv_w[(size_t)c * K + j], act_bf16) * in;
+                        acc += (double)rnd(conv_w[(size_t)c * K + j], act_bf16) * in;
                     }
-                    acc = rnd(acc, act_bf16);
-                    dst[i] = rnd(acc * sigmoidf(acc), act_bf16);
+                    const double cv = rnd_d(acc, act_bf16);
+                    dst[i] = rnd_d(cv * sigmoid_d(cv), act_bf16);
                 }
             }
             /* conv state roll: written once per channel (by the first value head of a key head for q/k) */
@@ -123,15 +140,15 @@ void gdn_ref_decode_f32(const float *qkv, const float *conv_in, float *conv_out,
                         co[(size_t)j * C + c] = j + 1 < K - 1 ? rnd(cs[(size_t)(j + 1) * C + c], act_bf16) : rnd(x[c], act_bf16);
                 }
             }
-            float ssq = 0.f, ssk = 0.f;
-            for (int i = 0; i < Dk; ++i) { ssq += qv[i] * qv[i]; ssk += kv[i] * kv[i]; }
-            const float rq = 1.f / sqrtf(ssq / Dk + 1e-6f), rk = 1.f / sqrtf(ssk / Dk + 1e-6f);
+            double ssq = 0.0, ssk = 0.0;
+            for (int i = 0; i < Dk; ++i) { ssq += (double)qv[i] * qv[i]; ssk += (double)kv[i] * kv[i]; }
+            const double rq = 1.0 / sqrt(ssq / Dk + 1e-6), rk = 1.0 / sqrt(ssk / Dk + 1e-6);
             for (int i = 0; i < Dk; ++i) {
-                qv[i] = rnd(sq * rnd(qv[i] * rq, act_bf16), act_bf16);
-                kv[i] = rnd(sk * rnd(kv[i] * rk, act_bf16), act_bf16);
+                qv[i] = rnd(sq * rnd_d(qv[i] * rq, act_bf16), act_bf16);
+                kv[i] = rnd(sk * rnd_d(kv[i] * rk, act_bf16), act_bf16);
             }
             const float gt = expf(-expf(A_log[h]) * softplusf(a[(size_t)b * Hv + h] + dt_bias[h]));
-            const float bt = rnd(sigmoidf(bb[(size_t)b * Hv + h]), act_bf16);
+            const float bt = rnd_d(sigmoid_d(bb[(size_t)b * Hv + h]), act_bf16);
             const float *S0 = state_in + ((size_t)b * Hv + h) * Dv * Dk;
             float *S = state_out + ((size_t)b * Hv + h) * Dv * Dk;
             if (S != S0) memcpy(S, S0, sizeof(float) * Dv * Dk);
@@ -147,14 +164,14 @@ void gdn_ref_decode_f32(const float *qkv, const float *conv_in, float *conv_out,
             }
             float *ot = out + ((size_t)b * Hv + h) * Dv;
             if (z) {
-                float ss = 0.f;
-                for (int i = 0; i < Dv; ++i) ss += yv[i] * yv[i];
-                const float rr = 1.f / sqrtf(ss / Dv + eps);
+                double ss = 0.0;
+                for (int i = 0; i < Dv; ++i) ss += (double)yv[i] * yv[i];
+                const double rr = 1.0 / sqrt(ss / Dv + (double)eps);
                 const float *zt = z + ((size_t)b * Hv + h) * Dv;
                 for (int i = 0; i < Dv; ++i) {
-                    const float nrm = rnd(yv[i] * rr * norm_w[i], act_bf16);
-                    const float zz = zt[i];
-                    ot[i] = rnd(zz * sigmoidf(zz) * nrm, act_bf16);
+                    const double nrm = rnd_d(yv[i] * rr * norm_w[i], act_bf16);
+                    const double zz = zt[i];
+                    ot[i] = rnd_d(zz * sigmoid_d(zz) * nrm, act_bf16);
                 }
             } else {
                 for (int i = 0; i < Dv; ++i) ot[i] = yv[i];

@@ -48,14 +48,31 @@ def bf16_ulp(x) -> np.ndarray:
 
 
 def assert_bf16_out_close(got, ref, atol: float = 2e-2) -> None:
-    """The bf16 output bar: |got - ref| <= 2e-2, or one bf16 ulp of the value
-    where an ulp is larger (a value of magnitude >= 4 has an ulp >= 2^-5, so
-    a single rounding flip there exceeds 2e-2)."""
+    """The bf16 output bar: |got - ref| <= 2e-2, or two bf16 ulps of the
+    value where those are larger. A gated-norm output passes through three
+    bf16 roundings (y, the normalised value, the gated product), so a
+    one-ulp flip of y, which a different float32 summation order produces
+    near a rounding boundary, moves the output by up to two of its ulps;
+    from |value| >= 2.56 an ulp is >= 2^-6 and two exceed 2e-2."""
 
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
-    tol = np.maximum(atol, bf16_ulp(ref))
+    tol = np.maximum(atol, 2 * bf16_ulp(ref))
     err = np.abs(got - ref)
     bad = err > tol
-    assert not bad.any(), (f"{int(bad.sum())} of {bad.size} values outside max(2e-2, 1 ulp); "
+    assert not bad.any(), (f"{int(bad.sum())} of {bad.size} values outside max(2e-2, 2 ulp); "
+                           f"worst {err.max():.3g} at |ref| {np.abs(ref).flat[err.argmax()]:.3g}")
+
+
+def assert_within_bf16_ulps(got, ref, ulps: int = 1) -> None:
+    """|got - ref| <= `ulps` bf16 ulps of the larger magnitude: values that
+    the two sides round to bf16 from float32 and float64 arithmetic, where a
+    value within a float32 ulp of a tie may go either way."""
+
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    tol = ulps * bf16_ulp(np.maximum(np.abs(got), np.abs(ref)))
+    err = np.abs(got - ref)
+    bad = err > tol
+    assert not bad.any(), (f"{int(bad.sum())} of {bad.size} values beyond {ulps} bf16 ulp; "
                            f"worst {err.max():.3g} at |ref| {np.abs(ref).flat[err.argmax()]:.3g}")

@@ -109,6 +109,47 @@ def test_bf16_layer_matches_oracle_with_bf16_rounding(gpu):
     assert rel < 2e-2  # projections run in bf16 BLAS on one side, float64 on the other
 
 
+@pytest.mark.parametrize("seq_len", [1, 7, 130])
+def test_bf16_layer_core_matches_oracle_on_its_own_projections(gpu, seq_len):
+    """The layer between its projections at the north-star bars: the
+    oracle's core (conv, q/k scaling, gates, recurrence, gated norm, with
+    bf16 rounding) fed the GPU layer's own bf16 projection outputs, so the
+    two sides differ only in the path itself. State within 1e-3 relative,
+    conv state bit for bit, the core output and the layer output (out_proj
+    of the core output, float64 on the oracle's side) within the bf16 bar.
+    One token takes the fused decode kernel, 7 the sequential scan, 130 the
+    chunked prefill."""
+
+    from tests.helpers import assert_bf16_out_close, max_rel
+
+    dims = DIMS_PROD
+    layer, w = _build(3, dims, gpu, dtype=torch.bfloat16)
+    rng = np.random.default_rng(103 + seq_len)
+    x = torch.tensor(R.bf16_round(rng.standard_normal((seq_len, HIDDEN))), device=gpu).to(torch.bfloat16)
+    cache = layer.new_cache(torch.bfloat16)
+    conv0, ssm0 = (t.float().cpu().numpy() for t in cache.state())
+    got = layer(x, cache)
+    qkv, z, a, b = (t.float().cpu().numpy() for t in layer._project(x))
+    d = (dims.num_key_heads, dims.num_value_heads, dims.key_head_dim, dims.value_head_dim)
+    core, conv, ssm = R.linear_attention_core(qkv, z.reshape(seq_len, dims.num_value_heads, -1),
+                                              a, b, conv0, ssm0, w["conv1d_weight"], w["A_log"],
+                                              w["dt_bias"], w["norm_weight"], d, 1e-6, "bf16")
+    assert max_rel(cache.ssm_state.cpu().numpy(), ssm) < 1e-3
+    np.testing.assert_array_equal(cache.conv_state.float().cpu().numpy(), conv)
+    # the GPU's core output on the path the layer took (the fused decode
+    # kernel for one token, the unfused core otherwise)
+    proj = layer._project(x)
+    conv_z, ssm_z = torch.zeros_like(cache.conv_state)[None], torch.zeros_like(cache.ssm_state)[None]
+    if seq_len == 1:
+        core_gpu = layer._decode_fused(*proj, conv_z, ssm_z, in_place=False)[0].reshape(1, -1)
+    else:
+        core_gpu = layer.core(*proj, conv_z, ssm_z)[0]
+    assert_bf16_out_close(core_gpu.float().cpu().numpy(), core)
+    expected = R.bf16_round(core_gpu.float().cpu().numpy().astype(np.float64)
+                            @ R.bf16_round(w["out_proj"]).astype(np.float64).T)
+    assert_bf16_out_close(got.float().cpu().numpy(), expected)
+
+
 def test_decode_batch_matches_per_sequence_layer_calls(gpu):
     dims = DIMS_PROD
     layer, _ = _build(4, dims, gpu, dtype=torch.bfloat16)

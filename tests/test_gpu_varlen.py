@@ -78,6 +78,31 @@ def test_varlen_prefill_then_128_decode_steps(gpu):
     for i in range(N):
         assert max_rel(state_dev[i].cpu().numpy(), state_ref[i]) < STATE_REL, i
 
+    # the same continuation as the benchmark runs it: 128 fused decode steps
+    # (conv + roll, q/k scaling, gates, recurrence, gated norm) of the 16
+    # sequences from the prefill's states, state in place, conv state
+    # alternating between two buffers, against the C oracle's decode step
+    dims = gdn.LinearAttentionDims(Hk, Hv, d, d, 4)
+    conv_w, _, _, norm_w = layer_params(rng, (Hk, Hv, d, d))
+    conv_ref = R.bf16_round(rng.standard_normal((N, 3, dims.conv_dim))).astype(np.float32)
+    conv_dev, conv_spare = bf(conv_ref), torch.empty(N, 3, dims.conv_dim, dtype=torch.bfloat16,
+                                                      device=gpu)
+    state_dev, state_ref = s.clone(), s_ref.copy()
+    params = [f32(conv_w), f32(A_log), f32(dt_bias), f32(norm_w)]
+    for t in range(steps):
+        x_qkv, x_z, x_a, x_b = layer_inputs(rng, (Hk, Hv, d, d), L=1, act_bf16=True, B=N)
+        out, _, _ = gdn.fused_decode_step(bf(x_qkv[:, 0]), bf(x_z[:, 0]), bf(x_a[:, 0]),
+                                          bf(x_b[:, 0]), conv_dev, state_dev, *params, 1e-6, dims,
+                                          conv_out=conv_spare, state_out=state_dev)
+        conv_dev, conv_spare = conv_spare, conv_dev
+        out_ref, conv_ref, state_ref = cref.decode_step(
+            x_qkv[:, 0], conv_ref, conv_w, x_a[:, 0], x_b[:, 0], A_log, dt_bias, state_ref,
+            x_z[:, 0], norm_w, 1e-6, (Hk, Hv, d, d), True, state_out=state_ref)
+        assert_bf16_out_close(out.float().cpu().numpy(), out_ref)
+        if t % 32 == 31 or t == 0:
+            np.testing.assert_array_equal(conv_dev.float().cpu().numpy(), conv_ref)
+    assert max_rel(state_dev.cpu().numpy(), state_ref) < STATE_REL
+
 
 def test_layer_varlen_prefill_then_fused_decode(gpu):
     """Front-end + prefill for 4 packed prompts (one shorter than the conv

@@ -182,3 +182,34 @@ def test_pool_host_bookkeeping_flips_bits_and_sizes():
     assert pool.conv_half.tolist() == [0, 0, 1, 0, 1, 0] and pool.size.tolist() == [0, 2, 1, 0, 1, 0]
     pool.flip_host(np.array([1, 2]), tokens=-1)
     assert pool.conv_half.tolist() == [0, 1, 0, 0, 1, 0] and pool.size.tolist() == [0, 1, 0, 0, 1, 0]
+
+
+@pytest.mark.parametrize("bad", ["short", "long", "start", "end", "order", "uneven"])
+def test_malformed_run_offsets_raise_before_any_launch(bad, no_launch, monkeypatch):
+    """The front-end and the layer's core check cu_seqlens on the host
+    before their first launch: N+1 offsets for N conv states, from 0 to
+    the token count, non-decreasing; without offsets the tokens must split
+    evenly. (The device check is bypassed so the CPU tensors reach the
+    offset checks.)"""
+    from types import SimpleNamespace
+
+    from mlx_lean_moe_amd import linear_attention as LA
+
+    monkeypatch.setattr(LA, "_require_device", lambda *t: torch.device("cpu"))
+    dims = gdn.LinearAttentionDims(2, 4, 32, 32, 4)
+    T, N, C = 10, 3, dims.conv_dim
+    cu = {"short": [0, 4, 10], "long": [0, 2, 4, 6, 10], "start": [1, 2, 4, 10],
+          "end": [0, 2, 4, 11], "order": [0, 5, 4, 10], "uneven": None}[bad]
+    qkv = torch.zeros(T, C, dtype=torch.bfloat16)
+    conv = torch.zeros(N, 3, C, dtype=torch.bfloat16)
+    w = torch.zeros(C, 4)
+    with pytest.raises(ValueError, match="cu_seqlens|equal runs"):
+        LA.conv_frontend(qkv, conv, w, dims, None if cu is None else torch.tensor(cu, dtype=torch.int32))
+    if cu is None:
+        return
+    layer = SimpleNamespace(linear=dims, conv1d_weight=w)
+    z = torch.zeros(T, 4, 32, dtype=torch.bfloat16)
+    ab = torch.zeros(T, 4, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        LA.Qwen3_5LinearAttention.core(layer, qkv, z, ab, ab, conv, torch.zeros(N, 4, 32, 32),
+                                       cu_seqlens=cu)

@@ -81,7 +81,7 @@ def test_index_and_reads_match_the_safetensors_loader(tmp_path):
         for name, loc in index.items():
             got, want = reader.read_tensor(name), lib[name]
             assert tuple(got.shape) == tuple(want.shape) == loc.shape
-            if loc.dtype == "BF16" and W.keeps_stored_width(name):
+            if loc.dtype == "BF16" and W.is_quant_metadata(name):
                 assert got.dtype == torch.bfloat16
                 assert torch.equal(got.view(torch.int16), want.view(torch.int16))
             elif loc.dtype == "BF16":
@@ -104,34 +104,47 @@ def test_bf16_widening_of_special_values():
         list(struct.unpack("<7h", raw))
     with pytest.raises(ValueError, match="unsupported safetensors dtype"):
         W.decode_tensor(b"\0\0", "F8_E4M3", (2,))
-    assert W.keeps_stored_width("a.b.scales") and W.keeps_stored_width("x.biases")
-    assert not W.keeps_stored_width("a.norm.weight") and not W.keeps_stored_width("a.A_log")
+    assert W.is_quant_metadata("a.b.scales") and W.is_quant_metadata("x.biases")
+    assert not W.is_quant_metadata("a.norm.weight") and not W.is_quant_metadata("a.A_log")
 
 
 def _loc(shape, dtype="U32"):
-    return W.TensorLocation("s", dtype, tuple(shape), 0, 0)
+    return W.TensorSpan("s", dtype, tuple(shape), 0, 0)
 
 
 def test_linear_layout_rules():
+    """The reference loader's conditions (expert_loader.py:95-141): a
+    missing weight is a KeyError; biases without scales, an affine scheme
+    without biases, biases not shaped like the scales, weight and scale rows
+    that differ, and a packed width other than groups * group_size * bits /
+    32 are each a LayoutError (a ValueError); several at once are all
+    named."""
+
     q4 = QuantScheme(4, 64)
+    check = W.projection_is_quantized
     ok = {"p.weight": _loc((8, 16)), "p.scales": _loc((8, 2), "BF16"), "p.biases": _loc((8, 2), "BF16")}
-    assert W.validate_linear_layout(ok, "p", q4) is True
-    assert W.validate_linear_layout({"p.weight": _loc((8, 128), "BF16")}, "p", q4) is False
-    with pytest.raises(KeyError, match="no weight tensor"):
-        W.validate_linear_layout({}, "p", q4)
-    with pytest.raises(ValueError, match="biases but no scales"):
-        W.validate_linear_layout({"p.weight": ok["p.weight"], "p.biases": ok["p.biases"]}, "p", q4)
-    with pytest.raises(ValueError, match="has no biases"):
-        W.validate_linear_layout({"p.weight": ok["p.weight"], "p.scales": ok["p.scales"]}, "p", q4)
-    with pytest.raises(ValueError, match="incompatible with scales"):
-        W.validate_linear_layout({**ok, "p.scales": _loc((9, 2), "BF16"), "p.biases": _loc((9, 2), "BF16")}, "p", q4)
-    with pytest.raises(ValueError, match="does not match scales"):
-        W.validate_linear_layout({**ok, "p.biases": _loc((8, 3), "BF16")}, "p", q4)
-    with pytest.raises(ValueError, match="expected packed width 32"):
-        W.validate_linear_layout(ok, "p", QuantScheme(8, 64))
+    assert check(ok, "p", q4) is True
+    assert check({"p.weight": _loc((8, 128), "BF16")}, "p", q4) is False
+    with pytest.raises(KeyError, match="p.weight"):
+        check({}, "p", q4)
+    cases = [
+        ({"p.weight": ok["p.weight"], "p.biases": ok["p.biases"]}, q4, "without the scales"),
+        ({"p.weight": ok["p.weight"], "p.scales": ok["p.scales"]}, q4, "none are stored"),
+        ({**ok, "p.scales": _loc((9, 2), "BF16"), "p.biases": _loc((9, 2), "BF16")}, q4,
+         "leading dimensions"),
+        ({**ok, "p.biases": _loc((8, 3), "BF16")}, q4, "differ in shape"),
+        (ok, QuantScheme(8, 64), "pack into 32 words a row"),
+    ]
+    for index, scheme, msg in cases:
+        with pytest.raises(W.LayoutError, match=msg):
+            check(index, "p", scheme)
+        assert issubclass(W.LayoutError, ValueError)
+    # two problems at once: both reported
+    with pytest.raises(W.LayoutError, match="differ in shape.*pack into 32"):
+        check({**ok, "p.biases": _loc((8, 3), "BF16")}, "p", QuantScheme(8, 64))
     # modes without biases (mxfp4) need none
     mx = {"p.weight": _loc((8, 8)), "p.scales": _loc((8, 2), "U8")}
-    assert W.validate_linear_layout(mx, "p", QuantScheme(4, 32, "mxfp4")) is True
+    assert check(mx, "p", QuantScheme(4, 32, "mxfp4")) is True
 
 
 def test_hf_config_shapes_and_quantization():
@@ -157,10 +170,10 @@ def test_hf_config_shapes_and_quantization():
 def test_read_linear_and_truncated_shard(tmp_path):
     write_checkpoint(tmp_path, dense_b=True)
     with W.CheckpointReader(tmp_path) as reader:
-        qkv = W.read_linear(reader, f"{PREFIX}.in_proj_qkv", QuantScheme(4, 32))
+        qkv = W.read_projection(reader, f"{PREFIX}.in_proj_qkv", QuantScheme(4, 32))
         assert qkv.quant == QuantScheme(4, 32) and set(qkv.tensors) == {"weight", "scales", "biases"}
         assert qkv.tensors["scales"].dtype == torch.bfloat16
-        dense = W.read_linear(reader, f"{PREFIX}.in_proj_b", QuantScheme(4, 32))
+        dense = W.read_projection(reader, f"{PREFIX}.in_proj_b", QuantScheme(4, 32))
         assert dense.quant is None and dense.tensors.dtype == torch.float32
     shard = tmp_path / "model-00002-of-00002.safetensors"
     shard.write_bytes(shard.read_bytes()[:-8])
