@@ -50,7 +50,7 @@ typedef enum {
  * adds input row strides and gdn_pool_advance, 6 the quantized matmul's
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
  * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride,
- * 10 the gated norm's z layout). */
+ * 10 the gated norm's z layout, 11 gdn_quantized_matmul_noalloc). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -263,6 +263,28 @@ int gdn_quantized_matmul(const void *x, int x_dtype, const void *w, const void *
                          const void *biases, int sb_dtype, void *y, int y_dtype,
                          const void *residual, int M, int N, int K, int bits, int group_size,
                          void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * gdn_quantized_matmul_noalloc - gdn_quantized_matmul that allocates nothing
+ * and takes no workspace: a call that splits K keeps its float32 partial
+ * products in the library's own device scratch (a static 4 MiB array per
+ * GPU, held until the process ends; every call the decode kernel takes
+ * needs at most that), so it splits exactly as gdn_quantized_matmul does
+ * with a full workspace and gives the same bits. A call needing more
+ * returns GDN_EINVAL. The first call on a GPU looks up that GPU's copy of
+ * the array (hipGetSymbolAddress); no call allocates or frees memory. Calls
+ * that overlap on one GPU share its scratch and race: the caller orders
+ * them (one stream, or events). Arguments and results as
+ * gdn_quantized_matmul without workspace and workspace_bytes.
+ * No counterpart in the reference (MLX's kernels allocate their own
+ * scratch): for callers that cannot allocate device memory, such as code
+ * under HIP graph capture, tight serving loops and harnesses that forbid
+ * hipMalloc.
+ */
+int gdn_quantized_matmul_noalloc(const void *x, int x_dtype, const void *w, const void *scales,
+                                 const void *biases, int sb_dtype, void *y, int y_dtype,
+                                 const void *residual, int M, int N, int K, int bits, int group_size,
+                                 void *stream);
 
 /*
  * gdn_quantized_matmul_workspace_size - workspace bytes gdn_quantized_matmul

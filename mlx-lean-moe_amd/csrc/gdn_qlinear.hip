@@ -15,6 +15,7 @@
 // weights mx.dequantize yields) next to a BM x 64 tile of x; fp32
 // accumulation. Loads of step s + 1 are issued before step s's MFMAs.
 // gdn_dequantize: the dense weights, for dtypes the MFMA kernel does not take.
+#include <mutex>
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -1082,10 +1083,12 @@ extern "C" int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype
     return decode_workspace_bytes(x_f32, sb_dtype, M, N, K, bits, group_size);
 }
 
-extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, const void* scales,
-                                    const void* biases, int sb_dtype, void* y, int y_dtype,
-                                    const void* residual, int M, int N, int K, int bits, int group_size,
-                                    void* workspace, int64_t workspace_bytes, void* stream) {
+namespace gdn {
+namespace {
+
+int quantized_matmul(const void* x, int x_dtype, const void* w, const void* scales, const void* biases,
+                     int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N, int K, int bits,
+                     int group_size, void* workspace, int64_t workspace_bytes, void* stream) {
     if (int rc = check_quant_args("gdn_quantized_matmul", w, scales, biases, sb_dtype, N, K, bits,
                                   group_size))
         return rc;
@@ -1121,6 +1124,76 @@ extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, c
         return fail(GDN_EUNSUPPORTED, "gdn_quantized_matmul: float32 x needs a shape the decode kernel takes");
     if (bits == 4) return dispatch_sb<4>(x, wp, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, s);
     return dispatch_sb<8>(x, wp, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, s);
+}
+
+// The split-K partial blocks of gdn_quantized_matmul_noalloc live in this
+// file-scope device array, one copy per GPU, held until the process ends.
+// 4 MiB is the most any call takes: a split call has at most kCUs
+// workgroups, so splits * N <= kCUs * 64 columns, and M <= 64 rows of
+// float32, i.e. 256 * 64 * 64 * 4 bytes. Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): it passes the per-device address from hipGetSymbolAddress.
+constexpr int64_t kScratchBytes = int64_t(kCUs) * 64 * 64 * 4;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the device that runs `stream`, looked up
+// once per device with that device current.
+int scratch_for(hipStream_t stream, void** ptr) {
+    int dev = -1;
+    hipError_t err = hipStreamGetDevice(stream, &dev);
+    if (err != hipSuccess) return fail(int(err), "gdn_quantized_matmul_noalloc: hipStreamGetDevice: %s",
+                                       hipGetErrorString(err));
+    GDN_REQUIRE(dev >= 0 && dev < kMaxDevices, "gdn_quantized_matmul_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        int current = -1;
+        err = hipGetDevice(&current);
+        if (err == hipSuccess && current != dev) err = hipSetDevice(dev);
+        void* p = nullptr;
+        if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (current >= 0 && current != dev) {
+            const hipError_t back = hipSetDevice(current);
+            if (err == hipSuccess) err = back;
+        }
+        if (err != hipSuccess || !p)
+            return fail(err != hipSuccess ? int(err) : GDN_EINVAL,
+                        "gdn_quantized_matmul_noalloc: scratch address on device %d: %s", dev,
+                        hipGetErrorString(err));
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_quantized_matmul(const void* x, int x_dtype, const void* w, const void* scales,
+                                    const void* biases, int sb_dtype, void* y, int y_dtype,
+                                    const void* residual, int M, int N, int K, int bits, int group_size,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+    return quantized_matmul(x, x_dtype, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, bits,
+                            group_size, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gdn_quantized_matmul_noalloc(const void* x, int x_dtype, const void* w, const void* scales,
+                                            const void* biases, int sb_dtype, void* y, int y_dtype,
+                                            const void* residual, int M, int N, int K, int bits,
+                                            int group_size, void* stream) {
+    const int64_t need = gdn_quantized_matmul_workspace_size(x_dtype, sb_dtype, M, N, K, bits, group_size);
+    if (need > kScratchBytes)
+        return fail(GDN_EINVAL,
+                    "gdn_quantized_matmul_noalloc: this call needs %lld bytes of split-K scratch; the "
+                    "library holds %lld (use gdn_quantized_matmul with a workspace)",
+                    static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+    void* ptr = nullptr;
+    if (int rc = scratch_for(as_stream(stream), &ptr)) return rc;
+    return quantized_matmul(x, x_dtype, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, bits,
+                            group_size, need > 0 ? ptr : nullptr, need, stream);
 }
 
 extern "C" int gdn_dequantize(const void* w, const void* scales, const void* biases, int sb_dtype,

@@ -1,0 +1,97 @@
+"""gdn_quantized_matmul_noalloc, the quantized matmul that allocates
+nothing: its split-K partials live in the library's static per-GPU scratch.
+On the GPU, through the C ABI, it gives the same bits as
+gdn_quantized_matmul with a full caller workspace, on two calls in a row
+(the second smaller, over the scratch the first one left behind); on the
+host, every decode-kernel shape needs at most the scratch it holds."""
+
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_lean_moe_amd import _lib
+
+SCRATCH_BYTES = 4 << 20
+
+
+def test_every_decode_shape_fits_the_scratch():
+    """The workspace the full split takes, over decode-kernel shapes (rows
+    1-64, the layer's projection widths and depths, both bit widths and all
+    group sizes), never exceeds the 4 MiB scratch; the out_proj shape at 64
+    rows takes all of it."""
+
+    lib = _lib.load()
+    worst = 0
+    for M, N, K, bits, gs, sb in itertools.product(
+            (1, 2, 16, 17, 32, 33, 64), (64, 256, 1024, 2048, 4096, 8192, 12352),
+            (512, 1024, 2048, 4096, 8192), (4, 8), (32, 64, 128), (_lib.GDN_BF16, _lib.GDN_F32)):
+        for xd in (_lib.GDN_BF16, _lib.GDN_F32):
+            need = lib.gdn_quantized_matmul_workspace_size(xd, sb, M, N, K, bits, gs)
+            assert 0 <= need <= SCRATCH_BYTES, (M, N, K, bits, gs, sb, xd, need)
+            worst = max(worst, need)
+    assert worst == SCRATCH_BYTES
+    assert lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, 64, 2048, 4096,
+                                                   4, 64) == SCRATCH_BYTES
+
+
+def _case(dev, M, N, K, bits, gs, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    words = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K * bits // 32), generator=g, device=dev,
+                          dtype=torch.int32)
+    scales = (torch.rand(N, K // gs, generator=g, device=dev) * 0.004 + 0.001).to(torch.bfloat16)
+    biases = ((torch.rand(N, K // gs, generator=g, device=dev) - 0.5) * 0.05).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    residual = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
+    return x, words, scales, biases, residual
+
+
+def _run(lib, fn, dev, x, words, scales, biases, residual, M, N, K, bits, gs, workspace=None):
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    args = [x.data_ptr(), _lib.GDN_BF16, words.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+            _lib.GDN_BF16, y.data_ptr(), _lib.GDN_BF16,
+            None if residual is None else residual.data_ptr(), M, N, K, bits, gs]
+    if fn == "gdn_quantized_matmul":
+        args += [None if workspace is None else workspace.data_ptr(),
+                 0 if workspace is None else workspace.numel()]
+    rc = getattr(lib, fn)(*args, stream)
+    assert rc == 0, lib.gdn_last_error().decode()
+    return y
+
+
+@pytest.mark.gpu
+def test_noalloc_matches_the_workspace_entry_point_on_two_calls(gpu):
+    """Two calls in a row, each against gdn_quantized_matmul with a full
+    workspace (same split, so the same bits): the layer's out_proj at 64
+    rows (8 splits, the whole scratch) with a residual, then a smaller call
+    (16 rows of a 1024 x 2048 projection, fewer and smaller partial
+    blocks) that reads none of what the first left in the scratch; and a
+    one-row call (no split, no scratch)."""
+
+    lib = _lib.load()
+    shapes = [(64, 2048, 4096, 4, 64, True), (16, 1024, 2048, 4, 64, False),
+              (1, 2048, 4096, 8, 32, False)]
+    for i, (M, N, K, bits, gs, with_res) in enumerate(shapes):
+        print(f"noalloc case {i}: M={M} N={N} K={K} bits={bits} group={gs}", flush=True)
+        x, words, scales, biases, residual = _case(gpu, M, N, K, bits, gs, seed=40 + i)
+        residual = residual if with_res else None
+        need = lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, M, N, K, bits, gs)
+        assert need <= SCRATCH_BYTES
+        if i == 0:
+            assert need == SCRATCH_BYTES
+        ws = torch.empty(max(need, 16), dtype=torch.uint8, device=gpu)
+        ref = _run(lib, "gdn_quantized_matmul", gpu, x, words, scales, biases, residual, M, N, K,
+                   bits, gs, ws if need else None)
+        got = _run(lib, "gdn_quantized_matmul_noalloc", gpu, x, words, scales, biases, residual, M,
+                   N, K, bits, gs)
+        torch.cuda.synchronize()
+        assert not torch.isnan(ref.float()).any()
+        assert torch.equal(got, ref), i
+    # an invalid call is refused before any launch
+    rc = lib.gdn_quantized_matmul_noalloc(None, _lib.GDN_BF16, None, None, None, _lib.GDN_BF16, None,
+                                          _lib.GDN_BF16, None, 4, 64, 64, 4, 64, None)
+    assert rc == _lib.GDN_EINVAL
