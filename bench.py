@@ -419,14 +419,15 @@ def prefill_flops(T, Hv, d=128, chunk=64):
 
 class PrefillWorkload:
     """Synthetic chunked-prefill inputs resident in HBM: N runs of L tokens
-    (or packed runs of the given lengths, through cu_seqlens), bf16 q/k/v
-    (q, k L2-normalised), bf16 a/b, initial state zero (or ~N(0, 0.05) with
-    packed runs); y in bf16."""
+    (or packed runs of the given lengths, through cu_seqlens), q/k/v and a/b
+    in `dtype` (bf16, or float32 as the reference's layers carry them; q, k
+    L2-normalised), initial state zero (or ~N(0, 0.05) with packed runs); y
+    in bf16."""
 
-    def __init__(self, dev, N, L, Hk, Hv, seed=0, lens=None):
+    def __init__(self, dev, N, L, Hk, Hv, seed=0, lens=None, dtype=torch.bfloat16):
         d = 128
         g = torch.Generator(device=dev).manual_seed(seed)
-        bf = torch.bfloat16
+        bf = dtype
         if lens is not None:
             N = len(lens)
             cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
@@ -447,15 +448,16 @@ class PrefillWorkload:
         self.dt_bias = torch.rand(Hv, generator=g, device=dev) * 2 - 1
         self.state_out = torch.empty(N, Hv, d, d, device=dev)
         self.state_in = (randn(N, Hv, d, d) * 0.05 if lens is not None else None)
-        self.y = torch.empty(T, Hv, d, dtype=bf, device=dev)
+        self.y = torch.empty(T, Hv, d, dtype=torch.bfloat16, device=dev)
         nbytes = gated_delta.prefill_workspace_bytes(N, T, Hk, Hv, d, d)
         self.ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         self.T, self.flops = T, prefill_flops(T, Hv)
         from mlx_lean_moe_amd import _lib
 
         self._fn = _lib.load().gdn_prefill_chunked
-        self._args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.a.data_ptr(),
-                      self.b.data_ptr(), _lib.GDN_BF16, Hv, self.A_log.data_ptr(),
+        self._args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                      _lib.dtype_code(dtype), self.a.data_ptr(),
+                      self.b.data_ptr(), _lib.dtype_code(dtype), Hv, self.A_log.data_ptr(),
                       self.dt_bias.data_ptr(), 0,
                       None if self.state_in is None else self.state_in.data_ptr(),
                       self.state_out.data_ptr(), self.y.data_ptr(), _lib.GDN_BF16,
@@ -535,12 +537,15 @@ def bench_qlinear(dev, M, steps, warmup, rotate=True, layer_path=False):
 VARLEN_LENS = np.random.default_rng(0).integers(128, 8193, 16)  # 16 runs, 67,128 tokens
 
 
-def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None):
-    w = PrefillWorkload(dev, N, L, Hk, Hv, lens=lens)
+def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None, dtype=torch.bfloat16,
+                  compare_scan=False):
+    w = PrefillWorkload(dev, N, L, Hk, Hv, lens=lens, dtype=dtype)
     total_ms, isolated_ms = time_steps(w.step, steps, warmup)
     call_ms = total_ms / steps  # one gdn_prefill_chunked call per step
     tflops = w.flops / (call_ms * 1e-3) / 1e12
     extra = {} if lens is None else {"continuation": bench_continuation(dev, w, Hk, Hv)}
+    if compare_scan:
+        extra["sequential_scan_us"] = scan_call_us(w, Hk, Hv, max(steps // 4, 2))
     return {
         **extra,
         "tokens_per_s": w.T * steps / (total_ms * 1e-3),
@@ -551,6 +556,27 @@ def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None):
         "tflops": tflops,
         "mfma_frac": tflops / BF16_PEAK_TFLOPS,
     }
+
+
+def scan_call_us(w, Hk, Hv, steps):
+    """The same workload through the sequential register-resident scan
+    (gdn_scan, the reference's Metal-kernel form), gates precomputed: the
+    path float32 activations took before the chunked prefill took them."""
+
+    d = 128
+    g, beta = gated_delta._gates(w.a, w.b, w.A_log, w.dt_bias)
+    state_in = (w.state_in if w.state_in is not None
+                else torch.zeros_like(w.state_out))
+    y = torch.empty(w.T, Hv, d, dtype=torch.float32, device=w.q.device)
+    cu = w.cu
+    N = state_in.shape[0]
+
+    def step(_):
+        gated_delta._launch_scan("gdn_scan", w.q, w.k, w.v, g, beta, state_in, w.state_out, y,
+                                 cu, N, w.T, Hk, Hv, d, d, w.q.device)
+
+    total_ms, _ = time_steps(step, steps, 1)
+    return total_ms / steps * 1e3
 
 
 def bench_continuation(dev, w, Hk, Hv, steps=128, warmup=8):
@@ -762,6 +788,8 @@ def bench_also(dev, cpu=True):
     sm = bench_decode(dev, 64, 16, 32, False, steps=64, warmup=8)
     pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
     pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
+    p32 = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3, dtype=torch.float32,
+                        compare_scan=True)
     sl = bench_decode_slots(dev, 64, 16, 32, steps=64, warmup=8)
     ld = bench_layer_decode(dev, 64, steps=64, warmup=8)
     lp = bench_layer_prefill(dev, 4096, steps=20, warmup=3)
@@ -775,6 +803,12 @@ def bench_also(dev, cpu=True):
             "tokens_per_s": pf["tokens_per_s"], "call_us": pf["call_us"],
             "roofline": prefill_roofline(pf),
             **({"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)} if cpu else {})},
+        "prefill_f32": {
+            "workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64, float32 q/k/v/a/b "
+                        "(bf16 hi + lo on MFMA)",
+            "tokens_per_s": p32["tokens_per_s"], "call_us": p32["call_us"],
+            "tflops": p32["tflops"], "mfma_frac": p32["mfma_frac"],
+            "sequential_scan_us": p32["sequential_scan_us"]},
         "prefill_varlen": {
             "workload": "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 "
                         "Hv=32, nonzero initial states",
@@ -803,7 +837,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode_large", "decode_b64", "decode_slots", "layer_decode",
-                             "layer_prefill",
+                             "layer_prefill", "prefill_f32",
                              "prefill", "prefill_varlen", "qlinear", "copy"])
     ap.add_argument("--layers", type=int, default=1,
                     help="layer_decode: also time this many layers chained in one graph")
@@ -942,10 +976,12 @@ def main(argv=None):
                 "layer_path_mfma_frac": pre["layer_path_tflops"] / BF16_PEAK_TFLOPS}}}))
         return 0
 
-    if args.workload in ("prefill", "prefill_varlen"):
+    if args.workload in ("prefill", "prefill_varlen", "prefill_f32"):
         varlen = args.workload == "prefill_varlen"
+        f32 = args.workload == "prefill_f32"
         r = bench_prefill(dev, 1, 4096, 16, 32, args.steps, args.warmup,
-                          lens=VARLEN_LENS if varlen else None)
+                          lens=VARLEN_LENS if varlen else None,
+                          dtype=torch.float32 if f32 else torch.bfloat16, compare_scan=f32)
         print(json.dumps({"metric": METRIC, "value": r["tokens_per_s"], "unit": "tokens/s",
                           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": r["ms_per_step"], "higher_is_better": True,
@@ -954,12 +990,14 @@ def main(argv=None):
                           "config": {"workload": (
                               "packed prefill of 16 runs U[128, 8192] (67,128 tokens) Hk=16 Hv=32 "
                               "d=128 chunk 64" if varlen else
-                              "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64")},
+                              "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64" +
+                              (", float32 q/k/v/a/b" if f32 else ""))},
                           "roofline": ({**prefill_roofline(r), "traffic": None} if varlen
                                        else prefill_roofline(r)),
-                          **({} if args.no_cpu_baseline or varlen else
+                          **({} if args.no_cpu_baseline or varlen or f32 else
                              {"cpu_baseline": cpu_baseline_prefill(16, 32, budget_s=10.0)}),
-                          **({"continuation": r["continuation"]} if varlen else {})}))
+                          **({"continuation": r["continuation"]} if varlen else {}),
+                          **({"sequential_scan_us": r["sequential_scan_us"]} if f32 else {})}))
         return 0
 
     raise SystemExit(f"workload {args.workload} is not available in this build")

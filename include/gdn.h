@@ -50,7 +50,8 @@ typedef enum {
  * adds input row strides and gdn_pool_advance, 6 the quantized matmul's
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
  * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride,
- * 10 the gated norm's z layout, 11 gdn_quantized_matmul_noalloc). */
+ * 10 the gated norm's z layout, 11 gdn_quantized_matmul_noalloc, 12 the
+ * prefill's float32 q/k/v). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -182,7 +183,9 @@ int gdn_pool_advance(const int32_t *slots, int B, int32_t *conv_half, int pool, 
 /*
  * gdn_prefill_chunked - chunked (WY/UT, 64-token chunks) prefill on bf16
  * MFMA with float32 accumulation, for N packed runs.
- *   q, k: (T_total, Hk, Dk) bf16;  v: (T_total, Hv, Dv) bf16
+ *   q, k: (T_total, Hk, Dk);  v: (T_total, Hv, Dv), all in qkv_dtype:
+ *         GDN_BF16 (used as they are) or GDN_F32 (each value split into a
+ *         bf16 high part and a bf16 residual, the residual products added)
  *   gate_mode 0: ga = a, gb = b, both (T_total, Hv) in gb_dtype, with A_log and
  *                dt_bias (Hv) float32 (gates computed in-kernel, beta held in gb_dtype)
  *   gate_mode 1: ga = g (T_total, Hv) float32, gb = beta (T_total, Hv) gb_dtype
@@ -191,7 +194,8 @@ int gdn_pool_advance(const int32_t *slots, int B, int32_t *conv_half, int pool, 
  *                projection output
  *   state_in: (N, Hv, Dv, Dk) float32 or NULL (zero state); state_out: (N, Hv, Dv, Dk),
  *             not aliasing state_in
- *   q, k, states and workspace 16-byte aligned, v 8-byte aligned
+ *   q, k, states and workspace 16-byte aligned, v 8-byte aligned (16 with
+ *   float32 input)
  *   y: (T_total, Hv, Dv) y_dtype
  *   workspace: device scratch of gdn_prefill_workspace_size(...) bytes
  * Specialised for Dk = Dv = 128. Equal, up to rounding, to gdn_scan on the
@@ -199,7 +203,7 @@ int gdn_pool_advance(const int32_t *slots, int B, int32_t *conv_half, int pool, 
  * sequential scan (_gated_delta_metal.py:64-87).
  */
 int64_t gdn_prefill_workspace_size(int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv);
-int gdn_prefill_chunked(const void *q, const void *k, const void *v, const void *ga,
+int gdn_prefill_chunked(const void *q, const void *k, const void *v, int qkv_dtype, const void *ga,
                         const void *gb, int gb_dtype, int64_t gate_stride, const float *A_log,
                         const float *dt_bias, int gate_mode, const float *state_in,
                         float *state_out, void *y, int y_dtype, const int32_t *cu_seqlens,

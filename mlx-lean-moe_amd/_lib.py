@@ -16,7 +16,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgdn.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 GDN_F32, GDN_BF16, GDN_F16 = 0, 1, 2
 GDN_EINVAL, GDN_EUNSUPPORTED = -1, -2
@@ -52,7 +52,7 @@ _SIGNATURES = {
                                  _c_i64_p, _c_void_p, _c_void_p]),
     "gdn_pool_advance": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_void_p]),
     "gdn_prefill_workspace_size": (_c_i64, [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int]),
-    "gdn_prefill_chunked": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+    "gdn_prefill_chunked": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                      _c_int, _c_i64, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                      _c_void_p, _c_int, _c_void_p, _c_int, _c_i64, _c_int,
                                      _c_int, _c_int, _c_int, _c_void_p, _c_i64, _c_void_p]),

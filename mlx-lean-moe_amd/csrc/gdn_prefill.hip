@@ -73,6 +73,20 @@ GDN_DEV uint2 pack4(const uint16_t (&x)[4]) {
 
 GDN_DEV bf16x8 load8(const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// Eight consecutive float32 inputs as bf16 high parts and bf16 residuals.
+GDN_DEV void load_split8(const float* p, u16x8& hi, u16x8& lo) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint16_t h, o;
+        split_bf16(x[j], h, o);
+        hi[j] = h;
+        lo[j] = o;
+    }
+}
+
 GDN_DEV bf16x8 zero8() {
     bf16x8 z;
 #pragma unroll
@@ -233,17 +247,24 @@ GDN_DEV void offdiag_inverse(float* As, float* Ts, int w, int l) {
 // round-robin over the 8 XCDs, so the r = Hv/Hk value heads of one
 // (chunk, key head) take ids 8 apart: same XCD, dispatched together, so all
 // but the first read that chunk's K and Q from the XCD's L2.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_chunk_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const void* __restrict__ ga,
+//
+// kF32: q and k are float32, entering the MFMAs as bf16 high parts plus
+// residuals (hi.hi + hi.lo + lo.hi), with two more LDS tiles for the
+// residuals; otherwise bf16, used as they are.
+template <bool kF32>
+GDN_DEV void prefill_chunk_body(
+    const void* __restrict__ q_in, const void* __restrict__ k_in, const void* __restrict__ ga,
     const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
     int Hk, int Hv) {
     // K/Q tiles first; once K K^T and K Q^T are in registers the same bytes
     // hold the A and T matrices.
-    __shared__ __attribute__((aligned(16))) char smem[2 * kChunk * kKS * 2];
+    __shared__ __attribute__((aligned(16))) char smem[(kF32 ? 4 : 2) * kChunk * kKS * 2];
     __shared__ __attribute__((aligned(16))) float l2_sh[kChunk], beta_sh[kChunk];
     uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
     uint16_t* Qs = Ks + kChunk * kKS;
+    uint16_t* Ks_lo = Qs + kChunk * kKS;  // kF32 only
+    uint16_t* Qs_lo = Ks_lo + kChunk * kKS;
     float* As = reinterpret_cast<float*>(smem);
     float* Ts = As + kChunk * kFS;
 
@@ -258,14 +279,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 
     // K and Q of the chunk: every load issued before the first LDS store
     // (rows past the run are read clamped and stored as zero).
-    u16x8 kv[4], qv[4];
+    u16x8 kv[4], qv[4], kvl[4], qvl[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int row = (tid + 256 * it) >> 4, seg = tid & 15;
         const int rc = row < pos.len ? row : pos.len - 1;
         const int64_t off = ((pos.t0 + rc) * Hk + hk) * kHD + seg * 8;
-        kv[it] = *reinterpret_cast<const u16x8*>(k + off);
-        qv[it] = *reinterpret_cast<const u16x8*>(q + off);
+        if constexpr (kF32) {
+            load_split8(static_cast<const float*>(k_in) + off, kv[it], kvl[it]);
+            load_split8(static_cast<const float*>(q_in) + off, qv[it], qvl[it]);
+        } else {
+            kv[it] = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(k_in) + off);
+            qv[it] = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(q_in) + off);
+        }
     }
     // Gates (wave 0, lane = token): l2 = inclusive prefix sum of log2 g
     // (exp2 of differences gives the decays).
@@ -300,6 +326,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
         *reinterpret_cast<u16x8*>(Ks + row * kKS + seg * 8) = row < pos.len ? kv[it] : z;
         *reinterpret_cast<u16x8*>(Qs + row * kKS + seg * 8) = row < pos.len ? qv[it] : z;
+        if constexpr (kF32) {
+            *reinterpret_cast<u16x8*>(Ks_lo + row * kKS + seg * 8) = row < pos.len ? kvl[it] : z;
+            *reinterpret_cast<u16x8*>(Qs_lo + row * kKS + seg * 8) = row < pos.len ? qvl[it] : z;
+        }
     }
     __syncthreads();
 
@@ -317,6 +347,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         for (int jt = 0; jt < 4; ++jt) {
             kk[jt] = mfma16(ak, load8(Ks + (16 * jt + lr) * kKS + 32 * s + lg8), kk[jt]);
             kq[jt] = mfma16(ak, load8(Qs + (16 * jt + lr) * kKS + 32 * s + lg8), kq[jt]);
+        }
+    }
+    if constexpr (kF32) {  // the residual products, summed apart and added once
+        f32x4 kk2[4], kq2[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) kk2[jt] = kq2[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kHD / 32; ++s) {
+            const bf16x8 ak = load8(Ks + (16 * w + lr) * kKS + 32 * s + lg8);
+            const bf16x8 akl = load8(Ks_lo + (16 * w + lr) * kKS + 32 * s + lg8);
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const int ro = (16 * jt + lr) * kKS + 32 * s + lg8;
+                kk2[jt] = mfma16(ak, load8(Ks_lo + ro), kk2[jt]);
+                kk2[jt] = mfma16(akl, load8(Ks + ro), kk2[jt]);
+                kq2[jt] = mfma16(ak, load8(Qs_lo + ro), kq2[jt]);
+                kq2[jt] = mfma16(akl, load8(Qs + ro), kq2[jt]);
+            }
+        }
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            kk[jt] += kk2[jt];
+            kq[jt] += kq2[jt];
         }
     }
     __syncthreads();  // K/Q tiles are dead from here on
@@ -361,6 +414,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
                     reinterpret_cast<uint16_t*>(rec + kRecTbLo), beta_sh, tid, 256);
 }
 
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_chunk_kernel(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ ga,
+    const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
+    int Hk, int Hv) {
+    prefill_chunk_body<false>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
+                              records, Hk, Hv);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_chunk_f32_kernel(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ ga,
+    const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
+    int Hk, int Hv) {
+    prefill_chunk_body<true>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
+                             records, Hk, Hv);
+}
+
 // ---------------------------------------------------------------------------
 // state pass
 // ---------------------------------------------------------------------------
@@ -393,6 +464,8 @@ struct StagedOperands {
     bf16x8 tbh[2], tbl[2];  // Tb fragments (2w + s) (hi, lo): row 16w + l%16, tokens 32s + 8(l/16) .. +7
     u32x2 v;                // V (bf16) at token 16w + l/4, dv dv0 + 4(l%4) .. +3
     f32x4 e;                // words 32w + 4(l%8) .. +3 of the record's [exp(l) | exp(l_C - l)]
+    bf16x8 kal[4], qal[4];  // float32 input only: the residuals of ka, qa
+    u32x2 vl;               // and of v
 };
 
 // P fragments of output wave w (used from registers).
@@ -402,9 +475,9 @@ struct OutputOperands {
 
 // Per-run constants of a state-pass workgroup.
 struct StatePassCtx {
-    const uint16_t* q;
-    const uint16_t* k;
-    const uint16_t* v;
+    const void* q;
+    const void* k;
+    const void* v;
     const char* records;
     int64_t rs, re, qk_stride;
     int c0, h, hk, Hv, dv0;
@@ -424,7 +497,7 @@ struct StatePassCtx {
 // token, which contribute nothing: their beta and log-decay are zero, so
 // their columns of Tb and P and their rows of D vanish. Addresses are a
 // uniform per-chunk base plus a 32-bit lane offset.
-template <bool kUpper>
+template <bool kUpper, bool kF32>
 GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int w, int l) {
     const int len = cx.len(c);
     const int64_t qk0 = cx.t0(c) * cx.qk_stride + cx.hk * kHD + 8 * (l & 15);
@@ -432,18 +505,46 @@ GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int
     for (int i = 0; i < 4; ++i) {
         const int tok = 16 * w + 4 * i + (l >> 4);
         const int tok_c = tok < len ? tok : len - 1;
-        op.ka[i] = load8(cx.k + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride));
+        const uint32_t o = uint32_t(tok_c) * uint32_t(cx.qk_stride);
+        if constexpr (kF32) {
+            u16x8 h, r;
+            load_split8(static_cast<const float*>(cx.k) + qk0 + o, h, r);
+            op.ka[i] = __builtin_bit_cast(bf16x8, h);
+            op.kal[i] = __builtin_bit_cast(bf16x8, r);
+        } else {
+            op.ka[i] = load8(static_cast<const uint16_t*>(cx.k) + qk0 + o);
+        }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tok = 16 * w + 4 * i + (l >> 4);
         const int tok_c = tok < len ? tok : len - 1;
-        op.qa[i] = load8(cx.q + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride));
+        const uint32_t o = uint32_t(tok_c) * uint32_t(cx.qk_stride);
+        if constexpr (kF32) {
+            u16x8 h, r;
+            load_split8(static_cast<const float*>(cx.q) + qk0 + o, h, r);
+            op.qa[i] = __builtin_bit_cast(bf16x8, h);
+            op.qal[i] = __builtin_bit_cast(bf16x8, r);
+        } else {
+            op.qa[i] = load8(static_cast<const uint16_t*>(cx.q) + qk0 + o);
+        }
     }
     const int tv = 16 * w + (l >> 2);
     const int tv_c = tv < len ? tv : len - 1;
-    const uint16_t* vb = cx.v + cx.t0(c) * cx.Hv * kHD + cx.h * kHD + cx.dv0 + 4 * (l & 3);
-    op.v = *reinterpret_cast<const u32x2*>(vb + uint32_t(tv_c) * uint32_t(cx.Hv * kHD));
+    const int64_t vo = cx.t0(c) * cx.Hv * kHD + cx.h * kHD + cx.dv0 + 4 * (l & 3) +
+                       uint32_t(tv_c) * uint32_t(cx.Hv * kHD);
+    if constexpr (kF32) {
+        const float4 v4 = *reinterpret_cast<const float4*>(static_cast<const float*>(cx.v) + vo);
+        const float x[4] = {v4.x, v4.y, v4.z, v4.w};
+        uint16_t h[4], r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) split_bf16(x[j], h[j], r[j]);
+        const uint2 ph = pack4(h), pr = pack4(r);
+        op.v = u32x2{ph.x, ph.y};
+        op.vl = u32x2{pr.x, pr.y};
+    } else {
+        op.v = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(cx.v) + vo);
+    }
     const char* rec = cx.rec(c);
     op.e = *reinterpret_cast<const f32x4*>(rec + kRecEl + 128 * w + 16 * (l & 7));
     const uint16_t* tb_hi = reinterpret_cast<const uint16_t*>(rec + kRecTbHi);
@@ -467,6 +568,8 @@ GDN_DEV void fetch_output(OutputOperands& op, const StatePassCtx& cx, int c, int
     }
 }
 
+// kF32 (float32 q, k, v): K, Q and V also keep their bf16 residuals.
+template <bool kF32>
 struct StatePassLds {
     uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];  // S[dv][dk]
     uint16_t Kr[2][kChunk * kHD];                                 // K[token][dk] (swizzled), two buffers
@@ -477,6 +580,9 @@ struct StatePassLds {
     uint16_t Ds_hi[kSliceRows * kTS], Ds_lo[kSliceRows * kTS];    // D[dv][token]
     uint16_t D2_hi[kSliceRows * kTS], D2_lo[kSliceRows * kTS];    // D''[dv][token]
     float ex[2 * kChunk];                                         // exp(l), exp(l_C - l)
+    uint16_t Kr_lo[kF32 ? 2 : 1][kF32 ? kChunk * kHD : 8];        // residuals (float32 input)
+    uint16_t Qs_lo[kF32 ? kChunk * kQS : 8];
+    uint16_t Vs_lo[kF32 ? kChunk * kSliceRows : 8];
 };
 
 // The K tile is read three ways: whole rows (staging), 16 rows at one
@@ -490,28 +596,39 @@ GDN_DEV int kr_off(int r, int G) { return r * kHD + ((G ^ kswz(r)) << 3); }
 
 // Output waves: staged operands into LDS, in the layouts the state waves
 // read them with.
-GDN_DEV void stage_k(const StagedOperands& op, StatePassLds& sm, int buf, int w, int l) {
+template <bool kF32>
+GDN_DEV void stage_k(const StagedOperands& op, StatePassLds<kF32>& sm, int buf, int w, int l) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<bf16x8*>(sm.Kr[buf] + kr_off(16 * w + 4 * i + (l >> 4), l & 15)) = op.ka[i];
+    for (int i = 0; i < 4; ++i) {
+        const int o = kr_off(16 * w + 4 * i + (l >> 4), l & 15);
+        *reinterpret_cast<bf16x8*>(sm.Kr[buf] + o) = op.ka[i];
+        if constexpr (kF32) *reinterpret_cast<bf16x8*>(sm.Kr_lo[buf] + o) = op.kal[i];
+    }
 }
 
 // Wave w's Q rows are read only by wave w (in output_project), so the next
 // chunk's may be written as soon as this wave's projection has read them.
-GDN_DEV void stage_q(const StagedOperands& op, StatePassLds& sm, int w, int l) {
-    uint16_t* qr = sm.Qs + (16 * w + (l >> 4)) * kQS + 8 * (l & 15);
+template <bool kF32>
+GDN_DEV void stage_q(const StagedOperands& op, StatePassLds<kF32>& sm, int w, int l) {
+    const int o = (16 * w + (l >> 4)) * kQS + 8 * (l & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<bf16x8*>(qr + 4 * i * kQS) = op.qa[i];
+    for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<bf16x8*>(sm.Qs + o + 4 * i * kQS) = op.qa[i];
+        if constexpr (kF32) *reinterpret_cast<bf16x8*>(sm.Qs_lo + o + 4 * i * kQS) = op.qal[i];
+    }
 }
 
-GDN_DEV void stage_v(const StagedOperands& op, StatePassLds& sm, int w, int l) {
-    *reinterpret_cast<u32x2*>(sm.Vs + (16 * w + (l >> 2)) * kSliceRows + 4 * (l & 3)) = op.v;
+template <bool kF32>
+GDN_DEV void stage_v(const StagedOperands& op, StatePassLds<kF32>& sm, int w, int l) {
+    const int o = (16 * w + (l >> 2)) * kSliceRows + 4 * (l & 3);
+    *reinterpret_cast<u32x2*>(sm.Vs + o) = op.v;
+    if constexpr (kF32) *reinterpret_cast<u32x2*>(sm.Vs_lo + o) = op.vl;
 }
 
 // Lanes 8-63 repeat lanes 0-7 for the decay words (same words, same values):
 // an unconditional store keeps the operand registers out of any branch.
-template <bool kUpper>
-GDN_DEV void stage_tb_e(const StagedOperands& op, StatePassLds& sm, int w, int l) {
+template <bool kUpper, bool kF32>
+GDN_DEV void stage_tb_e(const StagedOperands& op, StatePassLds<kF32>& sm, int w, int l) {
     const int row = (16 * w + (l & 15)) * kTS + 8 * (l >> 4);
 #pragma unroll
     for (int s = 0; s < (kUpper ? 2 : 1); ++s) {
@@ -522,7 +639,8 @@ GDN_DEV void stage_tb_e(const StagedOperands& op, StatePassLds& sm, int w, int l
 }
 
 // State waves, chunk part 1: the S operand (hi + lo) into LDS.
-GDN_DEV void state_stage(const f32x4 (&acc)[2], StatePassLds& sm, int w, int l) {
+template <bool kF32>
+GDN_DEV void state_stage(const f32x4 (&acc)[2], StatePassLds<kF32>& sm, int w, int l) {
     const int lr = l & 15, lq = l >> 4;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -537,21 +655,32 @@ GDN_DEV void state_stage(const f32x4 (&acc)[2], StatePassLds& sm, int w, int l) 
 
 // State waves, part 2 (between the staging and R barriers):
 // R^T = V^T - S K^T diag(exp l), lane (dv = 4(l/16) + i, token = 16w + l%16).
-GDN_DEV void state_residual(const StatePassLds& sm, StatePassLds& smw, int buf, int w, int l) {
+template <bool kF32>
+GDN_DEV void state_residual(const StatePassLds<kF32>& sm, StatePassLds<kF32>& smw, int buf, int w, int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
     const int tok = 16 * w + lr;
     f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xk2 = xk;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        const bf16x8 kb = load8(sm.Kr[buf] + kr_off(tok, 4 * s + lq));
-        xk = mfma16(load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), kb, xk);
+        const int ko = kr_off(tok, 4 * s + lq);
+        const bf16x8 kb = load8(sm.Kr[buf] + ko);
+        const bf16x8 sh = load8(sm.Ss_hi + lr * kSS + 32 * s + lg8);
+        xk = mfma16(sh, kb, xk);
         xk2 = mfma16(load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), kb, xk2);
+        if constexpr (kF32) xk2 = mfma16(sh, load8(sm.Kr_lo[buf] + ko), xk2);
     }
     xk += xk2;
     const float el = sm.ex[tok];
     const u32x2 vv = *reinterpret_cast<const u32x2*>(sm.Vs + tok * kSliceRows + 4 * lq);
-    const float v[4] = {__uint_as_float(vv[0] << 16), __uint_as_float(vv[0] & 0xffff0000u),
-                        __uint_as_float(vv[1] << 16), __uint_as_float(vv[1] & 0xffff0000u)};
+    float v[4] = {__uint_as_float(vv[0] << 16), __uint_as_float(vv[0] & 0xffff0000u),
+                  __uint_as_float(vv[1] << 16), __uint_as_float(vv[1] & 0xffff0000u)};
+    if constexpr (kF32) {  // V = hi + residual (exact to ~16 significant bits)
+        const u32x2 vr = *reinterpret_cast<const u32x2*>(sm.Vs_lo + tok * kSliceRows + 4 * lq);
+        v[0] += __uint_as_float(vr[0] << 16);
+        v[1] += __uint_as_float(vr[0] & 0xffff0000u);
+        v[2] += __uint_as_float(vr[1] << 16);
+        v[3] += __uint_as_float(vr[1] & 0xffff0000u);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         uint16_t hi, lo;
@@ -563,8 +692,8 @@ GDN_DEV void state_residual(const StatePassLds& sm, StatePassLds& smw, int buf, 
 
 // State waves, part 3 (between the R and D barriers): D = Tb R, stored as
 // D (hi + lo, for Y) and D'' = exp(l_C - l) D (hi + lo, for the update).
-template <bool kUpper>
-GDN_DEV void state_delta(StatePassLds& sm, int w, int l) {
+template <bool kUpper, bool kF32>
+GDN_DEV void state_delta(StatePassLds<kF32>& sm, int w, int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
     const int row = (16 * w + lr) * kTS + lg8;
     f32x4 d = {0.f, 0.f, 0.f, 0.f}, d2 = d;
@@ -599,10 +728,23 @@ GDN_DEV void state_delta(StatePassLds& sm, int w, int l) {
 // within each 16-lane group, lane i of a ds_read_b64_tr_b16 receives element
 // i%4 of source lane i/4 + 4k (k = 0..3); source lane s of group g points at
 // K[8g + 4h + s/4][dk0 + 4(s%4)] for the tokens 8g + 4h .. +3.
-GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds& sm, int buf, float eC, int w,
+template <bool kF32>
+GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds<kF32>& sm, int buf, float eC, int w,
                           int l) {
     const int g = l >> 4, sl = l & 15, lr = sl, lg8 = 8 * g;
     const uint16_t* kr = sm.Kr[buf];
+    const uint16_t* krl = sm.Kr_lo[kF32 ? buf : 0];
+    auto kt_operand = [&](const uint16_t* tile, int s, int dk0) {
+        v4s parts[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int r = 32 * s + 8 * g + 4 * hh + (sl >> 2);
+            const uint16_t* src = tile + kr_off(r, (dk0 >> 3) + ((sl & 3) >> 1)) + 4 * (sl & 1);
+            parts[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4s*)(src));
+        }
+        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(parts[0], parts[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         acc[t] *= eC;
@@ -610,33 +752,29 @@ GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds& sm, int buf, floa
         const int dk0 = 32 * w + 16 * t;
 #pragma unroll
         for (int s = 0; s < kChunk / 32; ++s) {
-            v4s parts[2];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int r = 32 * s + 8 * g + 4 * hh + (sl >> 2);
-                const uint16_t* src = kr + kr_off(r, (dk0 >> 3) + ((sl & 3) >> 1)) + 4 * (sl & 1);
-                parts[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) v4s*)(src));
-            }
-            const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(
-                parts[0], parts[1], 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[t] = mfma16(a, load8(sm.D2_hi + lr * kTS + 32 * s + lg8), acc[t]);
+            const bf16x8 a = kt_operand(kr, s, dk0);
+            const bf16x8 dh = load8(sm.D2_hi + lr * kTS + 32 * s + lg8);
+            acc[t] = mfma16(a, dh, acc[t]);
             lo_acc = mfma16(a, load8(sm.D2_lo + lr * kTS + 32 * s + lg8), lo_acc);
+            if constexpr (kF32) lo_acc = mfma16(kt_operand(krl, s, dk0), dh, lo_acc);
         }
         acc[t] += lo_acc;
     }
 }
 
 // Output waves, part 1 (between the staging and R barriers): exp(l) Q S^T.
-GDN_DEV f32x4 output_project(const StatePassLds& sm, int w, int l) {
+template <bool kF32>
+GDN_DEV f32x4 output_project(const StatePassLds<kF32>& sm, int w, int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
-    const uint16_t* qr = sm.Qs + (16 * w + lr) * kQS + lg8;
+    const int qo = (16 * w + lr) * kQS + lg8;
     f32x4 xq = {0.f, 0.f, 0.f, 0.f}, xq2 = xq;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        const bf16x8 qa = load8(qr + 32 * s);
-        xq = mfma16(qa, load8(sm.Ss_hi + lr * kSS + 32 * s + lg8), xq);
+        const bf16x8 qa = load8(sm.Qs + qo + 32 * s);
+        const bf16x8 sh = load8(sm.Ss_hi + lr * kSS + 32 * s + lg8);
+        xq = mfma16(qa, sh, xq);
         xq2 = mfma16(qa, load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xq2);
+        if constexpr (kF32) xq2 = mfma16(load8(sm.Qs_lo + qo + 32 * s), sh, xq2);
     }
     xq += xq2;
     const float4 el = *reinterpret_cast<const float4*>(sm.ex + 16 * w + 4 * lq);
@@ -648,8 +786,8 @@ GDN_DEV f32x4 output_project(const StatePassLds& sm, int w, int l) {
 }
 
 // Output waves, part 2 (after the D barrier): y = exp(l) Q S^T + P D.
-template <class Y, bool kUpper>
-GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassLds& sm,
+template <class Y, bool kUpper, bool kF32>
+GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassLds<kF32>& sm,
                           const StatePassCtx& cx, int c, typename Y::storage* __restrict__ y, int w,
                           int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
@@ -693,8 +831,8 @@ GDN_DEV void output_store(const OutputOperands& op, f32x4 yacc, const StatePassL
 // lets the compiler sink the first step's prefetch (invariant loads) to just
 // before its use. Chunk indices past the run repeat its last chunk, so every
 // fetch is unconditional.
-template <bool kUpper>
-GDN_DEV void state_loop(int nch, StatePassLds& sm, f32x4 (&acc)[2], int w, int l) {
+template <bool kUpper, bool kF32>
+GDN_DEV void state_loop(int nch, StatePassLds<kF32>& sm, f32x4 (&acc)[2], int w, int l) {
     auto step = [&](int buf) {
         state_stage(acc, sm, w, l);
         __syncthreads();
@@ -713,8 +851,8 @@ GDN_DEV void state_loop(int nch, StatePassLds& sm, f32x4 (&acc)[2], int w, int l
     if (c < nch) step(0);
 }
 
-template <class Y, bool kUpper>
-GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
+template <class Y, bool kUpper, bool kF32>
+GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds<kF32>& sm,
                          typename Y::storage* __restrict__ y, int w, int l) {
     const int last = nch - 1;
     StagedOperands ga, gb;
@@ -730,15 +868,15 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
         stage_q(gn, sm, w, l);
         stage_k(gn, sm, buf ^ 1, w, l);
         stage_v(gn, sm, w, l);
-        fetch_staged<kUpper>(gf, cx, c + 2 < last ? c + 2 : last, w, l);
+        fetch_staged<kUpper, kF32>(gf, cx, c + 2 < last ? c + 2 : last, w, l);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         stage_tb_e<kUpper>(gn, sm, w, l);
         output_store<Y, kUpper>(oc, yacc, sm, cx, c, y, w, l);
     };
     // chunk 0 into LDS; chunk 1 (or 0 again) into registers
-    fetch_staged<kUpper>(gb, cx, 0, w, l);
-    fetch_staged<kUpper>(ga, cx, 1 < last ? 1 : last, w, l);
+    fetch_staged<kUpper, kF32>(gb, cx, 0, w, l);
+    fetch_staged<kUpper, kF32>(ga, cx, 1 < last ? 1 : last, w, l);
     fetch_output<kUpper>(oa, cx, 0, w, l);
     stage_q(gb, sm, w, l);
     stage_k(gb, sm, 0, w, l);
@@ -752,13 +890,13 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds& sm,
     if (c < nch) step(c, 0, oa, ob, ga, gb);
 }
 
-template <class Y>
+template <class Y, bool kF32>
 __global__ __launch_bounds__(kStateThreads) void prefill_state_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ state_in, float* __restrict__ state_out,
     typename Y::storage* __restrict__ y, RunLayout rl, const char* __restrict__ records, int Hk,
     int Hv) {
-    __shared__ __attribute__((aligned(16))) StatePassLds sm;
+    __shared__ __attribute__((aligned(16))) StatePassLds<kF32> sm;
 
     // Work mapping: the 8 slices of one (run, head) share its K/Q and chunk
     // records, so they are placed on one XCD (workgroups go round-robin over
@@ -832,7 +970,7 @@ extern "C" int64_t gdn_prefill_workspace_size(int N, int64_t T_total, int Hk, in
     return records_offset(N) + chunks_bound(T_total, N) * Hv * kRecBytes;
 }
 
-extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* ga,
+extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, int qkv_dtype, const void* ga,
                                    const void* gb, int gb_dtype, int64_t gate_stride, const float* A_log,
                                    const float* dt_bias, int gate_mode, const float* state_in,
                                    float* state_out, void* y, int y_dtype,
@@ -847,6 +985,9 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     GDN_REQUIRE(gate_stride >= Hv, "gdn_prefill_chunked: gate_stride %lld below Hv=%d",
                 (long long)gate_stride, Hv);
     GDN_REQUIRE(valid_dtype(gb_dtype) && valid_dtype(y_dtype), "gdn_prefill_chunked: bad dtype");
+    if (qkv_dtype != GDN_BF16 && qkv_dtype != GDN_F32)
+        return fail(GDN_EUNSUPPORTED, "gdn_prefill_chunked: q, k, v must be bfloat16 or float32");
+    const bool f32 = qkv_dtype == GDN_F32;
     GDN_REQUIRE(gate_mode == 1 || (A_log && dt_bias), "gdn_prefill_chunked: gate_mode 0 needs A_log, dt_bias");
     GDN_REQUIRE(cu_seqlens || T_total % N == 0, "gdn_prefill_chunked: T_total not divisible by N");
     GDN_REQUIRE(T_total < (int64_t(1) << 31), "gdn_prefill_chunked: token count must fit int32");
@@ -856,7 +997,8 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
                  reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out) |
                  reinterpret_cast<uintptr_t>(workspace)) % 16 == 0,
                 "gdn_prefill_chunked: q, k, states and workspace must be 16-byte aligned");
-    GDN_REQUIRE(reinterpret_cast<uintptr_t>(v) % 8 == 0, "gdn_prefill_chunked: v must be 8-byte aligned");
+    GDN_REQUIRE(reinterpret_cast<uintptr_t>(v) % (f32 ? 16 : 8) == 0,
+                "gdn_prefill_chunked: v must be %d-byte aligned", f32 ? 16 : 8);
     const int64_t need = records_offset(N) + chunks_bound(T_total, N) * Hv * kRecBytes;
     GDN_REQUIRE(workspace && workspace_bytes >= need,
                 "gdn_prefill_chunked: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
@@ -883,19 +1025,23 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     }
     const int64_t nchunks = chunks_bound(T_total, N);
     const int64_t items = (nchunks * Hk + 7) / 8 * 8;
-    hipLaunchKernelGGL(prefill_chunk_kernel, dim3(unsigned(items * (Hv / Hk))), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), ga, gb,
+    hipLaunchKernelGGL(f32 ? prefill_chunk_f32_kernel : prefill_chunk_kernel,
+                       dim3(unsigned(items * (Hv / Hk))), dim3(256), 0, s, q, k, ga, gb,
                        gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl, records, Hk, Hv);
     if (int rc = check_launch("gdn_prefill_chunked/chunk")) return rc;
     const dim3 sgrid(unsigned(int64_t(N) * Hv * kSlices));
-#define GDN_STATE_LAUNCH(YT)                                                                      \
-    hipLaunchKernelGGL(prefill_state_kernel<YT>, sgrid, dim3(kStateThreads), 0, s,                          \
-                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),           \
-                       static_cast<const uint16_t*>(v), state_in, state_out,                       \
-                       static_cast<YT::storage*>(y), rl, records, Hk, Hv)
-    if (y_dtype == GDN_F32) GDN_STATE_LAUNCH(ActF32);
-    else if (y_dtype == GDN_BF16) GDN_STATE_LAUNCH(ActBF16);
-    else GDN_STATE_LAUNCH(ActF16);
+#define GDN_STATE_LAUNCH(YT, F32)                                                                 \
+    hipLaunchKernelGGL((prefill_state_kernel<YT, F32>), sgrid, dim3(kStateThreads), 0, s, q, k, v, \
+                       state_in, state_out, static_cast<YT::storage*>(y), rl, records, Hk, Hv)
+    if (f32) {
+        if (y_dtype == GDN_F32) GDN_STATE_LAUNCH(ActF32, true);
+        else if (y_dtype == GDN_BF16) GDN_STATE_LAUNCH(ActBF16, true);
+        else GDN_STATE_LAUNCH(ActF16, true);
+    } else {
+        if (y_dtype == GDN_F32) GDN_STATE_LAUNCH(ActF32, false);
+        else if (y_dtype == GDN_BF16) GDN_STATE_LAUNCH(ActBF16, false);
+        else GDN_STATE_LAUNCH(ActF16, false);
+    }
 #undef GDN_STATE_LAUNCH
     return check_launch("gdn_prefill_chunked/state");
 }

@@ -157,7 +157,8 @@ def _launch_prefill(q, k, v, ga, gb, A_log, dt_bias, gate_mode, state_in, state_
     nbytes = prefill_workspace_bytes(N, T, Hk, Hv, Dk, Dv)
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-    _lib.call("gdn_prefill_chunked", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(ga),
+    _lib.call("gdn_prefill_chunked", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
+              _lib.dtype_code(q.dtype), _lib.ptr(ga),
               _lib.ptr(gb), _lib.dtype_code(gb.dtype), Hv if gate_stride is None else gate_stride,
               _lib.ptr(A_log), _lib.ptr(dt_bias),
               gate_mode, _lib.ptr(state_in), _lib.ptr(state_out), _lib.ptr(y),
@@ -166,13 +167,19 @@ def _launch_prefill(q, k, v, ga, gb, A_log, dt_bias, gate_mode, state_in, state_
 
 
 def _prefill_eligible(q, k, v, tokens_per_run: float) -> bool:
-    """The chunked prefill's shapes, dtypes and operand alignment (q, k 16
-    bytes, v 8 bytes: a contiguous view may start anywhere in its storage)."""
+    """The chunked prefill's shapes, dtypes and operand alignment: q, k, v
+    all bfloat16 (q, k 16-byte aligned, v 8) or all float32 (each 16-byte
+    aligned); a contiguous view may start anywhere in its storage."""
 
-    return (q.dtype == k.dtype == v.dtype == torch.bfloat16 and q.shape[-1] == 128
-            and v.shape[-1] == 128
+    if q.dtype == k.dtype == v.dtype == torch.bfloat16:
+        v_align = 8
+    elif q.dtype == k.dtype == v.dtype == torch.float32:
+        v_align = 16
+    else:
+        return False
+    return (q.shape[-1] == 128 and v.shape[-1] == 128
             and tokens_per_run >= PREFILL_MIN_TOKENS
-            and q.data_ptr() % 16 == 0 and k.data_ptr() % 16 == 0 and v.data_ptr() % 8 == 0)
+            and q.data_ptr() % 16 == 0 and k.data_ptr() % 16 == 0 and v.data_ptr() % v_align == 0)
 
 
 # ---------------------------------------------------------------------------
@@ -307,7 +314,8 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=
     else:
         _check_out(state_out, (N, Hv, Dv, Dk), s_dtype, device, state_in, "state_out")
     if T > 0:
-        if (use_kernel and s_dtype == torch.float32 and a.dtype == b.dtype == torch.bfloat16
+        if (use_kernel and s_dtype == torch.float32 and a.dtype == b.dtype
+                and a.dtype in (torch.bfloat16, torch.float32)
                 and _prefill_eligible(q, k, v, mean_run)):
             if not rows_ok:
                 a, b = _c(a), _c(b)

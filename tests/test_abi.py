@@ -68,8 +68,8 @@ def test_invalid_arguments_return_einval_without_launching():
                                  None)
         assert rc == _lib.GDN_EINVAL and what in _err(lib), (what, _err(lib))
     # a gate row stride below Hv
-    rc = lib.gdn_prefill_chunked(*fake[:5], 1, 3, *fake[5:7], 0, None, fake[7], fake[8], 0, None, 1, 64,
-                                 2, 4, 128, 128, fake[9], 1 << 30, None)
+    rc = lib.gdn_prefill_chunked(*fake[:3], 1, *fake[3:5], 1, 3, *fake[5:7], 0, None, fake[7], fake[8], 0,
+                                 None, 1, 64, 2, 4, 128, 128, fake[9], 1 << 30, None)
     assert rc == _lib.GDN_EINVAL and "gate_stride" in _err(lib), _err(lib)
     # overlapping conv state buffers are rejected
     p = ctypes.c_void_p(4096)

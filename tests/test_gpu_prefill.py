@@ -305,3 +305,71 @@ def test_prefill_bf16_output_and_zero_state_pointer(gpu):
     assert y16.dtype == torch.bfloat16
     np.testing.assert_array_equal(y16.float().cpu().numpy(), R.bf16_round(y32.cpu().numpy()))
     torch.testing.assert_close(s16, s32, rtol=0, atol=0)
+
+
+def _f32_inputs(seed, T, Hk, Hv, d=128, state_scale=0.0, N=1):
+    """The workload's inputs in float32, as the reference's layers carry
+    activations: q/k L2-normalised (q also / sqrt(d)) but not bf16-rounded;
+    v, a, b ~N(0, 1)."""
+
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((T, Hk, d))
+    k = rng.standard_normal((T, Hk, d))
+    q /= np.linalg.norm(q, axis=-1, keepdims=True) * d ** 0.5
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    f = lambda x: np.asarray(x, np.float32)
+    v, a, b = rng.standard_normal((T, Hv, d)), rng.standard_normal((T, Hv)), rng.standard_normal((T, Hv))
+    A_log = rng.uniform(0, np.log(16), Hv).astype(np.float32)
+    dt_bias = rng.uniform(-1, 1, Hv).astype(np.float32)
+    state = (rng.standard_normal((N, Hv, d, d)) * state_scale).astype(np.float32)
+    return f(q), f(k), f(v), f(a), f(b), A_log, dt_bias, state
+
+
+@pytest.mark.parametrize("lens", [[64], [200], [3, 63, 130, 0, 65, 130]])
+def test_prefill_float32_inputs_match_float64_oracle(gpu, lens):
+    """float32 q, k, v, a, b (the reference's activation dtype, not
+    representable in bf16) take the chunked prefill, each value split into
+    a bf16 high part and residual: y and state within 1e-4 relative of the
+    float64 recurrence, with nonzero initial states and ragged packed runs."""
+
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T, N = int(cu[-1]), len(lens)
+    arrays = _f32_inputs(20 + T, T, Hk=2, Hv=4, state_scale=0.05, N=N)
+    t = _dev(gpu, arrays, bf16_names=())
+    assert gated_delta._prefill_eligible(t["q"], t["k"], t["v"], 64)
+    calls = []
+    real = gated_delta._lib.call
+    gated_delta._lib.call = lambda name, *a: (calls.append(name), real(name, *a))[1]
+    try:
+        y, s = gdn.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"],
+                                      t["dt_bias"], t["state"], cu_seqlens=cu)
+    finally:
+        gated_delta._lib.call = real
+    assert "gdn_prefill_chunked" in calls and y.dtype == torch.float32
+    q, k, v, a, b, A_log, dt_bias, state = arrays
+    ye, se = R.gated_delta_update(q, k, v, a, b, A_log, dt_bias, state, cu_seqlens=cu)
+    assert max_rel(y.cpu().numpy(), ye) < 1e-4
+    assert max_rel(s.cpu().numpy(), se) < 1e-4
+
+
+def test_prefill_float32_full_size_against_c_oracle(gpu):
+    """T=4096, Hk=16, Hv=32, float32 inputs, zero initial state: y and final
+    state within 1e-3 relative of the float32 token-by-token recurrence (C
+    oracle); and within 1e-4 of this library's sequential scan."""
+
+    T, Hk, Hv = 4096, 16, 32
+    arrays = _f32_inputs(1, T, Hk=Hk, Hv=Hv)
+    q, k, v, a, b, A_log, dt_bias, state = arrays
+    t = _dev(gpu, arrays, bf16_names=())
+    y, s = gdn.gated_delta_update(t["q"][None], t["k"][None], t["v"][None], t["a"][None],
+                                  t["b"][None], t["A_log"], t["dt_bias"], t["state"])
+    g = R.forget_gate(a, A_log, dt_bias).astype(np.float32)
+    beta = R.beta_gate(b).astype(np.float32)
+    ye, se = cref.scan(q[None], k[None], v[None], g[None], beta[None], state)
+    assert max_rel(y.cpu().numpy(), ye) < 1e-3
+    assert max_rel(s.cpu().numpy(), se) < STATE_REL
+    y2, s2 = gdn.gated_delta_update(t["q"][None], t["k"][None], t["v"][None], t["a"][None],
+                                    t["b"][None], t["A_log"], t["dt_bias"], t["state"],
+                                    use_kernel=False)
+    assert max_rel(s.cpu().numpy(), s2.cpu().numpy()) < 1e-4
+    assert max_rel(y.cpu().numpy(), y2.cpu().numpy()) < 1e-4
