@@ -12,8 +12,12 @@ exceeds the 256 MB Infinity Cache: the bandwidth figure is HBM's.
 Also measured in the same run (reported under "also"):
   decode_b64:   B=64, Hv=32, no gate (128 MiB state, four rotating buffers
                 as above: 512 MiB)
+  decode_b1:    one sequence (the reference's own decode), Hv=32, with and
+                without the gated norm; 64 steps per HIP graph, as the
+                launch itself takes longer than the step
   prefill:      B=1, T=4096 chunked prefill (bf16 MFMA), with its roofline
                 and CPU baseline
+  prefill_f32:  the same with float32 q/k/v/a/b
   prefill_varlen: 16 packed runs of U[128, 8192] tokens (67,128 in all)
   decode_slots: B=64 active sequences at random slots of a 256-sequence pool
   layer_decode: the whole layer's decode step with 4-bit projections, B=64
@@ -24,8 +28,8 @@ Also measured in the same run (reported under "also"):
   projections (--workload layer_prefill: the same alone)
 
 python bench.py [--steps K] [--warmup W] [--batch B]
-                [--workload decode|decode_b64|decode_slots|layer_decode|layer_prefill|prefill|
-                            prefill_varlen|qlinear|copy]
+                [--workload decode|decode_b64|decode_b1|decode_slots|layer_decode|layer_prefill|
+                            prefill|prefill_f32|prefill_varlen|qlinear|copy]
 (--workload decode_large is the default decode workload under its older name.)
 """
 
@@ -89,15 +93,17 @@ class DecodeWorkload:
         _, _, self.bytes_per_step = decode_bytes(B, Hk, Hv, d, K, with_z)
         self.args = self._bind()
 
-    def _bind(self):
+    def _bind(self, stream=None):
         """Pre-resolved C-ABI argument tuples, one per step phase, so the
-        timed loop is a bare sequence of launches."""
+        timed loop is a bare sequence of launches (on `stream`, by default
+        the current one)."""
 
         from mlx_lean_moe_amd import _lib
 
         d = self.dims
         lib = _lib.load()
-        stream = torch.cuda.current_stream().cuda_stream
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
         n_s, n_i = len(self.states), len(self.qkv)
         phases = []
         # step s reads state buffer s % n_s and writes (s + 2) % n_s: the
@@ -406,6 +412,44 @@ def bench_decode(dev, B, Hk, Hv, with_z, steps, warmup):
         "bytes_per_step": w.bytes_per_step,
         "hbm_gbs": achieved,
         "hbm_frac": achieved / HBM_PEAK_GBS,
+    }
+
+
+def bench_decode_graph(dev, B, Hk, Hv, with_z, replays=20, per_graph=64):
+    """Decode steps at sizes where one launch takes less time than issuing
+    it (a single sequence): `per_graph` steps captured in one HIP graph,
+    `replays` replays timed by one event pair; per-step time is the graph's
+    time over its steps (kernel time plus the graph's own gap between
+    launches)."""
+
+    w = DecodeWorkload(dev, B, Hk, Hv, with_z)
+    fn = w._fn
+    for s in range(8):
+        w.step(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        args = w._bind(torch.cuda.current_stream().cuda_stream)
+        for s in range(per_graph):
+            if fn(*args[s % len(args)]) != 0:
+                raise RuntimeError("gdn_decode_step failed during capture")
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * per_graph)
+    gbs = w.bytes_per_step / (us * 1e-6) / 1e9
+    return {
+        "workload": f"decode B={B} Hk={Hk} Hv={Hv} d=128 K=4, fused conv roll"
+                    + (" + gated RMSNorm" if with_z else ""),
+        "step_us": us, "tokens_per_s": B / (us * 1e-6), "hbm_gbs": gbs,
+        "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_step": w.bytes_per_step,
+        "timing": f"{per_graph} steps per HIP graph, {replays} replays",
     }
 
 
@@ -786,6 +830,8 @@ def bench_also(dev, cpu=True):
     """The secondary workloads of the default run."""
 
     sm = bench_decode(dev, 64, 16, 32, False, steps=64, warmup=8)
+    d1 = bench_decode_graph(dev, 1, 16, 32, True)
+    d1n = bench_decode_graph(dev, 1, 16, 32, False)
     pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
     pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
     p32 = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3, dtype=torch.float32,
@@ -798,6 +844,8 @@ def bench_also(dev, cpu=True):
             "workload": DECODE_WORKLOADS[True], "tokens_per_s": sm["tokens_per_s"],
             "roofline": decode_roofline(sm, True),
             **({"cpu_baseline": cpu_baseline_decode(64, 16, 32, False, budget_s=5.0)} if cpu else {})},
+        "decode_b1": d1,
+        "decode_b1_no_norm": d1n,
         "prefill": {
             "workload": "chunked prefill B=1 T=4096 Hk=16 Hv=32 d=128 chunk 64, bf16 MFMA",
             "tokens_per_s": pf["tokens_per_s"], "call_us": pf["call_us"],
@@ -836,7 +884,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "decode_b64", "decode_slots", "layer_decode",
+                    choices=["decode", "decode_large", "decode_b64", "decode_b1", "decode_slots", "layer_decode",
                              "layer_prefill", "prefill_f32",
                              "prefill", "prefill_varlen", "qlinear", "copy"])
     ap.add_argument("--layers", type=int, default=1,
@@ -898,6 +946,11 @@ def main(argv=None):
         if not args.no_also and not small:
             line["also"] = bench_also(dev, cpu=not args.no_cpu_baseline)
         print(json.dumps(line))
+        return 0
+
+    if args.workload == "decode_b1":
+        print(json.dumps({"decode_b1": bench_decode_graph(dev, 1, 16, 32, True),
+                          "decode_b1_no_norm": bench_decode_graph(dev, 1, 16, 32, False)}))
         return 0
 
     if args.workload == "layer_decode":

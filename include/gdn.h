@@ -125,8 +125,10 @@ int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dt
 /*
  * gdn_decode_step - one fused decode token for B sequences: conv + SiLU +
  * conv-state roll, q/k scaling, gates, the recurrence, and optionally the
- * gated RMSNorm. One workgroup per (sequence, value head); the float32
- * Dv x Dk state tile is read once and written once.
+ * gated RMSNorm. One workgroup per (sequence, value head), or, without the
+ * norm and when B * Hv is at most 128, 2-8 workgroups per head that each
+ * take a share of its rows (the same arithmetic per row: the same state and
+ * output bits); the float32 Dv x Dk state tile is read once and written once.
  *   qkv:            (B, C) act_dtype (pre-conv projection output)
  *   conv_state_in:  (B, K-1, C) act_dtype; conv_state_out must not overlap it
  *   conv_weight:    (C, K) float32

@@ -107,10 +107,19 @@ GDN_DEV float round_once(double x, int dtype) {
     return round_to(f, dtype);
 }
 
-// beta = sigmoid(b) held in `dtype` (linear_attention.py:116), evaluated in
-// double and rounded once: the value the exact sigmoid rounds to, so the
-// decision at a rounding boundary does not depend on float32 error.
+// beta = sigmoid(b) held in `dtype` (linear_attention.py:116): the value the
+// exact sigmoid rounds to, so the decision at a rounding boundary does not
+// depend on float32 error. For bfloat16 a float32 evaluation (within a few
+// float ulps: expf, the sum, the reciprocal) decides it when it lies more
+// than 16 float ulps from a bfloat16 rounding boundary (a low half-word of
+// 0x8000; |b| < 64 keeps the value normal); otherwise, and for the other
+// dtypes, the sigmoid is evaluated in double and rounded once.
 GDN_DEV float beta_of(float b, int dtype) {
+    if (dtype == GDN_BF16 && fabsf(b) < 64.f) {
+        const float f = 1.f / (1.f + expf(-b));
+        const uint32_t low = __float_as_uint(f) & 0xFFFFu;
+        if (low + 16u < 0x8000u || low > 0x8000u + 16u) return round_bf16(f);
+    }
     return round_once(1.0 / (1.0 + exp(-double(b))), dtype);
 }
 
@@ -172,17 +181,80 @@ GDN_DEV float mask_select(uint32_t m, float a, float b) {
     return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
 }
 
-template <int WIDTH>
-GDN_DEV float group_sum(float x) {
-#pragma unroll
-    for (int off = WIDTH / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
-    return x;
+// Lane pairings without an LDS round trip. At level OFF (1, 2, 4, 8, 16, 32)
+// the partner of lane l is l ^ 1 or l ^ 2 (DPP quad_perm), 7 - l within its
+// 8 lanes (row_half_mirror), l ^ 8 within its 16 (row_ror:8), l ^ 16
+// (v_permlane16_swap: rows 0 <-> 1, 2 <-> 3) or l ^ 32 (v_permlane32_swap).
+// The partner always differs from l in bit log2(OFF) and agrees with it in
+// every higher bit, so a butterfly over levels 1 .. WIDTH / 2 (or the other
+// way round) reaches each lane of an aligned group of WIDTH exactly once.
+// Every lane of the wave must be active.
+template <int OFF>
+constexpr int dpp_partner_ctrl() {
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8, "DPP levels: 1, 2, 4, 8");
+    return OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x141 : 0x128;
 }
 
-template <int WIDTH>
-GDN_DEV double group_sum(double x) {
-#pragma unroll
-    for (int off = WIDTH / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+// The partner lane's v, for OFF <= 8.
+template <int OFF>
+GDN_DEV float dpp_partner(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), dpp_partner_ctrl<OFF>(), 0xF, 0xF, false));
+}
+
+// The two operands of v_permlane16_swap / v_permlane32_swap (OFF = 16, 32)
+// after the swap: a lane of the lower row (half) gets {its a, the partner's a},
+// a lane of the upper one {the partner's b, its b}.
+template <int OFF>
+GDN_DEV void lane_swap(float& a, float& b) {
+    static_assert(OFF == 16 || OFF == 32, "swap levels: 16, 32");
+    const auto r = OFF == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false)
+                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+// x + the partner's x at level OFF: both lanes of a pair get the same bits.
+template <int OFF>
+GDN_DEV float pair_sum(float x) {
+    if constexpr (OFF <= 8) {
+        return x + dpp_partner<OFF>(x);
+    } else {
+        float a = x, b = x;
+        lane_swap<OFF>(a, b);  // lower: {x_lower, x_upper}; upper: the same
+        return a + b;
+    }
+}
+
+template <int OFF>
+GDN_DEV double pair_sum(double x) {
+    float lo = __uint_as_float(uint32_t(__double_as_longlong(x)));
+    float hi = __uint_as_float(uint32_t(uint64_t(__double_as_longlong(x)) >> 32));
+    double other;
+    if constexpr (OFF <= 8) {
+        const uint64_t pl = __float_as_uint(dpp_partner<OFF>(lo)), ph = __float_as_uint(dpp_partner<OFF>(hi));
+        other = __longlong_as_double(int64_t(pl | (ph << 32)));
+    } else {
+        float lo2 = lo, hi2 = hi;
+        lane_swap<OFF>(lo, lo2);
+        lane_swap<OFF>(hi, hi2);
+        const double a = __longlong_as_double(int64_t(uint64_t(__float_as_uint(lo)) | (uint64_t(__float_as_uint(hi)) << 32)));
+        const double b = __longlong_as_double(int64_t(uint64_t(__float_as_uint(lo2)) | (uint64_t(__float_as_uint(hi2)) << 32)));
+        return a + b;
+    }
+    return x + other;
+}
+
+// Sum over each aligned group of WIDTH lanes (a power of two up to 64), the
+// same bits in every lane of the group.
+template <int WIDTH, class T>
+GDN_DEV T group_sum(T x) {
+    static_assert(WIDTH >= 1 && WIDTH <= kWave && (WIDTH & (WIDTH - 1)) == 0, "group width");
+    if constexpr (WIDTH >= 2) x = pair_sum<1>(x);
+    if constexpr (WIDTH >= 4) x = pair_sum<2>(x);
+    if constexpr (WIDTH >= 8) x = pair_sum<4>(x);
+    if constexpr (WIDTH >= 16) x = pair_sum<8>(x);
+    if constexpr (WIDTH >= 32) x = pair_sum<16>(x);
+    if constexpr (WIDTH >= 64) x = pair_sum<32>(x);
     return x;
 }
 

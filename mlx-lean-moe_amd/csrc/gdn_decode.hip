@@ -15,12 +15,27 @@
 // Per thread (wave w, lane l, half = l / 32, l32 = l % 32) the tile rows are
 // r_i = 8 i + 2 w + half, i = 0..15, columns 4 l32 .. 4 l32 + 3. The 32
 // partial dot products a half-wave holds (S.k and S.q for its 16 rows) are
-// reduce-scattered across the 32 lanes (31 exchanges instead of 160), which
-// leaves lane l32 with the full S.k of row r_{l32} (l32 < 16) or the full S.q
-// of row r_{l32-16} (l32 >= 16). Then
+// reduce-scattered across the 32 lanes (31 exchanges instead of 160, all in
+// registers: permlane swaps and DPP, no LDS round trip), which leaves lane
+// l32 with the full S.k of row r_{l32} (l32 < 16) or the full S.q of row
+// r_{l32-16} (l32 >= 16). Then
 //     delta = beta (v - g S.k),   y = g S.q + delta (k.q),   S <- g S + delta k^T
 // (the reference's decay/read/delta/update/output step, gated_delta.py:35-39,
 // with the output taken from the pre-update row).
+//
+// Few sequences (B * Hv below 256 workgroups, a single sequence above all)
+// leave most of the 256 CUs idle, so there a step without the gated norm
+// gives each head kSplit workgroups: split p reads, updates and stores rows
+// [row0, row0 + 128 / kSplit), row0 = p * 128 / kSplit (rows r_i = row0 +
+// 8 i + 2 w + half, i < 16 / kSplit, and a reduce-scatter over 32 / kSplit
+// values per lane on the same butterfly). Each row's arithmetic is the
+// one-workgroup path's, so state and y are the same bits. Every split
+// recomputes the head's front-end (q, k and v are a few hundred channels);
+// the first rolls the conv state. The norm needs the head's 128 outputs
+// together: exchanging them between workgroups (a device-scope release and
+// acquire each) costs more than the split saves, and reading the whole tile
+// in every split races with the in-place update of the other splits' rows,
+// so a step with the norm keeps one workgroup per head.
 #include "gdn_common.h"
 #include "gdn_host.h"
 
@@ -33,6 +48,20 @@ constexpr int kTaps = 4;  // conv kernel K
 #ifndef GDN_DECODE_NT
 #define GDN_DECODE_NT 1
 #endif
+
+// Launches without the gated norm of at most kSplitGroups / 2 (sequence,
+// head) pairs share each head among up to kMaxSplit workgroups (a power of
+// two <= 16).
+#ifndef GDN_DECODE_SPLIT_GROUPS
+#define GDN_DECODE_SPLIT_GROUPS 256
+#endif
+#ifndef GDN_DECODE_MAX_SPLIT
+#define GDN_DECODE_MAX_SPLIT 8
+#endif
+constexpr int64_t kSplitGroups = GDN_DECODE_SPLIT_GROUPS;
+constexpr int kMaxSplit = GDN_DECODE_MAX_SPLIT;
+static_assert(kMaxSplit >= 1 && kMaxSplit <= 16 && (kMaxSplit & (kMaxSplit - 1)) == 0,
+              "GDN_DECODE_MAX_SPLIT: 1, 2, 4, 8 or 16");
 
 // The state is streamed exactly once per launch: optionally mark its loads
 // and stores non-temporal.
@@ -54,21 +83,44 @@ GDN_DEV void store_state(float4* p, float4 v) {
 #endif
 }
 
-// Sum `vals` (32 per lane) over the 32 lanes of each half-wave, leaving the
-// total of original index (lane % 32) in vals[0].
-GDN_DEV void reduce_scatter32(float (&vals)[32], int l32) {
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
+// One reduce-scatter level at partner distance OFF <= 8 over the first n of
+// `vals`: a lane whose bit OFF is set keeps the upper half, the other lane of
+// the pair the lower half, each adding the partner's copy of what it keeps.
+template <int OFF, int n, int N>
+GDN_DEV void scatter_level(float (&vals)[N], int l32) {
+    const uint32_t upper = opaque_mask((l32 & OFF) != 0);
 #pragma unroll
-    for (int step = 0; step < 5; ++step) {
-        const int off = 16 >> step;
-        const int n = 32 >> step;
-        const uint32_t upper = opaque_mask((l32 & off) != 0);
-#pragma unroll
-        for (int j = 0; j < n / 2; ++j) {
-            const float keep = mask_select(upper, vals[j + n / 2], vals[j]);
-            const float send = mask_select(upper, vals[j], vals[j + n / 2]);
-            vals[j] = keep + __shfl_xor(send, off, kWave);
-        }
+    for (int j = 0; j < n / 2; ++j) {
+        const float keep = mask_select(upper, vals[j + n / 2], vals[j]);
+        const float send = mask_select(upper, vals[j], vals[j + n / 2]);
+        vals[j] = keep + dpp_partner<OFF>(send);
     }
+}
+
+// Sum `vals` (N <= 32 per lane, a power of two) over the 32 lanes of each
+// half-wave on one butterfly, partners at levels 16, 8, 4, 2, 1 (lane pairings
+// of group_sum): the first log2(N) levels also halve the values a lane
+// carries (reduce-scatter), the rest add the one left (all-reduce). Lane l32
+// ends with the total of index l32 >> (5 - log2(N)) in vals[0]. Both lanes of
+// a pair add the same two partials, so every total is the same sum tree over
+// the same 32 lane partials, bit for bit, whatever N is.
+template <int N>
+GDN_DEV void reduce_scatter(float (&vals)[N], int l32) {
+    constexpr int kLevels = ilog2(N);
+    static_assert(N >= 2 && N <= 32 && (N & (N - 1)) == 0, "2 to 32 values");
+    // level 16: the swap leaves a lower-row lane its and its partner's lower
+    // half, an upper-row lane the partner's and its upper half
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+        lane_swap<16>(vals[j], vals[j + N / 2]);
+        vals[j] += vals[j + N / 2];
+    }
+    if constexpr (kLevels >= 2) scatter_level<8, N / 2>(vals, l32); else vals[0] = pair_sum<8>(vals[0]);
+    if constexpr (kLevels >= 3) scatter_level<4, N / 4>(vals, l32); else vals[0] = pair_sum<4>(vals[0]);
+    if constexpr (kLevels >= 4) scatter_level<2, N / 8>(vals, l32); else vals[0] = pair_sum<2>(vals[0]);
+    if constexpr (kLevels >= 5) scatter_level<1, N / 16>(vals, l32); else vals[0] = pair_sum<1>(vals[0]);
 }
 
 // One conv channel's inputs: its K = 4 weights, the three conv-state taps and
@@ -106,7 +158,7 @@ GDN_DEV void roll_taps(const ConvTaps& t, typename Act::storage* __restrict__ cs
     Act::store(cso, 2 * C + c, t.x3);
 }
 
-template <class Act, bool kNorm>
+template <class Act, bool kNorm, int kSplit>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const typename Act::storage* __restrict__ qkv, const typename Act::storage* __restrict__ cs_in,
     typename Act::storage* __restrict__ cs_out, const float* __restrict__ conv_w,
@@ -116,22 +168,31 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     float eps, void* __restrict__ out, int y_dtype, int Hk, int Hv,
     const int32_t* __restrict__ slots, int pool, int32_t* conv_half, int32_t* arrivals,
     int64_t qkv_stride, int64_t z_stride, int64_t a_stride, int64_t b_stride) {
+    static_assert(kSplit >= 1 && kSplit <= 16 && (kSplit & (kSplit - 1)) == 0, "kSplit: 1, 2, 4, 8 or 16");
+    static_assert(!kNorm || kSplit == 1, "the gated norm runs one workgroup per head");
+    constexpr int kRows = kD / kSplit;  // state rows per workgroup
+    constexpr int kR = 16 / kSplit;     // state rows per thread
+    constexpr int kN = 2 * kR;          // S.k and S.q partials per thread
     __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
     __shared__ float gate_g, gate_beta, norm_r;
 
     const int C = 2 * Hk * kD + Hv * kD;
-    const int bh = blockIdx.x;
+    const int bh = blockIdx.x / kSplit;
+    const int row0 = (blockIdx.x % kSplit) * kRows;  // this workgroup's first state row
+    const bool first = row0 == 0;
     const int b = bh / Hv, h = bh % Hv;
     const int r = Hv / Hk, hk = h / r;
     const int tid = threadIdx.x;
     const int w = tid >> 6, l = tid & 63, half = l >> 5, l32 = l & 31;
+    typename Act::storage* yo = static_cast<typename Act::storage*>(out);
     // the state slot of batch row b (its state tile is read and written
     // there) and its conv state rows (read at ci, rolled into co): the slot
     // and the batch row, or with conv_half the slot's current and other half
     // of a two-half array; the inputs are read at their row strides
     const int sl = slots ? slots[b] : b;
     if (unsigned(sl) >= unsigned(pool)) {  // a slot outside the pool: touch no state
-        if (tid < kD) store_any(out, size_t(bh) * kD + tid, kNorm ? Act::code : y_dtype, __builtin_nanf(""));
+        if (first && tid < kD)
+            store_any(out, size_t(bh) * kD + tid, kNorm ? Act::code : y_dtype, __builtin_nanf(""));
         return;
     }
     int ci = sl, co = b;
@@ -142,8 +203,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     }
     const size_t sh = size_t(sl) * Hv + h;  // the state tile's index
 
-    // A. the front-end's few inputs first, then the 16 float4 state loads:
-    // waiting for the former does not wait for the latter.
+    // A. the front-end's few inputs first, then the state loads: waiting for
+    // the former does not wait for the latter.
     const typename Act::storage* x = qkv + b * qkv_stride;
     const typename Act::storage* cs = cs_in + size_t(ci) * (kTaps - 1) * C;
     typename Act::storage* cso = cs_out + size_t(co) * (kTaps - 1) * C;
@@ -158,22 +219,31 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const ConvTaps t2 = load_taps<Act>(x, cs, w4, C, c2);
     const float av = Act::load(a_in, b * a_stride + h), bv = Act::load(b_in, b * b_stride + h);
     const float alog = A_log[h], dtb = dt_bias[h];
+    // the gated norm's gate and weight of this thread's output row (needed
+    // last: loaded first, so no load waits at the end)
+    float zz = 0.f, nw = 0.f;
+    if (kNorm && tid < kD) {
+        zz = Act::load(z, b * z_stride + h * kD + tid);
+        nw = norm_w[tid];
+    }
 
     const float4* Sb = reinterpret_cast<const float4*>(S_in + sh * kD * kD);
-    float4 s[16];
+    float4 s[kR];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = load_state(&Sb[(8 * i + 2 * w + half) * (kD / 4) + l32]);
+    for (int i = 0; i < kR; ++i) s[i] = load_state(&Sb[(row0 + 8 * i + 2 * w + half) * (kD / 4) + l32]);
 
     // B. front-end for this head's channels.
     (tid < kD ? qs : ks)[e] = conv_silu<Act>(t1);
     // q/k channels are shared by the r value heads of a key head: the first
-    // of them rolls their conv state.
-    if (h % r == 0) roll_taps<Act>(t1, cso, C, c1);
+    // workgroup of the first of them rolls their conv state.
+    if (first && h % r == 0) roll_taps<Act>(t1, cso, C, c1);
+    // the two gates on two otherwise idle waves, in parallel
     if (tid < kD) {
         vs[e] = conv_silu<Act>(t2);
-        roll_taps<Act>(t2, cso, C, c2);
+        if (first) roll_taps<Act>(t2, cso, C, c2);
     } else if (tid == kD) {
         gate_g = expf(log_forget_gate(av, alog, dtb));
+    } else if (tid == kD + kWave) {
         gate_beta = beta_of(bv, Act::code);
     }
     __syncthreads();
@@ -185,7 +255,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
         float* arr = w == 0 ? qs : ks;
         const float x0 = arr[l], x1 = arr[l + 64];
         const double ss = group_sum<kWave>(double(x0) * x0 + double(x1) * x1);
-        const double rr = 1.0 / sqrt(ss / kD + 1e-6);
+        const double rr = rsqrt(ss / kD + 1e-6);
         const float inv = 1.f / sqrtf(float(kD));
         const float sc = Act::round(w == 0 ? inv * inv : inv);
         arr[l] = Act::round(sc * round_once(x0 * rr, Act::code));
@@ -200,38 +270,39 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const float g = gate_g, beta = gate_beta;
 
     // D/E. partial dots, reduce-scattered over the half-wave.
-    float vals[32];
+    float vals[kN];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kR; ++i) {
         vals[i] = s[i].x * kk.x + s[i].y * kk.y + s[i].z * kk.z + s[i].w * kk.w;
-        vals[16 + i] = s[i].x * qq.x + s[i].y * qq.y + s[i].z * qq.z + s[i].w * qq.w;
+        vals[kR + i] = s[i].x * qq.x + s[i].y * qq.y + s[i].z * qq.z + s[i].w * qq.w;
     }
-    reduce_scatter32(vals, l32);
+    reduce_scatter<kN>(vals, l32);
 
-    // F. per-row delta (lanes < 16) and output (lanes >= 16).
+    // F. per-row delta (lanes < 16) and output (lanes >= 16); with kR < 16
+    // rows, 16 / kR lanes hold each total and write the same value.
     {
-        const int i = l32 & 15;
-        const int row = 8 * i + 2 * w + half;
+        const int idx = l32 >> (5 - ilog2(kN));
+        const int row = row0 + 8 * (idx & (kR - 1)) + 2 * w + half;
         const float tot = vals[0];
         const float delta = (vs[row] - g * tot) * beta;
-        const float delta_pair = __shfl_xor(delta, 16, kWave);
+        float delta_pair = delta, unused = delta;  // lanes >= 16: the partner's delta
+        lane_swap<16>(delta_pair, unused);
         if (l32 < 16) deltas[row] = delta;
         else ys[row] = g * tot + delta_pair * kq;
     }
     __syncthreads();
     // Every thread has read the slot's half bit (its conv loads used it). The
-    // last of the row's Hv workgroups to get here flips it and resets the
-    // count, so the next launch reads the half this one wrote.
-    if (arrivals && tid == 0 && atomicAdd(&arrivals[sl], 1) == Hv - 1) {
+    // last of the row's Hv * kSplit workgroups to get here flips it and resets
+    // the count, so the next launch reads the half this one wrote.
+    if (arrivals && tid == 0 && atomicAdd(&arrivals[sl], 1) == Hv * kSplit - 1) {
         atomicXor(&conv_half[sl], 1);
         atomicExch(&arrivals[sl], 0);
     }
-
     // H. update and store the tile.
     float4* So = reinterpret_cast<float4*>(S_out + sh * kD * kD);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int row = 8 * i + 2 * w + half;
+    for (int i = 0; i < kR; ++i) {
+        const int row = row0 + 8 * i + 2 * w + half;
         const float d = deltas[row];
         float4 o;
         o.x = g * s[i].x + d * kk.x;
@@ -243,7 +314,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
 
     // I. output: y, or the gated RMSNorm of y held in the activation dtype.
     if (!kNorm) {
-        if (tid < kD) store_any(out, size_t(bh) * kD + tid, y_dtype, ys[tid]);
+        if (tid < kRows) store_any(out, size_t(bh) * kD + row0 + tid, y_dtype, ys[row0 + tid]);
         return;
     }
     if (w == 0) {
@@ -254,10 +325,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     __syncthreads();
     if (tid < kD) {
         const float yv = Act::round(ys[tid]);
-        const float normed = Act::round(yv * norm_r * norm_w[tid]);
-        const float zz = Act::load(z, b * z_stride + h * kD + tid);
-        Act::store(static_cast<typename Act::storage*>(out), size_t(bh) * kD + tid,
-                   silu(zz) * normed);
+        const float normed = Act::round(yv * norm_r * nw);
+        Act::store(yo, size_t(bh) * kD + tid, silu(zz) * normed);
     }
 }
 
@@ -313,10 +382,16 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
     GDN_REQUIRE((reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out) |
                  reinterpret_cast<uintptr_t>(conv_weight)) % 16 == 0,
                 "gdn_decode_step: state and conv weight must be 16-byte aligned");
-    const dim3 grid(unsigned(int64_t(B) * Hv)), block(kDecodeThreads);
+    // Below kSplitGroups workgroups a step without the norm shares each head
+    // among up to kMaxSplit workgroups.
+    const int64_t heads = int64_t(B) * Hv;
+    int split = 1;
+    while (!z && split < kMaxSplit && heads * split * 2 <= kSplitGroups) split *= 2;
+    GDN_REQUIRE(heads * split <= INT32_MAX, "gdn_decode_step: B * Hv too large");
+    const dim3 grid(unsigned(heads * split)), block(kDecodeThreads);
     hipStream_t s = as_stream(stream);
-#define GDN_DECODE_LAUNCH(ACT, NORM)                                                          \
-    hipLaunchKernelGGL((decode_kernel<ACT, NORM>), grid, block, 0, s,                         \
+#define GDN_DECODE_LAUNCH(ACT, NORM, SPLIT)                                                   \
+    hipLaunchKernelGGL((decode_kernel<ACT, NORM, SPLIT>), grid, block, 0, s,                  \
                        static_cast<const ACT::storage*>(qkv),                                 \
                        static_cast<const ACT::storage*>(conv_state_in),                       \
                        static_cast<ACT::storage*>(conv_state_out), conv_weight,               \
@@ -324,11 +399,20 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                        A_log, dt_bias, state_in, state_out, static_cast<const ACT::storage*>(z), \
                        norm_weight, norm_eps, out, y_dtype, Hk, Hv, slots, pool, conv_half,         \
                        conv_arrivals, st[0], st[1], st[2], st[3])
-    if (act_dtype == GDN_BF16) {
-        if (z) GDN_DECODE_LAUNCH(ActBF16, true); else GDN_DECODE_LAUNCH(ActBF16, false);
-    } else {
-        if (z) GDN_DECODE_LAUNCH(ActF32, true); else GDN_DECODE_LAUNCH(ActF32, false);
+#define GDN_DECODE_SPLITS(ACT, NORM)                                   \
+    switch (split) {                                                  \
+        case 1: GDN_DECODE_LAUNCH(ACT, NORM, 1); break;               \
+        case 2: GDN_DECODE_LAUNCH(ACT, NORM, 2); break;               \
+        case 4: GDN_DECODE_LAUNCH(ACT, NORM, 4); break;               \
+        case 8: GDN_DECODE_LAUNCH(ACT, NORM, 8); break;               \
+        default: GDN_DECODE_LAUNCH(ACT, NORM, 16); break;             \
     }
+    if (act_dtype == GDN_BF16) {
+        if (z) GDN_DECODE_LAUNCH(ActBF16, true, 1); else GDN_DECODE_SPLITS(ActBF16, false)
+    } else {
+        if (z) GDN_DECODE_LAUNCH(ActF32, true, 1); else GDN_DECODE_SPLITS(ActF32, false)
+    }
+#undef GDN_DECODE_SPLITS
 #undef GDN_DECODE_LAUNCH
     return check_launch("gdn_decode_step");
 }

@@ -33,7 +33,16 @@ def lib():
         _lib.gdn_ref_scan_f32.restype = None
         _lib.gdn_ref_decode_f32.argtypes = [fp] * 12 + [ctypes.c_float, fp] + [i] * 7
         _lib.gdn_ref_decode_f32.restype = None
+        _lib.gdn_ref_bf16_of_double.argtypes = [ctypes.c_double]
+        _lib.gdn_ref_bf16_of_double.restype = ctypes.c_float
     return _lib
+
+
+def bf16_of_double(x) -> np.ndarray:
+    """The C oracle's one rounding of each float64 to bfloat16."""
+
+    f = lib().gdn_ref_bf16_of_double
+    return np.array([f(float(v)) for v in np.asarray(x, np.float64).reshape(-1)], np.float32)
 
 
 def _p(a):

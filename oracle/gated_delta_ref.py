@@ -55,7 +55,8 @@ def bf16_round(x) -> np.ndarray:
     """Round to the nearest bfloat16 (ties to even), once, from the value as
     given; returns float32 values. float64 input is rounded on its own bits
     (8 significant bits kept), not through float32, whose own rounding would
-    otherwise decide values within a float32 ulp of a bf16 tie."""
+    otherwise decide values within a float32 ulp of a bf16 tie; below 2^-126,
+    bfloat16's subnormal range, to a multiple of 2^-133."""
 
     x = np.asarray(x)
     if x.dtype == np.float64:
@@ -64,7 +65,12 @@ def bf16_round(x) -> np.ndarray:
         half = np.uint64((1 << 44) - 1)
         keep = np.uint64(0xFFFF_FFFF_FFFF_FFFF ^ ((1 << 45) - 1))
         u = (u + half + ((u >> drop) & np.uint64(1))) & keep
-        return u.view(np.float64).astype(np.float32)
+        out = u.view(np.float64)
+        with np.errstate(invalid="ignore"):
+            tiny = np.abs(x) < 2.0 ** -126
+        if tiny.any():  # np.rint: nearest, ties to even; the scalings are exact
+            out = np.where(tiny, np.rint(x * 2.0 ** 133) * 2.0 ** -133, out)
+        return np.asarray(out).astype(np.float32)
     x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
     u = x.view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000

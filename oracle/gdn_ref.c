@@ -33,12 +33,15 @@ static float rnd(float x, int act_bf16) { return act_bf16 ? bf16r(x) : x; }
 
 /* One rounding of a double to the activation dtype: float32 by the cast;
  * bfloat16 by rounding the double's own mantissa to 8 significant bits
- * (nearest, ties to even), after which the cast to float is exact. The
+ * (nearest, ties to even), after which the cast to float is exact; below
+ * 2^-126, bfloat16's subnormal range, to a multiple of 2^-133 (rint: ties to
+ * even in the default rounding mode; the scalings are exact). The
  * front-end below evaluates each value the reference rounds to bf16 in
  * double and rounds it once, so a float32 error never decides a rounding
  * boundary (the float64 restatement in gated_delta_ref.py does the same). */
 static float rnd_d(double x, int act_bf16) {
     if (!act_bf16) return (float)x;
+    if (fabs(x) < 0x1p-126) return (float)(rint(x * 0x1p133) * 0x1p-133);
     uint64_t u;
     memcpy(&u, &x, 8);
     u = (u + ((1ull << 44) - 1) + ((u >> 45) & 1)) & ~((1ull << 45) - 1);
@@ -179,3 +182,6 @@ void gdn_ref_decode_f32(const float *qkv, const float *conv_in, float *conv_out,
         }
     }
 }
+
+/* The one-rounding of a double to bfloat16 above, for the tests that pin it. */
+float gdn_ref_bf16_of_double(double x) { return rnd_d(x, 1); }

@@ -1,0 +1,153 @@
+"""GPU tests of the fused decode's row split. With few sequences (B * Hv up
+to 128) a step without the gated norm shares each value head among several
+workgroups, each reading, updating and storing its share of the 128 state
+rows: 8 at B=1, 4 at B=2 and 2 at B=4 for Hv=32. A batch of 8 (B * Hv =
+256) runs one workgroup per head, and decoding the same sequences in it
+gives the reference bits: the split launches must reproduce output, conv
+state and ssm state bit for bit, with the state updated in place. Steps
+with the gated norm keep one workgroup per head at every B (a split reading
+the whole tile would race with the other splits' in-place rows); the same
+comparison covers them. Also checked against the C oracle (gdn_ref.c) at B=1
+and B=4 over chained steps, and on a slot pool whose conv half bits the
+kernel flips (each slot's bit once per step, counted over all the
+workgroups of its heads)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mlx_lean_moe_amd as gdn
+from oracle import cref
+from tests.helpers import assert_bf16_out_close, layer_params, max_rel
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+HK, HV = 16, 32
+DIMS = gdn.LinearAttentionDims(HK, HV, D, D, 4)
+DT = (HK, HV, D, D)
+
+
+def _bf16(x) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).bfloat16().float().numpy()
+
+
+def _case(seed, B, bf16: bool):
+    rng = np.random.default_rng(seed)
+    conv_w, A_log, dt_bias, norm_w = layer_params(rng, DT)
+    f = lambda *s: rng.standard_normal(s, dtype=np.float32)
+    rnd = _bf16 if bf16 else (lambda x: x)
+    return dict(conv_w=conv_w, A_log=A_log, dt_bias=dt_bias, norm_w=norm_w,
+                conv=rnd(f(B, 3, DIMS.conv_dim)), state=f(B, HV, D, D) * np.float32(0.05),
+                steps=[dict(qkv=rnd(f(B, DIMS.conv_dim)), z=rnd(f(B, HV, D)), a=rnd(f(B, HV)),
+                            b=rnd(f(B, HV))) for _ in range(4)])
+
+
+def _dev(x, gpu, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu).to(dtype)
+
+
+def _params(c, gpu):
+    return [_dev(c[k], gpu) for k in ("conv_w", "A_log", "dt_bias", "norm_w")]
+
+
+def _step(x, rows, conv, state, params, gpu, adt, with_z, **kw):
+    """One fused decode step of the sequences ``rows`` (state in place)."""
+
+    return gdn.fused_decode_step(
+        _dev(x["qkv"][rows], gpu, adt), _dev(x["z"][rows], gpu, adt) if with_z else None,
+        _dev(x["a"][rows], gpu, adt), _dev(x["b"][rows], gpu, adt), conv, state, *params[:3],
+        params[3] if with_z else None, 1e-6, DIMS, state_out=state, **kw)
+
+
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+@pytest.mark.parametrize("with_z", [True, False])
+def test_split_launches_match_one_workgroup_per_head_bit_for_bit(gpu, act, with_z):
+    """Sequences 0..B-1 decoded alone (B = 1, 2, 4; without the norm split
+    8, 4, 2) against the same sequences inside the batch of 8, over four
+    chained in-place steps: output, rolled conv state and ssm state
+    identical."""
+
+    bf16 = act == "bf16"
+    adt = torch.bfloat16 if bf16 else torch.float32
+    c = _case(40 + bf16 + 2 * with_z, 8, bf16)
+    params = _params(c, gpu)
+    ref_state, ref_conv = _dev(c["state"], gpu), _dev(c["conv"], gpu, adt)
+    runs = {B: (_dev(c["state"][:B], gpu), _dev(c["conv"][:B], gpu, adt)) for B in (1, 2, 4)}
+    for step, x in enumerate(c["steps"]):
+        ref_out, ref_conv, _ = _step(x, slice(0, 8), ref_conv, ref_state, params, gpu, adt, with_z)
+        for B, (state, conv) in runs.items():
+            out, conv_new, _ = _step(x, slice(0, B), conv, state, params, gpu, adt, with_z)
+            runs[B] = (state, conv_new)
+            assert torch.equal(out, ref_out[:B]), (B, step)
+            assert torch.equal(conv_new, ref_conv[:B]), (B, step)
+            assert torch.equal(state, ref_state[:B]), (B, step)
+
+
+@pytest.mark.parametrize("with_z", [False, True])
+@pytest.mark.parametrize("B", [1, 4])
+def test_split_decode_matches_c_oracle(gpu, B, with_z):
+    """B=1 and B=4 (bf16) over four chained in-place steps against the C
+    oracle: the output (gated norm, or y of the split launches, both in
+    bf16) within max(2e-2, two bf16 ulps), conv state bit for bit, ssm state
+    within 1e-5 of its largest value."""
+
+    c = _case(50 + B + 10 * with_z, B, True)
+    params = _params(c, gpu)
+    state, conv = _dev(c["state"], gpu), _dev(c["conv"], gpu, torch.bfloat16)
+    ref_state, ref_conv = c["state"].copy(), c["conv"].copy()
+    for step, x in enumerate(c["steps"]):
+        out, conv, _ = _step(x, slice(0, B), conv, state, params, gpu, torch.bfloat16, with_z,
+                             y_dtype=torch.bfloat16)
+        out_ref, ref_conv, ref_state = cref.decode_step(
+            x["qkv"], ref_conv, c["conv_w"], x["a"], x["b"], c["A_log"], c["dt_bias"], ref_state,
+            x["z"] if with_z else None, c["norm_w"] if with_z else None, 1e-6, DT, True)
+        assert out.dtype == torch.bfloat16
+        assert_bf16_out_close(out.float().cpu().numpy(), out_ref)
+        np.testing.assert_array_equal(conv.float().cpu().numpy(), ref_conv)
+        assert max_rel(state.cpu().numpy(), ref_state) < 1e-5, step
+
+
+def test_split_decode_on_a_pool_flips_each_slot_once_per_step(gpu):
+    """One slot (B=1, split 8) of a 4-slot pool, then slots 3 and 0 (B=2,
+    split 4), without the norm: the conv state in the pool's two halves, the
+    kernel flipping a decoded slot's bit once all its Hv * split workgroups
+    have read it. Each step's y matches the oracle; the arrival counters end
+    at zero."""
+
+    P = 4
+    c = _case(60, P, True)
+    params = _params(c, gpu)
+    bits0 = np.array([0, 1, 1, 0], np.int32)
+    conv_buf = torch.zeros((2 * P, 3, DIMS.conv_dim), dtype=torch.bfloat16, device=gpu)
+    for s in range(P):
+        conv_buf[s + P * int(bits0[s])] = _dev(c["conv"][s], gpu, torch.bfloat16)
+    state = _dev(c["state"], gpu)
+    half = torch.from_numpy(bits0.copy()).to(gpu)
+    arrivals = torch.zeros(P, dtype=torch.int32, device=gpu)
+    ref_conv, ref_state = c["conv"].copy(), c["state"].copy()
+    flips = np.zeros(P, np.int32)
+    for step, slots in enumerate([[2], [2], [3, 0], [3, 0]]):
+        x = c["steps"][step]
+        idx = np.array(slots)
+        rows = slice(0, len(slots))
+        out, _, _ = gdn.fused_decode_step(
+            _dev(x["qkv"][rows], gpu, torch.bfloat16), None,
+            _dev(x["a"][rows], gpu, torch.bfloat16), _dev(x["b"][rows], gpu, torch.bfloat16),
+            conv_buf, state, *params[:3], None, 1e-6, DIMS,
+            slots=torch.tensor(slots, dtype=torch.int32, device=gpu), conv_half=half,
+            conv_arrivals=arrivals, y_dtype=torch.bfloat16)
+        out_ref, nc, ns = cref.decode_step(
+            x["qkv"][rows], ref_conv[idx], c["conv_w"], x["a"][rows], x["b"][rows], c["A_log"],
+            c["dt_bias"], ref_state[idx], None, None, 1e-6, DT, True)
+        ref_conv[idx], ref_state[idx] = nc, ns
+        flips[idx] ^= 1
+        assert_bf16_out_close(out.float().cpu().numpy(), out_ref)
+        bits = half.cpu().numpy()
+        np.testing.assert_array_equal(bits, bits0 ^ flips)
+        assert not arrivals.any()
+        cur = torch.from_numpy(np.arange(P) + P * bits).to(gpu)
+        np.testing.assert_array_equal(conv_buf[cur].float().cpu().numpy(), ref_conv)
+        assert max_rel(state.cpu().numpy(), ref_state) < 1e-5, step

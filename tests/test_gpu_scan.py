@@ -149,6 +149,26 @@ def test_forget_gate_and_beta_match_oracle(gpu):
                                   R.beta_gate(bb.float().cpu().numpy(), "bf16"))
 
 
+def test_beta_of_every_bf16_input_is_the_rounded_exact_sigmoid(gpu):
+    """All 65 536 bfloat16 bit patterns (NaNs aside) through the gates
+    kernel: each beta is sigmoid(b) evaluated in float64 and rounded once to
+    bfloat16, including the inputs whose float32 sigmoid lands near a
+    bfloat16 rounding boundary (the kernel re-evaluates those in double)."""
+
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    b = (bits << 16).view(np.float32)
+    b = b[np.isfinite(b)]
+    bb = torch.from_numpy(b).to(gpu).to(torch.bfloat16).reshape(-1, 4)
+    got = gdn.beta_gate(bb).float().cpu().numpy().reshape(-1)
+    # (b < -87.3 gives bfloat16 subnormals, multiples of 2^-133)
+    np.testing.assert_array_equal(got, R.beta_gate(b, "bf16"))
+    # the sweep does reach the boundary cases: some float32 sigmoids fall
+    # within 16 float ulps of a bfloat16 midpoint
+    f32 = (1.0 / (1.0 + np.exp(-b.astype(np.float32)))).astype(np.float32)
+    low = f32.view(np.uint32) & 0xFFFF
+    assert int((np.abs(low.astype(np.int64) - 0x8000) <= 16).sum()) > 0
+
+
 def test_varlen_update_matches_per_sequence_oracle(gpu):
     rng = np.random.default_rng(5)
     lens = [3, 0, 1, 17, 8]

@@ -328,6 +328,26 @@ def test_bf16_rounding_of_float64_is_one_rounding():
     assert [float(v) for v in got] == [_bf16_exact(float(v)) for v in x]
 
 
+def test_bf16_rounding_of_float64_below_the_normal_range():
+    """Below 2^-126 bfloat16 holds multiples of 2^-133 (its subnormals):
+    float64 values there, and across the boundary, round like torch's
+    float32 -> bfloat16 conversion of the same (float32-exact) values, in the
+    NumPy and the C oracle alike; sigmoid(-88.5) is one such beta."""
+
+    rng = np.random.default_rng(11)
+    x32 = np.concatenate([
+        (rng.uniform(-1, 1, 3000) * 2.0 ** -126).astype(np.float32),
+        (rng.uniform(0.9, 1.1, 1000) * 2.0 ** -126).astype(np.float32),
+        (np.arange(-600, 600) * 2.0 ** -134).astype(np.float32),  # every tie of the range
+    ])
+    want = torch.from_numpy(x32).to(torch.bfloat16).float().numpy()
+    x = x32.astype(np.float64)
+    np.testing.assert_array_equal(R.bf16_round(x), want)
+    np.testing.assert_array_equal(cref.bf16_of_double(x), want)
+    beta = R.beta_gate(np.array([-88.5], np.float32), "bf16")
+    assert 0 < beta[0] < 2.0 ** -126 and float(beta[0] / 2.0 ** -133).is_integer()
+
+
 # ---------------------------------------------------------------------------
 # the C restatement (timed CPU comparator) agrees with the NumPy oracle
 # ---------------------------------------------------------------------------
