@@ -51,7 +51,7 @@ typedef enum {
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
  * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride,
  * 10 the gated norm's z layout, 11 gdn_quantized_matmul_noalloc, 12 the
- * prefill's float32 q/k/v). */
+ * prefill's float32 q/k/v, 13 gdn_prefill_fused). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -211,6 +211,38 @@ int gdn_prefill_chunked(const void *q, const void *k, const void *v, int qkv_dty
                         float *state_out, void *y, int y_dtype, const int32_t *cu_seqlens,
                         int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv, void *workspace,
                         int64_t workspace_bytes, void *stream);
+
+/*
+ * gdn_prefill_fused - the layer's prefill between the projections, short of
+ * the gated norm: the front-end (conv + SiLU + conv-state roll, q/k scaling,
+ * as gdn_frontend computes them, to the bit) and the chunked prefill, the
+ * front-end done inside the chunk pass (q, k and v go to the workspace for
+ * the state pass only). For N packed runs, bf16 activations.
+ *   qkv: (T_total, C) bfloat16 rows at qkv_stride elements (>= C, a multiple
+ *        of 8), C = (2 Hk + Hv) Dk
+ *   conv_state_in: (N, K-1, C) conv_dtype (GDN_BF16 or GDN_F32);
+ *   conv_state_out: (N, K-1, C) bfloat16, not overlapping conv_state_in
+ *   conv_weight: (C, K) float32
+ *   a, b: (T_total, Hv) gate_dtype at gate_stride (>= Hv) elements per token;
+ *         A_log, dt_bias: (Hv) float32 (the gates as gdn_prefill_chunked's
+ *         gate_mode 0)
+ *   state_in: (N, Hv, Dv, Dk) float32 or NULL (zero); state_out: the same,
+ *             not aliasing state_in
+ *   y: (T_total, Hv, Dv) y_dtype
+ *   workspace: device scratch of gdn_prefill_fused_workspace_size(...) bytes
+ *   qkv, conv states, conv weight, states and workspace 16-byte aligned.
+ * Specialised for Dk = Dv = 128, K = 4. Replaces the layer's conv and
+ * gated_delta_update for a prompt (linear_attention.py:103-121), with the
+ * same results as gdn_frontend followed by gdn_prefill_chunked.
+ */
+int64_t gdn_prefill_fused_workspace_size(int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv);
+int gdn_prefill_fused(const void *qkv, int64_t qkv_stride, const void *conv_state_in,
+                      void *conv_state_out, int conv_dtype, const float *conv_weight, int K,
+                      const void *a, const void *b, int gate_dtype, int64_t gate_stride,
+                      const float *A_log, const float *dt_bias, const float *state_in,
+                      float *state_out, void *y, int y_dtype, const int32_t *cu_seqlens, int N,
+                      int64_t T_total, int Hk, int Hv, int Dk, int Dv, void *workspace,
+                      int64_t workspace_bytes, void *stream);
 
 /*
  * gdn_gated_rmsnorm - out = silu(z) * rms_norm(x, w, eps) with x first rounded

@@ -11,7 +11,7 @@ from .config import QWEN3_5_LINEAR, LinearAttentionDims
 from .gated_delta import (beta_gate, forget_gate, gated_delta_scan, gated_delta_step,
                           gated_delta_update)
 from .linear_attention import (DecodeGraph, PrefillGraph, Qwen3_5LinearAttention, conv_frontend,
-                               fused_decode_step, gated_rms_norm)
+                               fused_decode_step, fused_prefill_ok, gated_rms_norm, prefill_fused)
 from .quant import LinearWeights, QuantScheme, dequantize, quantized_linear
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
 
@@ -30,9 +30,11 @@ __all__ = [
     "dequantize",
     "forget_gate",
     "fused_decode_step",
+    "fused_prefill_ok",
     "gated_delta_scan",
     "gated_delta_step",
     "gated_delta_update",
     "gated_rms_norm",
+    "prefill_fused",
     "quantized_linear",
 ]

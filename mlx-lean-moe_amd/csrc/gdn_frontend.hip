@@ -14,6 +14,7 @@
 #include <type_traits>
 
 #include "gdn_common.h"
+#include "gdn_conv.h"
 #include "gdn_host.h"
 
 namespace gdn {
@@ -101,39 +102,6 @@ constexpr int kTileWaves = 4;    // waves a block, four channel groups each
 
 constexpr int kStateChunk = kTileWaves * kWave * 8;  // conv-state elements a block writes
 
-// silu(x) = x / (1 + e^-x) on the hardware exp2 and reciprocal (about 1 ulp
-// each; the argument's rounding adds under 2^-20 relative for |x| < 16):
-// five instructions against about twenty-five for libm's expf and an IEEE
-// divide, and within a few float ulp of them, far below the bf16 rounding
-// the result gets next.
-GDN_DEV float silu_hw(float x) {
-    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.44269504088896341f));
-}
-
-// Eight consecutive conv-state values at element `at`, rounded to bf16 (the
-// state may be held in any float dtype; `at` is a multiple of 8, the buffer
-// 16-byte aligned).
-template <int kDt>
-GDN_DEV void load_state8(const void* __restrict__ p, int64_t at, float* x) {
-    if constexpr (kDt == GDN_F32) {
-        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + at);
-        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + at + 4);
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = round_bf16(v[e]);
-    } else if constexpr (kDt == GDN_BF16) {
-        unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + at), x);
-    } else {
-        const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + at);
-        const uint32_t d[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[2 * i] = round_bf16(f16_bits_to_f32(uint16_t(d[i] & 0xFFFF)));
-            x[2 * i + 1] = round_bf16(f16_bits_to_f32(uint16_t(d[i] >> 16)));
-        }
-    }
-}
-
 // Tiles of kTileTokens = TT tokens (16, or 8 or 4 for short inputs).
 // grid (n_state + n_tiles, ceil(G / 16)) for G = 2 Hk + Hv channel groups of
 // 128. The first n_state columns write the runs' new conv states, flattened
@@ -209,14 +177,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
         }
     }
     float wr[8][K];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float4 v4 = *reinterpret_cast<const float4*>(w + int64_t(c0 + e) * K);
-        wr[e][0] = round_bf16(v4.x);
-        wr[e][1] = round_bf16(v4.y);
-        wr[e][2] = round_bf16(v4.z);
-        wr[e][3] = round_bf16(v4.w);
-    }
+    load_conv_w8(w, c0, wr);
 
     const float inv = 1.f / sqrtf(float(D));
     const float sc = g < Hk ? round_bf16(inv * inv) : round_bf16(inv);
@@ -245,29 +206,10 @@ __global__ __launch_bounds__(kTileWaves * kWave) void frontend_tiled_kernel(
         unpack8(raw[i % kAhead], x);
         if (i + kAhead < kTileTokens) raw[i % kAhead] = row_at(i + kAhead);
         float o[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 0; j < S; ++j) acc += wr[e][j] * win[j][e];
-            o[e] = acc + wr[e][S] * x[e];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) round_bf16x2(o[e], o[e + 1]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = silu_hw(o[e]);
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) round_bf16x2(o[e], o[e + 1]);
+        conv_silu8(wr, win, x, o);
         if (qk_wave) {  // q and k heads: scaled RMS norm (v lanes keep o)
-            float ss = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss += o[e] * o[e];
-            const float r = __builtin_amdgcn_rsqf(row16_sum(ss) / float(D) + 1e-6f);
             float n[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) n[e] = o[e] * r;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) round_bf16x2(n[e], n[e + 1]);
+            rms_norm8(o, n);
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = is_v ? o[e] : sc * n[e];
         }

@@ -28,6 +28,7 @@
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+j],
 // B[8(l/16)+j][l%16] (j = 0..7) and D[4(l/16)+i][l%16] (i = 0..3).
 #include "gdn_common.h"
+#include "gdn_conv.h"
 #include "gdn_host.h"
 
 namespace gdn {
@@ -248,15 +249,41 @@ GDN_DEV void offdiag_inverse(float* As, float* Ts, int w, int l) {
 // (chunk, key head) take ids 8 apart: same XCD, dispatched together, so all
 // but the first read that chunk's K and Q from the XCD's L2.
 //
-// kF32: q and k are float32, entering the MFMAs as bf16 high parts plus
+// The raw projection rows and conv parameters of the fused chunk pass, which
+// computes q, k and v itself (the prefill front-end, linear_attention.py:61-79,
+// 103-113) and leaves them for the state pass.
+struct ConvIn {
+    const uint16_t* qkv;      // (T, qs) bf16: the q, k and v channels of each token
+    int64_t qs;               // qkv row stride (elements)
+    const void* cs_in;        // (N, K-1, C) conv states, in the kernel's conv dtype
+    uint16_t* cs_out;         // (N, K-1, C) new conv states, bf16
+    const float* w;           // (C, K) conv weights
+    uint16_t *qo, *ko, *vo;   // (T, Hk, 128), (T, Hk, 128), (T, Hv, 128) bf16
+};
+
+// The inputs of the chunk pass: bf16 q and k, float32 q and k, or (fused)
+// the raw projection rows and a conv state in bf16 or float32.
+constexpr int kInBF16 = 0, kInF32 = 1, kInConvBF16 = 2, kInConvF32 = 3;
+
+// kInF32: q and k are float32, entering the MFMAs as bf16 high parts plus
 // residuals (hi.hi + hi.lo + lo.hi), with two more LDS tiles for the
-// residuals; otherwise bf16, used as they are.
-template <bool kF32>
+// residuals; kInBF16: bf16, used as they are. kInConv*: each workgroup runs
+// the front-end for its chunk's q and k with the arithmetic of the tiled
+// front-end kernel (conv, SiLU, the scaled RMS norm, the same bits): thread
+// (group g: q or k, rows 8 rg .. 8 rg + 7, channels 8 seg .. 8 seg + 7) walks
+// its rows with the previous three in registers (a run's first rows take
+// them from its conv state) into the K / Q tiles; the first value head of
+// each key head also stores q and k for the state pass (v: conv_v_block).
+// `id` is the workgroup's index in the (chunk, head) order below.
+template <int kIn>
 GDN_DEV void prefill_chunk_body(
     const void* __restrict__ q_in, const void* __restrict__ k_in, const void* __restrict__ ga,
     const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
-    int Hk, int Hv) {
+    int Hk, int Hv, ConvIn cv = {}, int id = -1) {
+    constexpr bool kF32 = kIn == kInF32;
+    constexpr bool kConv = kIn == kInConvBF16 || kIn == kInConvF32;
+    constexpr int kConvDt = kIn == kInConvF32 ? GDN_F32 : GDN_BF16;
     // K/Q tiles first; once K K^T and K Q^T are in registers the same bytes
     // hold the A and T matrices.
     __shared__ __attribute__((aligned(16))) char smem[(kF32 ? 4 : 2) * kChunk * kKS * 2];
@@ -269,7 +296,8 @@ GDN_DEV void prefill_chunk_body(
     float* Ts = As + kChunk * kFS;
 
     const int r = Hv / Hk;
-    const int id = blockIdx.x, e = (id >> 3) % r;
+    if (id < 0) id = blockIdx.x;
+    const int e = (id >> 3) % r;
     const int item = (id / (8 * r)) * 8 + (id & 7);  // (chunk, key head)
     const int g = item / Hk, hk = item % Hk, hv = hk * r + e;
     if (g >= rl.total()) return;
@@ -280,17 +308,41 @@ GDN_DEV void prefill_chunk_body(
     // K and Q of the chunk: every load issued before the first LDS store
     // (rows past the run are read clamped and stored as zero).
     u16x8 kv[4], qv[4], kvl[4], qvl[4];
+    // fused: this thread's raw rows, the three before them and its weights
+    const int cgrp = tid >> 7, crg = (tid >> 4) & 7, cseg = tid & 15;
+    const int C = (2 * Hk + Hv) * kHD;
+    uint4 raw[8];
+    float win[3][8], wr[8][4];
+    if constexpr (kConv) {
+        const int64_t c0 = int64_t(cgrp * Hk + hk) * kHD + cseg * 8;
+        const int64_t rs = rl.start(pos.run), last = rl.end(pos.run) - 1;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int row = (tid + 256 * it) >> 4, seg = tid & 15;
-        const int rc = row < pos.len ? row : pos.len - 1;
-        const int64_t off = ((pos.t0 + rc) * Hk + hk) * kHD + seg * 8;
-        if constexpr (kF32) {
-            load_split8(static_cast<const float*>(k_in) + off, kv[it], kvl[it]);
-            load_split8(static_cast<const float*>(q_in) + off, qv[it], qvl[it]);
-        } else {
-            kv[it] = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(k_in) + off);
-            qv[it] = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(q_in) + off);
+        for (int i = 0; i < 8; ++i) {
+            const int64_t t = pos.t0 + 8 * crg + i;
+            raw[i] = *reinterpret_cast<const uint4*>(cv.qkv + (t < last ? t : last) * cv.qs + c0);
+        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int64_t t = pos.t0 + 8 * crg - 3 + j;
+            if (t >= rs)
+                unpack8(*reinterpret_cast<const uint4*>(cv.qkv + (t < last ? t : last) * cv.qs + c0), win[j]);
+            else  // row t - rs + 3 of the run's conv state
+                load_state8<kConvDt>(cv.cs_in, (int64_t(pos.run) * 3 + (t - rs + 3)) * C + c0, win[j]);
+        }
+        load_conv_w8(cv.w, c0, wr);
+    } else {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int row = (tid + 256 * it) >> 4, seg = tid & 15;
+            const int rc = row < pos.len ? row : pos.len - 1;
+            const int64_t off = ((pos.t0 + rc) * Hk + hk) * kHD + seg * 8;
+            if constexpr (kF32) {
+                load_split8(static_cast<const float*>(k_in) + off, kv[it], kvl[it]);
+                load_split8(static_cast<const float*>(q_in) + off, qv[it], qvl[it]);
+            } else {
+                kv[it] = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(k_in) + off);
+                qv[it] = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(q_in) + off);
+            }
         }
     }
     // Gates (wave 0, lane = token): l2 = inclusive prefix sum of log2 g
@@ -320,15 +372,43 @@ GDN_DEV void prefill_chunk_body(
         reinterpret_cast<float*>(rec + kRecEl)[l] = exp2f(lg);
         reinterpret_cast<float*>(rec + kRecEd)[l] = exp2f(lC - lg);
     }
+    if constexpr (kConv) {
+        // conv, SiLU and the scaled norm of rows 8 crg .. 8 crg + 7 into the
+        // tile; the first value head of the key head also stores them
+        const float inv = 1.f / sqrtf(float(kHD));
+        const float sc = cgrp == 0 ? round_bf16(inv * inv) : round_bf16(inv);
+        uint16_t* tile = cgrp == 0 ? Qs : Ks;
+        uint16_t* out = (cgrp == 0 ? cv.qo : cv.ko) + int64_t(hk) * kHD + cseg * 8;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int row = (tid + 256 * it) >> 4, seg = tid & 15;
-        const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-        *reinterpret_cast<u16x8*>(Ks + row * kKS + seg * 8) = row < pos.len ? kv[it] : z;
-        *reinterpret_cast<u16x8*>(Qs + row * kKS + seg * 8) = row < pos.len ? qv[it] : z;
-        if constexpr (kF32) {
-            *reinterpret_cast<u16x8*>(Ks_lo + row * kKS + seg * 8) = row < pos.len ? kvl[it] : z;
-            *reinterpret_cast<u16x8*>(Qs_lo + row * kKS + seg * 8) = row < pos.len ? qvl[it] : z;
+        for (int i = 0; i < 8; ++i) {
+            const int row = 8 * crg + i;
+            float x[8], o[8], n[8];
+            unpack8(raw[i], x);
+            conv_silu8(wr, win, x, o);
+            rms_norm8(o, n);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = sc * n[e];
+            const uint4 p = pack8(o);
+            *reinterpret_cast<uint4*>(tile + row * kKS + cseg * 8) = row < pos.len ? p : make_uint4(0, 0, 0, 0);
+            if (e == 0 && row < pos.len) *reinterpret_cast<uint4*>(out + (pos.t0 + row) * Hk * kHD) = p;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                win[0][j] = win[1][j];
+                win[1][j] = win[2][j];
+                win[2][j] = x[j];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int row = (tid + 256 * it) >> 4, seg = tid & 15;
+            const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            *reinterpret_cast<u16x8*>(Ks + row * kKS + seg * 8) = row < pos.len ? kv[it] : z;
+            *reinterpret_cast<u16x8*>(Qs + row * kKS + seg * 8) = row < pos.len ? qv[it] : z;
+            if constexpr (kF32) {
+                *reinterpret_cast<u16x8*>(Ks_lo + row * kKS + seg * 8) = row < pos.len ? kvl[it] : z;
+                *reinterpret_cast<u16x8*>(Qs_lo + row * kKS + seg * 8) = row < pos.len ? qvl[it] : z;
+            }
         }
     }
     __syncthreads();
@@ -414,13 +494,84 @@ GDN_DEV void prefill_chunk_body(
                     reinterpret_cast<uint16_t*>(rec + kRecTbLo), beta_sh, tid, 256);
 }
 
+// The fused chunk pass's v part, done by each chunk workgroup after its
+// records: the front-end of chunk g's v channels of value head hv, for the
+// state pass (SiLU(conv), no norm), thread (rows 4 rg .. 4 rg + 3, channels
+// 8 seg ..). (Separate v workgroups interleaved with the chunk workgroups
+// were slower: 84 against 64 us at T=4096, as they take the LDS-limited
+// workgroup slots.) The workgroups of a run's last chunk also write the
+// run's new conv state (row j: row len + j of concat(state, tokens)): the v
+// channels of hv, and with the first value head the q and k channels of hk;
+// 48 pieces of 8 channels a group.
+template <int kConvDt>
+GDN_DEV void conv_v_block(RunLayout rl, const ConvIn& cv, int id, int Hk, int Hv) {
+    const int r = Hv / Hk, e = (id >> 3) % r;
+    const int item = (id / (8 * r)) * 8 + (id & 7);  // (chunk, key head)
+    const int g = item / Hk, hk = item % Hk, hv = hk * r + e;
+    if (g >= rl.total()) return;
+    const ChunkPos pos = locate_chunk(rl, g);
+    const int tid = threadIdx.x;
+    const int C = (2 * Hk + Hv) * kHD;
+    float win[3][8], wr[8][4];
+    const int vrg = tid >> 4, vseg = tid & 15;
+    const int64_t c0 = int64_t(2 * Hk + hv) * kHD + vseg * 8;
+    const int64_t rs = rl.start(pos.run), last = rl.end(pos.run) - 1;
+    uint4 vraw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t t = pos.t0 + 4 * vrg + i;
+        vraw[i] = *reinterpret_cast<const uint4*>(cv.qkv + (t < last ? t : last) * cv.qs + c0);
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int64_t t = pos.t0 + 4 * vrg - 3 + j;
+        if (t >= rs)
+            unpack8(*reinterpret_cast<const uint4*>(cv.qkv + (t < last ? t : last) * cv.qs + c0), win[j]);
+        else
+            load_state8<kConvDt>(cv.cs_in, (int64_t(pos.run) * 3 + (t - rs + 3)) * C + c0, win[j]);
+    }
+    load_conv_w8(cv.w, c0, wr);
+    uint16_t* out = cv.vo + int64_t(hv) * kHD + vseg * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * vrg + i;
+        float x[8], o[8];
+        unpack8(vraw[i], x);
+        conv_silu8(wr, win, x, o);
+        if (row < pos.len) *reinterpret_cast<uint4*>(out + (pos.t0 + row) * Hv * kHD) = pack8(o);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            win[0][j] = win[1][j];
+            win[1][j] = win[2][j];
+            win[2][j] = x[j];
+        }
+    }
+    if (pos.t0 + pos.len == rl.end(pos.run)) {  // the run's last chunk: its new conv state
+        const int64_t len = rl.end(pos.run) - rs;
+        const int grp = tid / 48, pc = tid % 48, j = pc / 16, sg = pc % 16;
+        if (grp < 3 && (grp == 2 || e == 0)) {
+            const int64_t ch = (grp == 2 ? int64_t(2 * Hk + hv) : int64_t(grp * Hk + hk)) * kHD + sg * 8;
+            const int64_t idx = len + j;  // in concat(state, tokens)
+            uint4 v;
+            if (idx < 3) {
+                float x[8];
+                load_state8<kConvDt>(cv.cs_in, (int64_t(pos.run) * 3 + idx) * C + ch, x);
+                v = pack8(x);
+            } else {
+                v = *reinterpret_cast<const uint4*>(cv.qkv + (rs + idx - 3) * cv.qs + ch);
+            }
+            *reinterpret_cast<uint4*>(cv.cs_out + (int64_t(pos.run) * 3 + j) * C + ch) = v;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_chunk_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ ga,
     const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
     int Hk, int Hv) {
-    prefill_chunk_body<false>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
-                              records, Hk, Hv);
+    prefill_chunk_body<kInBF16>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
+                                records, Hk, Hv);
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_chunk_f32_kernel(
@@ -428,8 +579,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
     int Hk, int Hv) {
-    prefill_chunk_body<true>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
-                             records, Hk, Hv);
+    prefill_chunk_body<kInF32>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
+                               records, Hk, Hv);
+}
+
+// The fused chunk pass: the front-end (bf16 projection rows, conv state in
+// bf16 or float32) and the chunk pass in one launch; each workgroup ends
+// with the v channels of its (chunk, value head).
+template <int kConvDt>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_chunk_conv_kernel(
+    const void* __restrict__ ga, const void* __restrict__ gb, int gb_dtype, int64_t gate_stride,
+    const float* __restrict__ A_log, const float* __restrict__ dt_bias, RunLayout rl,
+    char* __restrict__ records, int Hk, int Hv, ConvIn cv) {
+    prefill_chunk_body<kConvDt == GDN_F32 ? kInConvF32 : kInConvBF16>(
+        nullptr, nullptr, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, 0, rl, records, Hk, Hv, cv);
+    conv_v_block<kConvDt>(rl, cv, blockIdx.x, Hk, Hv);
+}
+
+// The new conv state of each empty run (no chunk writes it): its old state,
+// rounded to bf16. One block per run.
+template <int kConvDt>
+__global__ __launch_bounds__(256) void conv_state_empty_runs_kernel(RunLayout rl, ConvIn cv, int C) {
+    const int run = blockIdx.x;
+    if (rl.end(run) != rl.start(run)) return;
+    for (int64_t i = threadIdx.x * 8; i < 3 * int64_t(C); i += 256 * 8) {
+        float x[8];
+        load_state8<kConvDt>(cv.cs_in, int64_t(run) * 3 * C + i, x);
+        *reinterpret_cast<uint4*>(cv.cs_out + int64_t(run) * 3 * C + i) = pack8(x);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1044,4 +1221,116 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     }
 #undef GDN_STATE_LAUNCH
     return check_launch("gdn_prefill_chunked/state");
+}
+
+namespace {
+
+// The fused prefill's q, k and v (bf16) follow the chunked prefill's workspace.
+int64_t fused_qkv_offset(int N, int64_t T_total, int Hv) {
+    return (records_offset(N) + chunks_bound(T_total, N) * Hv * kRecBytes + 255) & ~int64_t(255);
+}
+
+}  // namespace
+
+extern "C" int64_t gdn_prefill_fused_workspace_size(int N, int64_t T_total, int Hk, int Hv, int Dk, int Dv) {
+    if (N <= 0 || T_total < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk)
+        return fail(GDN_EINVAL, "gdn_prefill_fused_workspace_size: bad sizes");
+    if (Dk != kHD || Dv != kHD)
+        return fail(GDN_EUNSUPPORTED, "gdn_prefill_fused_workspace_size: specialised for Dk=Dv=128");
+    return fused_qkv_offset(N, T_total, Hv) + T_total * (2LL * Hk + Hv) * kHD * 2;
+}
+
+extern "C" int gdn_prefill_fused(const void* qkv, int64_t qkv_stride, const void* conv_state_in,
+                                 void* conv_state_out, int conv_dtype, const float* conv_weight, int K,
+                                 const void* a, const void* b, int gate_dtype, int64_t gate_stride,
+                                 const float* A_log, const float* dt_bias, const float* state_in,
+                                 float* state_out, void* y, int y_dtype, const int32_t* cu_seqlens, int N,
+                                 int64_t T_total, int Hk, int Hv, int Dk, int Dv, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+    GDN_REQUIRE(N > 0 && T_total >= 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, "gdn_prefill_fused: bad sizes");
+    if (Dk != kHD || Dv != kHD || K != 4)
+        return fail(GDN_EUNSUPPORTED, "gdn_prefill_fused: specialised for Dk=Dv=128, K=4 (got %d, %d, %d)",
+                    Dk, Dv, K);
+    if (conv_dtype != GDN_BF16 && conv_dtype != GDN_F32)
+        return fail(GDN_EUNSUPPORTED, "gdn_prefill_fused: conv state must be bfloat16 or float32");
+    GDN_REQUIRE(valid_dtype(gate_dtype) && valid_dtype(y_dtype), "gdn_prefill_fused: bad dtype");
+    GDN_REQUIRE(gate_stride >= Hv, "gdn_prefill_fused: gate_stride %lld below Hv=%d", (long long)gate_stride,
+                Hv);
+    GDN_REQUIRE(cu_seqlens || T_total % N == 0, "gdn_prefill_fused: T_total not divisible by N");
+    GDN_REQUIRE(T_total < (int64_t(1) << 31), "gdn_prefill_fused: token count must fit int32");
+    const int64_t C = (2LL * Hk + Hv) * kHD;
+    GDN_REQUIRE(qkv_stride >= C && qkv_stride % 8 == 0,
+                "gdn_prefill_fused: qkv_stride %lld must be at least conv_dim %lld and a multiple of 8",
+                (long long)qkv_stride, (long long)C);
+    GDN_REQUIRE(state_out && conv_state_in && conv_state_out && conv_weight && A_log && dt_bias,
+                "gdn_prefill_fused: null pointer");
+    GDN_REQUIRE(T_total == 0 || (qkv && a && b && y), "gdn_prefill_fused: null pointer");
+    const auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    GDN_REQUIRE(al(qkv) && al(conv_state_in) && al(conv_state_out) && al(conv_weight) && al(state_in) &&
+                    al(state_out) && al(workspace),
+                "gdn_prefill_fused: qkv, conv states, conv weight, states and workspace must be 16-byte aligned");
+    const int64_t qkv_off = fused_qkv_offset(N, T_total, Hv);
+    const int64_t need = qkv_off + T_total * C * 2;
+    GDN_REQUIRE(workspace && workspace_bytes >= need, "gdn_prefill_fused: workspace of %lld bytes, need %lld",
+                (long long)workspace_bytes, (long long)need);
+    const int64_t cb = int64_t(N) * 3 * C;
+    GDN_REQUIRE(!overlaps(conv_state_in, cb * dtype_size(conv_dtype), conv_state_out, cb * 2),
+                "gdn_prefill_fused: conv_state_out overlaps conv_state_in");
+    GDN_REQUIRE(state_in != state_out, "gdn_prefill_fused: state_out must not alias state_in");
+    if (state_in) {
+        const int64_t sb = int64_t(N) * Hv * kHD * kHD * 4;
+        GDN_REQUIRE(!overlaps(state_in, sb, state_out, sb), "gdn_prefill_fused: states overlap");
+    }
+
+    hipStream_t s = as_stream(stream);
+    RunLayout rl;
+    rl.cu = cu_seqlens;
+    rl.N = N;
+    rl.L_uniform = cu_seqlens ? 0 : T_total / N;
+    rl.cpr = int((rl.L_uniform + kChunk - 1) / kChunk);
+    rl.chunk_off = nullptr;
+    char* ws = static_cast<char*>(workspace);
+    char* records = ws + records_offset(N);
+    if (cu_seqlens) {
+        int32_t* chunk_off = reinterpret_cast<int32_t*>(ws);
+        hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(64), 0, s, cu_seqlens, N, chunk_off);
+        if (int rc = check_launch("gdn_prefill_fused/offsets")) return rc;
+        rl.chunk_off = chunk_off;
+    }
+    ConvIn cv;
+    cv.qkv = static_cast<const uint16_t*>(qkv);
+    cv.qs = qkv_stride;
+    cv.cs_in = conv_state_in;
+    cv.cs_out = static_cast<uint16_t*>(conv_state_out);
+    cv.w = conv_weight;
+    cv.qo = reinterpret_cast<uint16_t*>(ws + qkv_off);
+    cv.ko = cv.qo + T_total * Hk * kHD;
+    cv.vo = cv.ko + T_total * Hk * kHD;
+    const int64_t items = (chunks_bound(T_total, N) * Hk + 7) / 8 * 8;
+    const dim3 cgrid(unsigned(items * (Hv / Hk)));
+    if (conv_dtype == GDN_F32)
+        hipLaunchKernelGGL(prefill_chunk_conv_kernel<GDN_F32>, cgrid, dim3(256), 0, s, a, b, gate_dtype,
+                           gate_stride, A_log, dt_bias, rl, records, Hk, Hv, cv);
+    else
+        hipLaunchKernelGGL(prefill_chunk_conv_kernel<GDN_BF16>, cgrid, dim3(256), 0, s, a, b, gate_dtype,
+                           gate_stride, A_log, dt_bias, rl, records, Hk, Hv, cv);
+    if (int rc = check_launch("gdn_prefill_fused/chunk")) return rc;
+    if (cu_seqlens || T_total == 0) {  // runs without tokens keep their conv state
+        if (conv_dtype == GDN_F32)
+            hipLaunchKernelGGL(conv_state_empty_runs_kernel<GDN_F32>, dim3(unsigned(N)), dim3(256), 0, s, rl, cv,
+                               int(C));
+        else
+            hipLaunchKernelGGL(conv_state_empty_runs_kernel<GDN_BF16>, dim3(unsigned(N)), dim3(256), 0, s, rl,
+                               cv, int(C));
+        if (int rc = check_launch("gdn_prefill_fused/conv_state")) return rc;
+    }
+    const dim3 sgrid(unsigned(int64_t(N) * Hv * kSlices));
+#define GDN_STATE_LAUNCH(YT)                                                                            \
+    hipLaunchKernelGGL((prefill_state_kernel<YT, false>), sgrid, dim3(kStateThreads), 0, s, cv.qo, cv.ko, \
+                       cv.vo, state_in, state_out, static_cast<YT::storage*>(y), rl, records, Hk, Hv)
+    if (y_dtype == GDN_F32) GDN_STATE_LAUNCH(ActF32);
+    else if (y_dtype == GDN_BF16) GDN_STATE_LAUNCH(ActBF16);
+    else GDN_STATE_LAUNCH(ActF16);
+#undef GDN_STATE_LAUNCH
+    return check_launch("gdn_prefill_fused/state");
 }

@@ -29,8 +29,8 @@ import torch
 
 from . import _lib
 from .config import LinearAttentionDims
-from .gated_delta import (_c, _check_cu_seqlens, _check_out, _require_device, _stream,
-                          gated_delta_update)
+from .gated_delta import (PREFILL_MIN_TOKENS, _c, _check_cu_seqlens, _check_out, _require_device,
+                          _stream, gated_delta_update)
 from .quant import (LinearWeights, QuantScheme, concat_quantized, quantized_linear,
                     quantized_linear_split)
 from .recurrent_cache import RecurrentCache, RecurrentStatePool
@@ -110,6 +110,87 @@ def conv_frontend(qkv: torch.Tensor, conv_state: torch.Tensor, conv_weight: torc
               _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), dims.num_key_heads, dims.num_value_heads,
               dims.key_head_dim, dims.value_head_dim, K, _lib.dtype_code(act), _stream(device))
     return q, k, v, new_conv
+
+
+def fused_prefill_ok(qkv, a, b, conv_state, ssm_state, dims: LinearAttentionDims, N: int) -> bool:
+    """Whether :func:`prefill_fused` takes these operands: bf16 activations,
+    Dk = Dv = 128, K = 4, a bf16 or float32 conv state, a float32 ssm state,
+    a and b of one dtype (bf16 or float32), and runs long enough (on
+    average) for the chunked prefill, i.e. the inputs for which
+    ``conv_frontend`` and ``gated_delta_update`` take the tiled front-end and
+    the chunked prefill."""
+
+    T = qkv.shape[0]
+    return (qkv.dtype == torch.bfloat16 and dims.key_head_dim == 128
+            and dims.value_head_dim == 128 and dims.conv_kernel_dim == 4
+            and conv_state.dtype in (torch.bfloat16, torch.float32)
+            and ssm_state.dtype == torch.float32 and a.dtype == b.dtype
+            and a.dtype in (torch.bfloat16, torch.float32)
+            and T > 0 and T / N >= PREFILL_MIN_TOKENS)
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def prefill_fused(qkv, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias,
+                  dims: LinearAttentionDims, cu_seqlens=None, *, y_dtype=None, conv_out=None,
+                  state_out=None):
+    """The layer's prompt path between the projections, short of the gated
+    norm, in one call: the front-end of :func:`conv_frontend` computed
+    inside the chunked prefill's chunk pass, then the state pass
+    (linear_attention.py:103-121). The same results, to the bit, as
+    ``conv_frontend`` followed by ``gated_delta_update`` on these inputs
+    (:func:`fused_prefill_ok` says which).
+
+    ``qkv (T, C)`` bf16 (a column view of a stacked projection output is
+    read in place), ``a, b (T, Hv)``, ``conv_state (N, K-1, C)``,
+    ``ssm_state (N, Hv, Dv, Dk)`` float32, ``cu_seqlens`` as in
+    :func:`conv_frontend`. Returns ``(y (T, Hv, Dv), new_conv (N, K-1, C)
+    bf16, new_ssm)``, y in ``y_dtype`` (float32 by default); the new states
+    go to ``conv_out`` / ``state_out`` when given."""
+
+    device = _require_device(qkv, a, b, conv_state, ssm_state, conv_weight, A_log, dt_bias)
+    T, C = qkv.shape
+    N = conv_state.shape[0]
+    Hk, Hv, D, K = (dims.num_key_heads, dims.num_value_heads, dims.value_head_dim,
+                    dims.conv_kernel_dim)
+    if C != dims.conv_dim or tuple(conv_state.shape[1:]) != (K - 1, C):
+        raise ValueError("qkv/conv_state do not match the layer's conv_dim and kernel")
+    if a.shape != (T, Hv) or b.shape != a.shape or tuple(ssm_state.shape) != (N, Hv, D, D):
+        raise ValueError("prefill_fused: inconsistent shapes")
+    if not fused_prefill_ok(qkv, a, b, conv_state, ssm_state, dims, N):
+        raise ValueError("prefill_fused needs bf16 activations, Dk = Dv = 128, K = 4, a bf16 or "
+                         "float32 conv state, a float32 ssm state and runs of at least "
+                         f"{PREFILL_MIN_TOKENS} tokens on average")
+    cu = _runs_on_device(cu_seqlens, N, T, device)
+    if not (qkv.stride(1) == 1 and qkv.stride(0) >= C and qkv.stride(0) % 8 == 0
+            and qkv.data_ptr() % 16 == 0):
+        qkv = qkv.contiguous()
+    conv_state, ssm_in = _aligned(_c(conv_state)), _aligned(_c(ssm_state))
+    w = _aligned(_c(conv_weight.float().reshape(C, K)))
+    if not (a.stride() == b.stride() and a.stride(1) == 1 and a.stride(0) >= Hv):
+        a, b = _c(a), _c(b)
+    y = torch.empty((T, Hv, D), dtype=y_dtype or torch.float32, device=device)
+    if conv_out is None:
+        conv_out = torch.empty((N, K - 1, C), dtype=torch.bfloat16, device=device)
+    else:
+        _check_out(conv_out, (N, K - 1, C), torch.bfloat16, device, conv_state, "conv_out")
+    if state_out is None:
+        state_out = torch.empty_like(ssm_in)
+    else:
+        _check_out(state_out, (N, Hv, D, D), torch.float32, device, ssm_in, "state_out")
+    nbytes = int(_lib.load().gdn_prefill_fused_workspace_size(N, T, Hk, Hv, D, D))
+    if nbytes < 0:
+        raise RuntimeError("gdn_prefill_fused_workspace_size: " + _lib.load().gdn_last_error().decode())
+    workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    _lib.call("gdn_prefill_fused", _lib.ptr(qkv), qkv.stride(0), _lib.ptr(conv_state),
+              _lib.ptr(conv_out), _lib.dtype_code(conv_state.dtype), _lib.ptr(w), K, _lib.ptr(a),
+              _lib.ptr(b), _lib.dtype_code(a.dtype), a.stride(0), _lib.ptr(_c(A_log.float())),
+              _lib.ptr(_c(dt_bias.float())), _lib.ptr(ssm_in), _lib.ptr(state_out), _lib.ptr(y),
+              _lib.dtype_code(y.dtype), _lib.ptr(cu), N, T, Hk, Hv, D, D, _lib.ptr(workspace),
+              workspace.numel(), _stream(device))
+    return y, conv_out, state_out
 
 
 def _runs_on_device(cu_seqlens, N: int, T: int, device) -> torch.Tensor | None:
@@ -408,6 +489,15 @@ class Qwen3_5LinearAttention:
         # the first launch (each launch below checks the host list again)
         if cu_seqlens is not None:
             cu_seqlens = _check_cu_seqlens(cu_seqlens, T)
+        N = conv_state.shape[0]
+        if fused_prefill_ok(qkv, a, b, conv_state, ssm_state, d, N):
+            # front-end inside the chunk pass: the same bits, no q/k/v round trip
+            y, new_conv, new_ssm = prefill_fused(qkv, a, b, conv_state, ssm_state,
+                                                 self.conv1d_weight, self.A_log, self.dt_bias, d,
+                                                 cu_seqlens, y_dtype=z.dtype, conv_out=conv_out,
+                                                 state_out=ssm_out)
+            out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out_dtype=z.dtype)
+            return out.reshape(T, d.value_dim), new_conv, new_ssm
         q, k, v, new_conv = conv_frontend(qkv, conv_state, self.conv1d_weight, d, cu_seqlens,
                                           conv_out=conv_out)
         # y straight in z's dtype: the norm's first step rounds it there

@@ -115,3 +115,38 @@ def test_quantized_matmul_workspace_size():
     rc = lib.gdn_quantized_matmul(p, bf, p, p, p, bf, ctypes.c_void_p(1 << 31), bf, None, 1, 64, 512, 4,
                                   64, ctypes.c_void_p((1 << 32) + 8), 1024, None)
     assert rc == _lib.GDN_EINVAL and "workspace" in _err(lib)
+
+
+def test_fused_prefill_workspace_and_argument_checks():
+    """gdn_prefill_fused's workspace is the chunked prefill's plus bf16 q, k
+    and v, and every argument it cannot take is refused before a launch."""
+
+    lib = _lib.load()
+    N, T, Hk, Hv = 1, 4096, 16, 32
+    base = lib.gdn_prefill_workspace_size(N, T, Hk, Hv, 128, 128)
+    fused = lib.gdn_prefill_fused_workspace_size(N, T, Hk, Hv, 128, 128)
+    assert fused >= base + T * (2 * Hk + Hv) * 128 * 2
+    assert fused - base - T * (2 * Hk + Hv) * 128 * 2 < 256
+    assert lib.gdn_prefill_fused_workspace_size(N, T, Hk, Hv, 64, 128) == _lib.GDN_EUNSUPPORTED
+    C = (2 * Hk + Hv) * 128
+    P = lambda i: ctypes.c_void_p((1 << 32) + (i << 28))  # distinct, aligned, never dereferenced
+
+    def call(**over):
+        args = dict(qkv=P(0), qs=C, cs_in=P(1), cs_out=P(2), cdt=_lib.GDN_BF16, w=P(3), K=4, a=P(4),
+                    b=P(5), gdt=_lib.GDN_BF16, gs=Hv, A_log=P(6), dt=P(7), s_in=P(8), s_out=P(9),
+                    y=P(10), ydt=_lib.GDN_BF16, cu=None, N=N, T=T, Hk=Hk, Hv=Hv, Dk=128, Dv=128,
+                    ws=P(11), wsb=fused)
+        args.update(over)
+        return lib.gdn_prefill_fused(*args.values(), None)
+
+    assert call(K=3) == _lib.GDN_EUNSUPPORTED
+    assert call(cdt=_lib.GDN_F16) == _lib.GDN_EUNSUPPORTED
+    assert call(qs=C + 4) == _lib.GDN_EINVAL and "qkv_stride" in _err(lib)
+    assert call(qs=C - 8) == _lib.GDN_EINVAL and "qkv_stride" in _err(lib)
+    assert call(wsb=fused - 1) == _lib.GDN_EINVAL and "workspace" in _err(lib)
+    assert call(cs_out=ctypes.c_void_p((1 << 32) + (1 << 28) + 16)) == _lib.GDN_EINVAL
+    assert "overlaps" in _err(lib)
+    assert call(s_out=P(8)) == _lib.GDN_EINVAL and "alias" in _err(lib)
+    assert call(qkv=ctypes.c_void_p((1 << 32) + 8)) == _lib.GDN_EINVAL and "aligned" in _err(lib)
+    assert call(gs=Hv - 1) == _lib.GDN_EINVAL and "gate_stride" in _err(lib)
+    assert call(N=2, T=T + 1) == _lib.GDN_EINVAL and "divisible" in _err(lib)
