@@ -51,7 +51,7 @@ typedef enum {
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
  * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride,
  * 10 the gated norm's z layout, 11 gdn_quantized_matmul_noalloc, 12 the
- * prefill's float32 q/k/v, 13 gdn_prefill_fused). */
+ * prefill's float32 q/k/v, 13 gdn_prefill_fused, 14 gdn_dequantize's mode). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -332,14 +332,31 @@ int gdn_quantized_matmul_noalloc(const void *x, int x_dtype, const void *w, cons
 int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype, int M, int N, int K,
                                             int bits, int group_size);
 
+/* Quantization modes (the reference's QuantScheme.mode, config.py:17-33). */
+#define GDN_QUANT_AFFINE 0
+#define GDN_QUANT_MXFP4 1
+#define GDN_QUANT_MXFP8 2
+#define GDN_QUANT_NVFP4 3
+
 /*
- * gdn_dequantize - the dense weights of gdn_quantized_matmul's layout:
- * out[n][k] = scales[n][g] * q + biases[n][g] (float32 product, one rounding
- * to out_dtype). out: (N, K) out_dtype. Counterpart of mx.dequantize, which
- * the reference's tests use to build dense weights (tests/test_qwen3_5_linear_attention.py:59-70).
+ * gdn_dequantize - the dense weights of a quantized projection, for every
+ * scheme the reference's QuantScheme accepts. w: (N, K * bits / 32) uint32,
+ * element k of row n the bits-wide field at bit bits * k of the row's
+ * little-endian bit stream (for 2, 4 and 8 bits: bits [bits * (k % (32 /
+ * bits)), +bits) of word k / (32 / bits)). out: (N, K) out_dtype.
+ *   GDN_QUANT_AFFINE (bits 2, 3, 4, 5, 6 or 8; group_size 32, 64 or 128):
+ *     out[n][k] = scales[n][g] * q + biases[n][g] (float32 product, one
+ *     rounding to out_dtype), scales and biases (N, K / group_size) sb_dtype
+ *   GDN_QUANT_MXFP4 (4 bits, group 32), GDN_QUANT_MXFP8 (8 bits, group 32),
+ *   GDN_QUANT_NVFP4 (4 bits, group 16): the code's e2m1 (fp4) or e4m3 (fp8)
+ *     value times its group's scale, (N, K / group_size) uint8: e8m0 (2^(s -
+ *     127)) for the mx formats, e4m3 for nvfp4; biases unused (NULL); exact
+ *     in float32 and bf16
+ * Counterpart of mx.dequantize, which the reference's tests use to build dense
+ * weights (tests/test_qwen3_5_linear_attention.py:59-70).
  */
 int gdn_dequantize(const void *w, const void *scales, const void *biases, int sb_dtype, void *out,
-                   int out_dtype, int N, int K, int bits, int group_size, void *stream);
+                   int out_dtype, int N, int K, int bits, int group_size, int mode, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1196,14 +1196,107 @@ extern "C" int gdn_quantized_matmul_noalloc(const void* x, int x_dtype, const vo
                             group_size, need > 0 ? ptr : nullptr, need, stream);
 }
 
+namespace gdn {
+namespace {
+
+// The microscaling float codes (OCP MX formats): e2m1 (fp4: sign, 2-bit
+// exponent of bias 1, 1-bit mantissa; exponent 0 is 0 or 0.5), e4m3 (fp8:
+// sign, 4-bit exponent of bias 7, 3-bit mantissa; exponent 0 subnormal,
+// 0x7F / 0xFF NaN) and e8m0 (a power of two, 2^(c - 127); 255 NaN).
+GDN_DEV float e2m1_value(uint32_t c) {
+    const int e = int(c >> 1) & 3;
+    const float mag = e == 0 ? 0.5f * float(c & 1) : ldexpf(1.f + 0.5f * float(c & 1), e - 1);
+    return (c & 8) ? -mag : mag;
+}
+
+GDN_DEV float e4m3_value(uint32_t c) {
+    const int e = int(c >> 3) & 15, m = int(c & 7);
+    if (e == 15 && m == 7) return __builtin_nanf("");
+    const float mag = e == 0 ? ldexpf(float(m), -9) : ldexpf(1.f + float(m) * 0.125f, e - 7);
+    return (c & 0x80) ? -mag : mag;
+}
+
+GDN_DEV float e8m0_value(uint32_t c) { return c == 255 ? __builtin_nanf("") : ldexpf(1.f, int(c) - 127); }
+
+// Dense weights of any scheme QuantScheme accepts, one thread per 32
+// elements of a row (the last may hold 16): element k of a row is the
+// bits-wide field at bit bits * k of the row's little-endian bit stream
+// (MLX packs 3-, 5- and 6-bit codes into byte groups, which reads the same),
+// so a thread's 32 codes are its `bits` consecutive words. affine:
+// s * q + b in float32, rounded once to out's dtype; mxfp4 / mxfp8 / nvfp4:
+// the code's value times the group's scale (e8m0, or e4m3 for nvfp4), exact
+// in float32 and in bf16 (at most 6 significant bits).
+__global__ __launch_bounds__(256) void dequantize_scheme_kernel(
+    const uint32_t* __restrict__ w, const void* __restrict__ scales, const void* __restrict__ biases,
+    int sb_dtype, void* __restrict__ out, int out_dtype, int N, int K, int bits, int group_size, int mode) {
+    const int chunks = (K + 31) / 32;
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= int64_t(N) * chunks) return;
+    const int n = int(t / chunks), k0 = int(t % chunks) * 32;
+    const int64_t row_words = int64_t(K) * bits / 32;
+    const uint32_t* rw = w + int64_t(n) * row_words + int64_t(k0) * bits / 32;
+    const int words = int((int64_t(K - k0 < 32 ? K - k0 : 32) * bits + 31) / 32);
+    uint32_t wd[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) wd[i] = i < words ? rw[i] : 0u;
+    const uint32_t mask = (1u << bits) - 1u;
+    const int gpr = K / group_size;
+    const int64_t sb_row = int64_t(n) * gpr;
+    for (int e = 0; e < 32 && k0 + e < K; ++e) {
+        const int off = bits * e, wi = off >> 5, sh = off & 31;
+        const uint64_t pair = uint64_t(wd[wi]) | (uint64_t(wd[wi + 1]) << 32);
+        const uint32_t q = uint32_t(pair >> sh) & mask;
+        const int64_t g = sb_row + (k0 + e) / group_size;
+        float v;
+        if (mode == GDN_QUANT_AFFINE) {
+            v = __builtin_fmaf(load_any(scales, g, sb_dtype), float(q), load_any(biases, g, sb_dtype));
+        } else {
+            const uint32_t sc = static_cast<const uint8_t*>(scales)[g];
+            const float code = mode == GDN_QUANT_MXFP8 ? e4m3_value(q) : e2m1_value(q);
+            v = code * (mode == GDN_QUANT_NVFP4 ? e4m3_value(sc) : e8m0_value(sc));
+        }
+        store_any(out, int64_t(n) * K + k0 + e, out_dtype, v);
+    }
+}
+
+}  // namespace
+}  // namespace gdn
+
 extern "C" int gdn_dequantize(const void* w, const void* scales, const void* biases, int sb_dtype,
-                              void* out, int out_dtype, int N, int K, int bits, int group_size,
+                              void* out, int out_dtype, int N, int K, int bits, int group_size, int mode,
                               void* stream) {
-    if (int rc = check_quant_args("gdn_dequantize", w, scales, biases, sb_dtype, N, K, bits, group_size))
-        return rc;
     GDN_REQUIRE(out && valid_dtype(out_dtype), "gdn_dequantize: bad output");
     hipStream_t s = as_stream(stream);
-    const auto* wp = static_cast<const uint32_t*>(w);
-    if (bits == 4) return launch_dequant<4>(wp, scales, biases, sb_dtype, out, out_dtype, N, K, group_size, s);
-    return launch_dequant<8>(wp, scales, biases, sb_dtype, out, out_dtype, N, K, group_size, s);
+    if (mode == GDN_QUANT_AFFINE && (bits == 4 || bits == 8)) {
+        if (int rc = check_quant_args("gdn_dequantize", w, scales, biases, sb_dtype, N, K, bits, group_size))
+            return rc;
+        const auto* wp = static_cast<const uint32_t*>(w);
+        if (bits == 4) return launch_dequant<4>(wp, scales, biases, sb_dtype, out, out_dtype, N, K, group_size, s);
+        return launch_dequant<8>(wp, scales, biases, sb_dtype, out, out_dtype, N, K, group_size, s);
+    }
+    // the schemes of the reference's QuantScheme (config.py:17-33)
+    bool ok;
+    switch (mode) {
+        case GDN_QUANT_AFFINE:
+            ok = (bits >= 2 && bits <= 8 && bits != 7) &&
+                 (group_size == 32 || group_size == 64 || group_size == 128);
+            break;
+        case GDN_QUANT_MXFP4: ok = bits == 4 && group_size == 32; break;
+        case GDN_QUANT_MXFP8: ok = bits == 8 && group_size == 32; break;
+        case GDN_QUANT_NVFP4: ok = bits == 4 && group_size == 16; break;
+        default: ok = false;
+    }
+    GDN_REQUIRE(ok, "gdn_dequantize: mode %d with bits=%d, group_size=%d is not a scheme", mode, bits,
+                group_size);
+    GDN_REQUIRE(N > 0 && K > 0 && K % group_size == 0 && int64_t(K) * bits % 32 == 0,
+                "gdn_dequantize: K=%d must be a multiple of group_size and fill whole words", K);
+    GDN_REQUIRE(w && scales && (mode != GDN_QUANT_AFFINE || biases), "gdn_dequantize: null weight, scales or biases");
+    GDN_REQUIRE(mode != GDN_QUANT_AFFINE || valid_dtype(sb_dtype), "gdn_dequantize: bad scales/biases dtype");
+    const int64_t threads = int64_t(N) * ((K + 31) / 32);
+    GDN_REQUIRE(threads < (int64_t(1) << 31), "gdn_dequantize: %lld elements exceed the grid",
+                (long long)N * K);
+    hipLaunchKernelGGL(dequantize_scheme_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const uint32_t*>(w), scales, biases, sb_dtype, out, out_dtype, N, K, bits,
+                       group_size, mode);
+    return check_launch("gdn_dequantize");
 }

@@ -1,15 +1,18 @@
-"""Affine-quantized linear projections (MLX's packing) for the layer's input
-and output projections.
+"""Quantized linear projections (MLX's packings) for the layer's input and
+output projections.
 
 Mirrors ``mlx_lean_moe.config.QuantScheme`` (``config.py:10-33``) and
 ``mlx_lean_moe.model.moe_block.{LinearWeights, quantized_linear}``
 (``model/moe_block.py:13-55``): a projection is either a dense ``(N, K)``
-matrix or a dict ``{"weight", "scales", "biases"}`` with ``weight`` uint32
-``(N, K * bits / 32)`` (MLX's packing, least significant element first) and
-``scales``/``biases`` ``(N, K / group_size)``; ``w = scales * q + biases``.
-Quantized projections of bf16 activations run on ``gdn_quantized_matmul``;
-other activation dtypes dequantize on the GPU (``gdn_dequantize``) and
-multiply on the vendor BLAS. Dense projections are ``x @ W.T``.
+matrix or a dict ``{"weight", "scales"[, "biases"]}`` with ``weight`` uint32
+``(N, K * bits / 32)`` (MLX's packing: element k at bit ``bits * k`` of the
+row's little-endian bit stream) and per-group ``scales`` ``(N, K /
+group_size)``. Affine schemes (2-8 bits): ``w = scales * q + biases``;
+mxfp4 / mxfp8 / nvfp4: ``w`` = the e2m1 / e4m3 code's value times a uint8
+scale (e8m0, e4m3 for nvfp4), no biases. Affine 4- and 8-bit projections of
+bf16 activations run on ``gdn_quantized_matmul``; the other schemes and
+activation dtypes dequantize on the GPU (``gdn_dequantize``) and multiply on
+the vendor BLAS. Dense projections are ``x @ W.T``.
 """
 
 from __future__ import annotations
@@ -28,7 +31,10 @@ _SUPPORTED = {
     "mxfp8": ({8}, {32}),
     "nvfp4": ({4}, {16}),
 }
-# what the kernels implement (valid schemes outside it raise NotImplementedError)
+# the mode codes of gdn_dequantize
+_MODES = {"affine": 0, "mxfp4": 1, "mxfp8": 2, "nvfp4": 3}
+# the affine widths the quantized matmul kernels take (the other schemes
+# dequantize, then multiply on the vendor BLAS)
 _KERNEL_BITS = {4, 8}
 # From this many rows on, quantized_linear dequantizes the weights to bf16
 # once and multiplies on the vendor BLAS (measured at hidden 2048 -> 12352:
@@ -98,27 +104,37 @@ class LinearWeights:
         return LinearWeights(self.tensors, self.quant, dequantize(self.tensors, self.quant, torch.bfloat16))
 
 
-def _kernel_scheme(quant: QuantScheme) -> None:
-    if quant.mode != "affine" or quant.bits not in _KERNEL_BITS:
-        raise NotImplementedError(
-            f"{quant.mode} {quant.bits}-bit weights: this build runs affine 4- and 8-bit")
+def _on_kernels(quant: QuantScheme) -> bool:
+    """Whether ``gdn_quantized_matmul`` multiplies by these codes directly."""
+
+    return quant.mode == "affine" and quant.bits in _KERNEL_BITS
 
 
 def _check_quantized(tensors: dict, quant: QuantScheme, K: int | None):
     w, scales = tensors["weight"], tensors["scales"]
     biases = tensors.get("biases")
-    if biases is None:
+    affine = quant.mode == "affine"
+    if affine and biases is None:
         raise ValueError("affine quantized weights need biases")
+    if not affine and biases is not None:
+        raise ValueError(f"{quant.mode} weights carry no biases")
     if w.dtype not in (torch.int32, torch.uint32) or w.dim() != 2:
         raise ValueError("quantized weight must be a 2-D 32-bit integer tensor")
     N, words = w.shape
+    if words * 32 % quant.bits:
+        raise ValueError(f"{words} words per row hold no whole number of {quant.bits}-bit codes")
     k = words * 32 // quant.bits
     if K is not None and K != k:
         raise ValueError(f"input width {K} does not match the weight's {k}")
-    if tuple(scales.shape) != (N, k // quant.group_size) or scales.shape != biases.shape:
-        raise ValueError(f"scales and biases must have shape {(N, k // quant.group_size)}")
-    if scales.dtype != biases.dtype:
+    if k % quant.group_size:
+        raise ValueError(f"a row of {k} codes holds no whole number of groups of {quant.group_size}")
+    if tuple(scales.shape) != (N, k // quant.group_size) or (affine and scales.shape != biases.shape):
+        raise ValueError(f"scales{' and biases' if affine else ''} must have shape "
+                         f"{(N, k // quant.group_size)}")
+    if affine and scales.dtype != biases.dtype:
         raise ValueError("scales and biases must share a dtype")
+    if not affine and scales.dtype != torch.uint8:
+        raise ValueError(f"{quant.mode} scales are uint8 codes, got {scales.dtype}")
     return w, scales, biases, N, k
 
 
@@ -128,18 +144,23 @@ def _c(t: torch.Tensor) -> torch.Tensor:
 
 def dequantize(tensors: dict, quant: QuantScheme, dtype: torch.dtype | None = None):
     """Dense ``(N, K)`` weights of a quantized projection, in ``dtype``
-    (default: the scales' dtype), computed on the GPU (mx.dequantize's
-    counterpart)."""
+    (default: the scales' dtype for affine schemes, bf16 for the float
+    ones), computed on the GPU (mx.dequantize's counterpart)."""
 
-    _kernel_scheme(quant)
     w, scales, biases, N, K = _check_quantized(tensors, quant, None)
     if w.device.type != "cuda":
         raise RuntimeError(f"quantized weights must be on a ROCm device, got {w.device}")
-    out = torch.empty((N, K), dtype=dtype or scales.dtype, device=w.device)
-    w, scales, biases = _c(w), _c(scales), _c(biases)
-    _lib.call("gdn_dequantize", _lib.ptr(w), _lib.ptr(scales), _lib.ptr(biases),
-              _lib.dtype_code(scales.dtype), _lib.ptr(out), _lib.dtype_code(out.dtype), N, K,
-              quant.bits, quant.group_size, _lib.stream_ptr(w.device))
+    if dtype is None:
+        dtype = scales.dtype if quant.mode == "affine" else torch.bfloat16
+    out = torch.empty((N, K), dtype=dtype, device=w.device)
+    w, scales = _c(w), _c(scales)
+    if w.data_ptr() % 16:
+        w = w.clone()
+    biases = _c(biases) if biases is not None else None
+    sb_dtype = _lib.dtype_code(scales.dtype) if quant.mode == "affine" else 0
+    _lib.call("gdn_dequantize", _lib.ptr(w), _lib.ptr(scales), _lib.ptr(biases), sb_dtype,
+              _lib.ptr(out), _lib.dtype_code(out.dtype), N, K, quant.bits, quant.group_size,
+              _MODES[quant.mode], _lib.stream_ptr(w.device))
     return out
 
 
@@ -189,10 +210,14 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None,
         return with_residual(x.to(dt) @ tensors.to(dt).T)
     if quant is None:
         raise ValueError("quantized linear weights require a quantization scheme")
-    _kernel_scheme(quant)
     w, scales, biases, N, K = _check_quantized(tensors, quant, x.shape[-1])
     if x.device.type != "cuda":
         raise RuntimeError(f"quantized projections run on ROCm devices only; got {x.device}")
+    if not _on_kernels(quant):
+        # the other schemes: their exact weights in x's dtype (bf16 for the
+        # float schemes is exact), then the vendor BLAS
+        wd = dense if dense is not None else dequantize(tensors, quant, x.dtype)
+        return with_residual(x @ wd.to(x.dtype).T)
     lead = x.shape[:-1]
     rows = x.reshape(-1, K).shape[0]
     x_f32 = (x.dtype == torch.float32 and rows <= 32
@@ -250,8 +275,7 @@ def quantized_linear_split(x: torch.Tensor, weights: LinearWeights, sizes) -> li
     K = x.shape[-1]
     rows = x.reshape(-1, K).shape[0]
     if (x.dtype == torch.bfloat16 and x.device.type == "cuda"
-            and _dense_rows(rows, tensors["weight"].shape[0], K)):
-        _kernel_scheme(quant)
+            and (_dense_rows(rows, tensors["weight"].shape[0], K) or not _on_kernels(quant))):
         _check_quantized(tensors, quant, K)
         lead = x.shape[:-1]
         x2 = _c(x.reshape(-1, K))
@@ -282,4 +306,5 @@ def concat_quantized(parts: list[dict]) -> dict:
     """Stacks quantized projections that share an input (same K, scheme and
     scales dtype) along N, so that one launch computes all of them."""
 
-    return {key: torch.cat([p[key] for p in parts], dim=0) for key in ("weight", "scales", "biases")}
+    keys = [k for k in ("weight", "scales", "biases") if k in parts[0]]
+    return {key: torch.cat([p[key] for p in parts], dim=0) for key in keys}

@@ -177,8 +177,9 @@ def projection_is_quantized(index: dict[str, TensorSpan], name: str, scheme: Qua
 
     A missing weight raises ``KeyError``. Otherwise every inconsistency is
     collected and reported together in one :class:`LayoutError`: biases
-    stored without scales; an affine scheme without biases; biases not
-    shaped like the scales; weight and scales disagreeing in their leading
+    stored without scales; an affine scheme without biases; biases beside
+    the codes of a float scheme (mxfp4, mxfp8, nvfp4), which has none; biases
+    not shaped like the scales; weight and scales disagreeing in their leading
     (row) dimensions; a packed row width other than the scale groups'
     ``groups * group_size * bits / 32`` words. These are the conditions the
     reference's loader enforces (expert_loader.py:95-141)."""
@@ -196,7 +197,9 @@ def projection_is_quantized(index: dict[str, TensorSpan], name: str, scheme: Qua
     else:
         if biases is None and scheme.mode == "affine":
             problems.append("the affine scheme dequantizes with per-group biases; none are stored")
-        if biases is not None and biases.shape != scales.shape:
+        if biases is not None and scheme.mode != "affine":
+            problems.append(f"the {scheme.mode} scheme has no biases; some are stored")
+        elif biases is not None and biases.shape != scales.shape:
             problems.append(f"biases {biases.shape} and scales {scales.shape} differ in shape")
         if weight.shape[:-1] != scales.shape[:-1]:
             problems.append(f"weight {weight.shape} and scales {scales.shape} differ in their "

@@ -309,3 +309,75 @@ def test_residual_is_the_unfused_add(gpu, M, N, K, gs, dt):
         assert torch.equal(y, want)
     with pytest.raises(ValueError, match="residual"):
         gdn.quantized_linear(x, W, scheme, residual=r[:, :-1])
+
+
+@pytest.mark.parametrize("bits,gs,sb,out", [(2, 64, "bf16", "bf16"), (3, 32, "bf16", "f32"),
+                                             (5, 128, "f16", "f16"), (6, 32, "f32", "bf16"),
+                                             (6, 64, "bf16", "f32")])
+def test_dequantize_every_affine_width_is_bit_exact(gpu, bits, gs, sb, out):
+    """2-, 3-, 5- and 6-bit codes (the 3/5/6-bit ones straddle word
+    boundaries) against the oracle: s * q + b in float32, one rounding."""
+
+    rng = np.random.default_rng(bits * 1000 + gs)
+    words, s, b = _weights(rng, 33, 256, bits, gs, sb)
+    W = _dev_weights(gpu, words, s, b, sb)
+    dense = gdn.dequantize(W, gdn.QuantScheme(bits, gs), _TORCH[out])
+    np.testing.assert_array_equal(dense.float().cpu().numpy(),
+                                  Q.dequantize(words, s, b, bits, gs, out=out))
+
+
+def _fp_weights(rng, gpu, N, K, mode, gs):
+    bits = 8 if mode == "mxfp8" else 4
+    q = rng.integers(0, 2 ** bits, (N, K))
+    if mode == "mxfp8":
+        q[(q & 0x7F) == 0x7F] = 0x7E  # no NaN codes
+    if mode == "nvfp4":
+        scales = rng.integers(0x08, 0x7F, (N, K // gs))  # positive e4m3, none NaN
+    else:
+        scales = rng.integers(110, 140, (N, K // gs))
+    W = {"weight": torch.tensor(Q.pack(q, bits).view(np.int32), device=gpu),
+         "scales": torch.tensor(scales.astype(np.uint8), device=gpu)}
+    return W, Q.dequantize_fp(Q.pack(q, bits), scales, mode, gs)
+
+
+@pytest.mark.parametrize("mode,gs,K", [("mxfp4", 32, 256), ("mxfp8", 32, 256), ("nvfp4", 16, 256),
+                                        ("nvfp4", 16, 240)])
+def test_dequantize_float_schemes_is_bit_exact(gpu, mode, gs, K):
+    """mxfp4, mxfp8 and nvfp4 codes (nvfp4 with a row of 240: a 16-code
+    tail) against the oracle: value times scale, exact in bf16 and float32."""
+
+    rng = np.random.default_rng(K + gs + len(mode))
+    W, ref = _fp_weights(rng, gpu, 37, K, mode, gs)
+    scheme = gdn.QuantScheme(8 if mode == "mxfp8" else 4, gs, mode)
+    for dt in (torch.bfloat16, torch.float32):
+        dense = gdn.dequantize(W, scheme, dt)
+        np.testing.assert_array_equal(dense.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M", [1, 64, 600])
+@pytest.mark.parametrize("scheme", [(3, 64, "affine"), (6, 32, "affine"), (2, 128, "affine"),
+                                    (4, 32, "mxfp4"), (8, 32, "mxfp8"), (4, 16, "nvfp4")])
+def test_quantized_linear_every_scheme_matches_oracle(gpu, scheme, M):
+    """The schemes outside the quantized matmul kernels (dequantize, then
+    the vendor BLAS) through quantized_linear, bf16 x, with and without the
+    residual, against x @ W.T in float64."""
+
+    bits, gs, mode = scheme
+    rng = np.random.default_rng(bits + gs + M)
+    N, K = 96, 512
+    if mode == "affine":
+        words, s, b = _weights(rng, N, K, bits, gs, "bf16")
+        W = _dev_weights(gpu, words, s, b, "bf16")
+        w = Q.dequantize(words, s, b, bits, gs, out="bf16")  # the bf16 weights multiplied
+    else:
+        W, w = _fp_weights(rng, gpu, N, K, mode, gs)  # exact in bf16
+    x = R.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    xt = torch.tensor(x, device=gpu).to(torch.bfloat16)
+    q = gdn.QuantScheme(bits, gs, mode)
+    y = gdn.quantized_linear(xt, gdn.LinearWeights(W, q))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    assert y.dtype == torch.bfloat16 and y.shape == (M, N)
+    assert np.abs(y.float().cpu().numpy() - ref).max() <= 1e-2 * np.abs(ref).max()
+    r = torch.randn(M, N, device=gpu).to(torch.bfloat16)
+    yr = gdn.quantized_linear(xt, gdn.LinearWeights(W, q), residual=r)
+    assert torch.equal(yr, y + r)

@@ -76,3 +76,98 @@ def test_quantized_matmul_is_x_times_dequantized_weights():
     for m in range(2):
         for n in range(3):
             assert abs(y[m, n] - sum(x[m, k] * deq[n, k] for k in range(64))) < 1e-12
+
+
+def _word_layout_pack(q, bits):
+    """4-, 2- and 8-bit packing by words: code k at bit bits * (k % per) of
+    word k // per (per = 32 / bits)."""
+
+    per = 32 // bits
+    N, K = q.shape
+    out = np.zeros((N, K // per), np.uint64)
+    for k in range(K):
+        out[:, k // per] |= q[:, k].astype(np.uint64) << np.uint64(bits * (k % per))
+    return out.astype(np.uint32)
+
+
+def _byte_group_pack(q, bits):
+    """3-, 5- and 6-bit packing as MLX's byte groups: pack_factor codes
+    (8, 8, 4) into bytes_per_pack bytes (3, 5, 3), least significant code
+    first, each group's integer written little-endian."""
+
+    factor, nbytes = {3: (8, 3), 5: (8, 5), 6: (4, 3)}[bits]
+    rows = []
+    for row in q:
+        out = bytearray()
+        for i in range(0, len(row), factor):
+            v = sum(int(c) << (bits * j) for j, c in enumerate(row[i:i + factor]))
+            out += v.to_bytes(nbytes, "little")
+        rows.append(np.frombuffer(bytes(out), "<u4").astype(np.uint32))
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_packing_of_every_affine_width(bits):
+    """One bit stream for every width: 2/4/8-bit codes by words, 3/5/6-bit
+    codes by MLX's byte groups (constructed independently), round trips,
+    extreme codes and the reference's packed-width rule (K * bits / 32
+    words, expert_loader.py's "expected packed width")."""
+
+    rng = np.random.default_rng(100 + bits)
+    q = rng.integers(0, 2 ** bits, (4, 128))
+    q[0] = 2 ** bits - 1
+    q[1] = 0
+    w = Q.pack(q, bits)
+    assert w.shape == (4, 128 * bits // 32)
+    ref = _word_layout_pack(q, bits) if bits in (2, 4, 8) else _byte_group_pack(q, bits)
+    np.testing.assert_array_equal(w, ref)
+    np.testing.assert_array_equal(Q.unpack(w, bits), q)
+    assert (w[0] == 0xFFFFFFFF).all() and (w[1] == 0).all()
+
+
+def test_three_bit_codes_fixed_words():
+    # codes 1..7, 0 repeated: each group of 8 is the 24-bit 0x1F58D1 (bytes D1 58 1F)
+    q = np.array([[1, 2, 3, 4, 5, 6, 7, 0] * 4])
+    np.testing.assert_array_equal(Q.pack(q, 3)[0], [0xD11F58D1, 0x58D11F58, 0x1F58D11F])
+
+
+def test_e4m3_and_e8m0_codes_match_torch_float8():
+    torch = pytest.importorskip("torch")
+    codes = np.arange(256)
+    as8 = torch.from_numpy(codes.astype(np.uint8))
+    for mine, dt in ((Q.e4m3_value, torch.float8_e4m3fn), (Q.e8m0_value, torch.float8_e8m0fnu)):
+        ref = as8.view(dt).double().numpy()
+        got = mine(codes)
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+        np.testing.assert_array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+
+
+def test_e2m1_codes_are_their_e4m3_reencoding():
+    """Each fp4 code re-encoded in fp8's fields (the same sign, the exponent
+    re-biased from 1 to 7, the mantissa bit on top of three) decodes to the
+    same value through torch; and the OCP table's magnitudes."""
+
+    torch = pytest.importorskip("torch")
+    c = np.arange(16)
+    s, e, m = c >> 3, (c >> 1) & 3, c & 1
+    # exponent 0: 0 or 0.5 (= 2^-1: e4m3 exponent field 6, mantissa 0)
+    fp8 = np.where(e > 0, (s << 7) | ((e - 1 + 7) << 3) | (m << 2), np.where(m == 1, (s << 7) | (6 << 3), s << 7))
+    ref = torch.from_numpy(fp8.astype(np.uint8)).view(torch.float8_e4m3fn).double().numpy()
+    np.testing.assert_array_equal(Q.e2m1_value(c), ref)
+    np.testing.assert_array_equal(np.abs(Q.e2m1_value(c[:8])), [0, 0.5, 1, 1.5, 2, 3, 4, 6])
+
+
+@pytest.mark.parametrize("mode,gs", [("mxfp4", 32), ("mxfp8", 32), ("nvfp4", 16)])
+def test_float_scheme_is_code_value_times_group_scale(mode, gs):
+    bits = 8 if mode == "mxfp8" else 4
+    rng = np.random.default_rng(len(mode) + gs)
+    q = rng.integers(0, 2 ** bits, (3, 64))
+    scales = rng.integers(120, 135, (3, 64 // gs)) if mode != "nvfp4" else rng.integers(0x30, 0x50, (3, 4))
+    w = Q.dequantize_fp(Q.pack(q, bits), scales, mode, gs)
+    value = Q.e4m3_value if mode == "mxfp8" else Q.e2m1_value
+    scale = Q.e4m3_value if mode == "nvfp4" else Q.e8m0_value
+    for n in range(3):
+        for k in range(64):
+            assert w[n, k] == value(q[n, k]) * scale(scales[n, k // gs]) or np.isnan(w[n, k])
+    finite = w[np.isfinite(w)]
+    np.testing.assert_array_equal(bf16_round(finite), finite)  # exact in bf16

@@ -42,12 +42,23 @@ def test_quantized_weights_need_a_scheme():
         gdn.quantized_linear(torch.randn(2, 128), _qweights())
 
 
-def test_schemes_outside_the_kernels_are_not_silently_run():
-    with pytest.raises(NotImplementedError):
-        gdn.quantized_linear(torch.randn(2, 128), _qweights(bits=4),
-                             gdn.QuantScheme(3, 64))
-    with pytest.raises(NotImplementedError):
+def test_every_scheme_is_checked_before_any_launch():
+    # 3-bit codes: 128 of them fill 12 words; 16 words of 4-bit codes hold no
+    # whole number of 3-bit ones, 24 hold 256
+    with pytest.raises(ValueError, match="no whole number"):
+        gdn.quantized_linear(torch.randn(2, 128), _qweights(bits=4), gdn.QuantScheme(3, 64))
+    with pytest.raises(ValueError, match="input width"):
+        gdn.quantized_linear(torch.randn(2, 128), _qweights(K=256, bits=3), gdn.QuantScheme(3, 64))
+    # the float schemes carry uint8 scales and no biases
+    with pytest.raises(ValueError, match="no biases"):
         gdn.quantized_linear(torch.randn(2, 128), _qweights(), gdn.QuantScheme(4, 32, "mxfp4"))
+    fp = _qweights(gs=32)
+    del fp["biases"]
+    with pytest.raises(ValueError, match="uint8"):
+        gdn.quantized_linear(torch.randn(2, 128), fp, gdn.QuantScheme(4, 32, "mxfp4"))
+    fp["scales"] = torch.zeros(fp["weight"].shape[0], 4, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        gdn.quantized_linear(torch.randn(2, 128), fp, gdn.QuantScheme(4, 32, "mxfp4"))
 
 
 def test_shape_checks_before_any_launch():

@@ -115,7 +115,8 @@ def _loc(shape, dtype="U32"):
 def test_linear_layout_rules():
     """The reference loader's conditions (expert_loader.py:95-141): a
     missing weight is a KeyError; biases without scales, an affine scheme
-    without biases, biases not shaped like the scales, weight and scale rows
+    without biases, biases for a scheme that has none (the float schemes),
+    biases not shaped like the scales, weight and scale rows
     that differ, and a packed width other than groups * group_size * bits /
     32 are each a LayoutError (a ValueError); several at once are all
     named."""
@@ -145,6 +146,11 @@ def test_linear_layout_rules():
     # modes without biases (mxfp4) need none
     mx = {"p.weight": _loc((8, 8)), "p.scales": _loc((8, 2), "U8")}
     assert check(mx, "p", QuantScheme(4, 32, "mxfp4")) is True
+    # ... and biases stored beside them are a layout error
+    with pytest.raises(W.LayoutError, match="mxfp4 scheme has no biases"):
+        check({**mx, "p.biases": _loc((8, 2), "BF16")}, "p", QuantScheme(4, 32, "mxfp4"))
+    nv = {"p.weight": _loc((8, 8)), "p.scales": _loc((8, 4), "U8")}
+    assert check(nv, "p", QuantScheme(4, 16, "nvfp4")) is True
 
 
 def test_hf_config_shapes_and_quantization():
