@@ -1,7 +1,10 @@
 // The bf16 prefill front-end's per-token arithmetic for eight channels of one
 // 128-channel group (linear_attention.py:61-79,103-113): the causal K = 4
 // conv, SiLU and the q/k scaling. Shared by the tiled front-end kernel and the
-// fused chunk pass of the prefill, so that both produce the same bits.
+// fused chunk pass of the prefill, so that both produce the same bits. Every
+// rounding is written out (fused multiply-adds where named, no other
+// contraction), so that the two kernels round alike whatever code surrounds
+// the calls.
 #pragma once
 
 #include "gdn_common.h"
@@ -14,6 +17,7 @@ namespace gdn {
 // divide, and within a few float ulp of them, far below the bf16 rounding
 // the result gets next.
 GDN_DEV float silu_hw(float x) {
+#pragma clang fp contract(off)
     return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.44269504088896341f));
 }
 
@@ -58,12 +62,13 @@ GDN_DEV void load_conv_w8(const float* __restrict__ w, int64_t c0, float (&wr)[8
 // (x), rounded to bf16, then SiLU, rounded to bf16.
 GDN_DEV void conv_silu8(const float (&wr)[8][4], const float (&win)[3][8], const float (&x)[8],
                         float (&o)[8]) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) acc += wr[e][j] * win[j][e];
-        o[e] = acc + wr[e][3] * x[e];
+        float acc = wr[e][0] * win[0][e];
+        acc = __builtin_fmaf(wr[e][1], win[1][e], acc);
+        acc = __builtin_fmaf(wr[e][2], win[2][e], acc);
+        o[e] = __builtin_fmaf(wr[e][3], x[e], acc);
     }
 #pragma unroll
     for (int e = 0; e < 8; e += 2) round_bf16x2(o[e], o[e + 1]);
@@ -76,10 +81,11 @@ GDN_DEV void conv_silu8(const float (&wr)[8][4], const float (&win)[3][8], const
 // rms_norm(o, 1e-6) of one token's 128-channel group held 8 channels a lane by
 // the 16 lanes of a DPP row (every lane of the wave active), rounded to bf16.
 GDN_DEV void rms_norm8(const float (&o)[8], float (&n)[8]) {
-    float ss = 0.f;
+#pragma clang fp contract(off)
+    float ss = o[0] * o[0];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += o[e] * o[e];
-    const float r = __builtin_amdgcn_rsqf(row16_sum(ss) / 128.f + 1e-6f);
+    for (int e = 1; e < 8; ++e) ss = __builtin_fmaf(o[e], o[e], ss);
+    const float r = __builtin_amdgcn_rsqf(row16_sum(ss) * (1.f / 128.f) + 1e-6f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) n[e] = o[e] * r;
 #pragma unroll

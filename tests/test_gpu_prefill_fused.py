@@ -38,8 +38,13 @@ def _case(gpu, seed, T, N, Hk, Hv, conv_dtype=torch.bfloat16):
 
 
 def _unfused(c, cu, y_dtype):
+    """gdn_frontend's tiled kernel (which the fused pass shares its
+    arithmetic with) on a contiguous copy of qkv: the stacked rows of an
+    odd head count are not a multiple of 8 elements, which sends the view to
+    the general front-end kernel (another summation order)."""
+
     d = c["dims"]
-    q, k, v, conv = gdn.conv_frontend(c["qkv"], c["conv"], c["w"], d, cu)
+    q, k, v, conv = gdn.conv_frontend(c["qkv"].contiguous(), c["conv"], c["w"], d, cu)
     if cu is None:
         y, ssm = gdn.gated_delta_update(q[None], k[None], v[None], c["a"][None], c["b"][None],
                                         c["A_log"], c["dt_bias"], c["ssm"], y_dtype=y_dtype)
@@ -63,12 +68,17 @@ def test_fused_prefill_equals_frontend_then_chunked_prefill_t4096(gpu, y_dtype):
     assert torch.equal(ssm, ssm_ref)
 
 
-@pytest.mark.parametrize("conv_dtype", [torch.bfloat16, torch.float32])
-def test_fused_prefill_over_packed_runs_with_short_and_empty_ones(gpu, conv_dtype):
+@pytest.mark.parametrize("conv_dtype,Hk,Hv", [(torch.bfloat16, 2, 4), (torch.float32, 2, 4),
+                                              (torch.bfloat16, 2, 8), (torch.float32, 1, 4),
+                                              (torch.bfloat16, 3, 3)])
+def test_fused_prefill_over_packed_runs_with_short_and_empty_ones(gpu, conv_dtype, Hk, Hv):
+    """Two or four value heads per key head (one workgroup per key head) and
+    one (one per value head)."""
+
     lens = [700, 0, 2, 130, 1, 64, 65, 300, 0, 3]
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32), device=gpu)
     T, N = int(sum(lens)), len(lens)
-    c = _case(gpu, 2, T, N, 2, 4, conv_dtype)
+    c = _case(gpu, 2, T, N, Hk, Hv, conv_dtype)
     assert gdn.fused_prefill_ok(c["qkv"], c["a"], c["b"], c["conv"], c["ssm"], c["dims"], N)
     y, conv, ssm = gdn.prefill_fused(c["qkv"], c["a"], c["b"], c["conv"], c["ssm"], c["w"],
                                      c["A_log"], c["dt_bias"], c["dims"], cu, y_dtype=torch.bfloat16)
