@@ -614,8 +614,9 @@ __global__ __launch_bounds__(256) void conv_state_empty_runs_kernel(RunLayout rl
 // ---------------------------------------------------------------------------
 
 constexpr int kSS = kHD + 8;     // bf16 row stride of the S operand tile
-constexpr int kQS = kHD + 8;     // bf16 row stride of the Q tile
 constexpr int kTS = kChunk + 8;  // bf16 row stride of token-minor operand tiles
+
+constexpr int kQS = kHD + 8;     // bf16 row stride of the Q tile (float32 input)
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -625,7 +626,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // their accumulators. Waves 4-7 compute the output (Q S^T, P D, y) and fetch
 // every chunk operand from global memory for both halves: those of the
 // state waves (K, V, Tb, the decay factors) two chunks ahead into registers,
-// then into LDS one chunk ahead. Issuing the loads is what the state
+// then into LDS one chunk ahead, and their own Q rows, straight into MFMA
+// A fragments two chunks ahead. Issuing the loads is what the state
 // recurrence cannot afford (the vector-memory queue stalls the issuing
 // wave); the output waves have slack. Both halves meet at the same three
 // barriers per chunk. Output wave w fetches the rows state wave w consumes;
@@ -633,11 +635,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // (kUpper = false) fetch and multiply only their first 32 columns.
 constexpr int kStateThreads = 512;
 
-// Chunk operands of state wave w, fetched by output wave w. They only pass
+// Chunk operands of state wave w, fetched by output wave w. They pass
 // through registers on the way to LDS, so each load covers whole rows (full
 // cache lines): 16 lanes per 256-byte K row, 8 per 128-byte Tb row.
 struct StagedOperands {
-    bf16x8 ka[4], qa[4];    // K, Q row 16w + 4i + l/16, dk 8(l%16) .. +7
+    bf16x8 ka[4];           // K row 16w + 4i + l/16, dk 8(l%16) .. +7
+    bf16x8 qa[4];           // Q: bf16 input, wave w's A fragments (row 16w + l%16, dk 32i + 8(l/16)
+                            // .. +7); float32 input, laid out as ka (staged in LDS)
     bf16x8 tbh[2], tbl[2];  // Tb fragments (2w + s) (hi, lo): row 16w + l%16, tokens 32s + 8(l/16) .. +7
     u32x2 v;                // V (bf16) at token 16w + l/4, dv dv0 + 4(l%4) .. +3
     f32x4 e;                // words 32w + 4(l%8) .. +3 of the record's [exp(l) | exp(l_C - l)]
@@ -692,19 +696,26 @@ GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int
             op.ka[i] = load8(static_cast<const uint16_t*>(cx.k) + qk0 + o);
         }
     }
+    // Q: output wave w reads only its own 16 rows. bf16: they load straight
+    // into its A fragments (no LDS). float32 (held as hi + lo): staged in LDS
+    // like K (kept in registers until the projection, the hi + lo fragments
+    // spill: 467 against 317 us at T=4096).
+    if constexpr (kF32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int tok = 16 * w + 4 * i + (l >> 4);
-        const int tok_c = tok < len ? tok : len - 1;
-        const uint32_t o = uint32_t(tok_c) * uint32_t(cx.qk_stride);
-        if constexpr (kF32) {
+        for (int i = 0; i < 4; ++i) {
+            const int tok = 16 * w + 4 * i + (l >> 4);
+            const int tok_c = tok < len ? tok : len - 1;
             u16x8 h, r;
-            load_split8(static_cast<const float*>(cx.q) + qk0 + o, h, r);
+            load_split8(static_cast<const float*>(cx.q) + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride), h, r);
             op.qa[i] = __builtin_bit_cast(bf16x8, h);
             op.qal[i] = __builtin_bit_cast(bf16x8, r);
-        } else {
-            op.qa[i] = load8(static_cast<const uint16_t*>(cx.q) + qk0 + o);
         }
+    } else {
+        const int qtok = 16 * w + (l & 15), qtok_c = qtok < len ? qtok : len - 1;
+        const int64_t q0 = cx.t0(c) * cx.qk_stride + cx.hk * kHD + 8 * (l >> 4) +
+                           uint32_t(qtok_c) * uint32_t(cx.qk_stride);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) op.qa[i] = load8(static_cast<const uint16_t*>(cx.q) + q0 + 32 * i);
     }
     const int tv = 16 * w + (l >> 2);
     const int tv_c = tv < len ? tv : len - 1;
@@ -750,7 +761,7 @@ template <bool kF32>
 struct StatePassLds {
     uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];  // S[dv][dk]
     uint16_t Kr[2][kChunk * kHD];                                 // K[token][dk] (swizzled), two buffers
-    uint16_t Qs[kChunk * kQS];                                   // Q[token][dk]
+    uint16_t Qs[kF32 ? kChunk * kQS : 8];                         // Q[token][dk] (float32 input)
     uint16_t Tb_hi[kChunk * kTS], Tb_lo[kChunk * kTS];            // Tb[token][token]
     uint16_t Vs[kChunk * kSliceRows];                             // V[token][dv]
     uint16_t Rs_hi[kSliceRows * kTS], Rs_lo[kSliceRows * kTS];    // R[dv][token]
@@ -772,7 +783,7 @@ GDN_DEV int kswz(int r) { return (((r & 3) | ((r >> 1) & 4)) << 1) | ((r >> 2) &
 GDN_DEV int kr_off(int r, int G) { return r * kHD + ((G ^ kswz(r)) << 3); }
 
 // Output waves: staged operands into LDS, in the layouts the state waves
-// read them with.
+// read them with (and, for float32 input, their own Q rows).
 template <bool kF32>
 GDN_DEV void stage_k(const StagedOperands& op, StatePassLds<kF32>& sm, int buf, int w, int l) {
 #pragma unroll
@@ -791,7 +802,7 @@ GDN_DEV void stage_q(const StagedOperands& op, StatePassLds<kF32>& sm, int w, in
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         *reinterpret_cast<bf16x8*>(sm.Qs + o + 4 * i * kQS) = op.qa[i];
-        if constexpr (kF32) *reinterpret_cast<bf16x8*>(sm.Qs_lo + o + 4 * i * kQS) = op.qal[i];
+        *reinterpret_cast<bf16x8*>(sm.Qs_lo + o + 4 * i * kQS) = op.qal[i];
     }
 }
 
@@ -939,15 +950,16 @@ GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds<kF32>& sm, int buf
     }
 }
 
-// Output waves, part 1 (between the staging and R barriers): exp(l) Q S^T.
+// Output waves, part 1 (between the staging and R barriers): exp(l) Q S^T,
+// Q from the wave's registers (the chunk's operands; float32 input: LDS).
 template <bool kF32>
-GDN_DEV f32x4 output_project(const StatePassLds<kF32>& sm, int w, int l) {
+GDN_DEV f32x4 output_project(const StagedOperands& op, const StatePassLds<kF32>& sm, int w, int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
     const int qo = (16 * w + lr) * kQS + lg8;
     f32x4 xq = {0.f, 0.f, 0.f, 0.f}, xq2 = xq;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        const bf16x8 qa = load8(sm.Qs + qo + 32 * s);
+        const bf16x8 qa = kF32 ? load8(sm.Qs + qo + 32 * s) : op.qa[s];
         const bf16x8 sh = load8(sm.Ss_hi + lr * kSS + 32 * s + lg8);
         xq = mfma16(qa, sh, xq);
         xq2 = mfma16(qa, load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xq2);
@@ -1034,15 +1046,16 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds<kF32>& sm
     const int last = nch - 1;
     StagedOperands ga, gb;
     OutputOperands oa, ob;
-    // gn: staged operands of chunk c + 1 (in registers), gf: receives chunk c + 2
+    // gn: staged operands of chunk c + 1 (in registers), gf: chunk c's (its
+    // Q fragments are read first), then receives chunk c + 2
     auto step = [&](int c, int buf, const OutputOperands& oc, OutputOperands& on,
                     const StagedOperands& gn, StagedOperands& gf) {
         __syncthreads();
-        const f32x4 yacc = output_project(sm, w, l);
+        const f32x4 yacc = output_project(gf, sm, w, l);  // gf still holds chunk c
         fetch_output<kUpper>(on, cx, c + 1 < last ? c + 1 : last, w, l);
         __builtin_amdgcn_sched_barrier(0);  // the prefetches stay where they are issued
         __syncthreads();
-        stage_q(gn, sm, w, l);
+        if constexpr (kF32) stage_q(gn, sm, w, l);
         stage_k(gn, sm, buf ^ 1, w, l);
         stage_v(gn, sm, w, l);
         fetch_staged<kUpper, kF32>(gf, cx, c + 2 < last ? c + 2 : last, w, l);
@@ -1055,7 +1068,7 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds<kF32>& sm
     fetch_staged<kUpper, kF32>(gb, cx, 0, w, l);
     fetch_staged<kUpper, kF32>(ga, cx, 1 < last ? 1 : last, w, l);
     fetch_output<kUpper>(oa, cx, 0, w, l);
-    stage_q(gb, sm, w, l);
+    if constexpr (kF32) stage_q(gb, sm, w, l);
     stage_k(gb, sm, 0, w, l);
     stage_v(gb, sm, w, l);
     stage_tb_e<kUpper>(gb, sm, w, l);
