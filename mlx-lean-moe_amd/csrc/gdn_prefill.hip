@@ -1040,8 +1040,10 @@ GDN_DEV void state_loop(int nch, StatePassLds<kF32>& sm, f32x4 (&acc)[2], int w,
     if (c < nch) step(0);
 }
 
+// Float32 input (operands with their residuals): chunk c + 2's operands
+// fetched at step c, its P fragments one chunk ahead.
 template <class Y, bool kUpper, bool kF32>
-GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds<kF32>& sm,
+GDN_DEV void output_loop_2ahead(const StatePassCtx& cx, int nch, StatePassLds<kF32>& sm,
                          typename Y::storage* __restrict__ y, int w, int l) {
     const int last = nch - 1;
     StagedOperands ga, gb;
@@ -1078,6 +1080,53 @@ GDN_DEV void output_loop(const StatePassCtx& cx, int nch, StatePassLds<kF32>& sm
         step(c + 1, 1, ob, oa, gb, ga);
     }
     if (c < nch) step(c, 0, oa, ob, ga, gb);
+}
+
+// bf16 input: the operand loads are issued three chunks ahead and the P
+// fragments two (at two chunks, the stores into LDS of the next chunk's
+// operands waited for loads issued a whole step before: the phase between
+// the second and third barrier is the step's longest). Chunk c's operands
+// live in slot c % 3 of the ring, its P fragments in slot c % 3 of theirs.
+template <class Y, bool kUpper, bool kF32>
+GDN_DEV void output_loop_3ahead(const StatePassCtx& cx, int nch, StatePassLds<kF32>& sm,
+                                typename Y::storage* __restrict__ y, int w, int l) {
+    const int last = nch - 1;
+    const auto at = [&](int c) { return c < last ? c : last; };
+    StagedOperands g0, g1, g2;
+    OutputOperands p0, p1, p2;
+    // step c: cur holds chunk c (its Q read, then refilled with chunk c + 3),
+    // nxt chunk c + 1 (staged into LDS); pc chunk c's P, pf receives c + 2's
+    auto step = [&](int c, StagedOperands& cur, const StagedOperands& nxt, const OutputOperands& pc,
+                    OutputOperands& pf) {
+        __syncthreads();
+        const f32x4 yacc = output_project(cur, sm, w, l);
+        fetch_output<kUpper>(pf, cx, at(c + 2), w, l);
+        __builtin_amdgcn_sched_barrier(0);  // the prefetches stay where they are issued
+        __syncthreads();
+        stage_k(nxt, sm, (c + 1) & 1, w, l);
+        stage_v(nxt, sm, w, l);
+        fetch_staged<kUpper, kF32>(cur, cx, at(c + 3), w, l);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        stage_tb_e<kUpper>(nxt, sm, w, l);
+        output_store<Y, kUpper>(pc, yacc, sm, cx, c, y, w, l);
+    };
+    fetch_staged<kUpper, kF32>(g0, cx, 0, w, l);
+    fetch_staged<kUpper, kF32>(g1, cx, at(1), w, l);
+    fetch_staged<kUpper, kF32>(g2, cx, at(2), w, l);
+    fetch_output<kUpper>(p0, cx, 0, w, l);
+    fetch_output<kUpper>(p1, cx, at(1), w, l);
+    stage_k(g0, sm, 0, w, l);
+    stage_v(g0, sm, w, l);
+    stage_tb_e<kUpper>(g0, sm, w, l);
+    int c = 0;
+    for (; c + 2 < nch; c += 3) {
+        step(c, g0, g1, p0, p2);
+        step(c + 1, g1, g2, p1, p0);
+        step(c + 2, g2, g0, p2, p1);
+    }
+    if (c < nch) step(c, g0, g1, p0, p2);
+    if (c + 1 < nch) step(c + 1, g1, g2, p1, p0);
 }
 
 template <class Y, bool kF32>
@@ -1145,8 +1194,13 @@ __global__ __launch_bounds__(kStateThreads) void prefill_state_kernel(
             *reinterpret_cast<float4*>(state_out + sbase + dk) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
         }
     } else if (nch > 0) {
-        if (w >= 2) output_loop<Y, true>(cx, nch, sm, y, w, l);
-        else output_loop<Y, false>(cx, nch, sm, y, w, l);
+        if constexpr (kF32) {
+            if (w >= 2) output_loop_2ahead<Y, true>(cx, nch, sm, y, w, l);
+            else output_loop_2ahead<Y, false>(cx, nch, sm, y, w, l);
+        } else {
+            if (w >= 2) output_loop_3ahead<Y, true>(cx, nch, sm, y, w, l);
+            else output_loop_3ahead<Y, false>(cx, nch, sm, y, w, l);
+        }
     }
 }
 
