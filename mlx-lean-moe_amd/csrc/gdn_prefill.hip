@@ -645,9 +645,14 @@ struct StagedOperands {
     bf16x8 tbh[2], tbl[2];  // Tb fragments (2w + s) (hi, lo): row 16w + l%16, tokens 32s + 8(l/16) .. +7
     u32x2 v;                // V (bf16) at token 16w + l/4, dv dv0 + 4(l%4) .. +3
     f32x4 e;                // words 32w + 4(l%8) .. +3 of the record's [exp(l) | exp(l_C - l)]
-    bf16x8 kal[4], qal[4];  // float32 input only: the residuals of ka, qa
-    u32x2 vl;               // and of v
+    bf16x8 kal[4], qal[4];  // float32 input only (see below)
+    u32x2 vl;
 };
+// Float32 input: the fetch keeps the loaded floats as they are (their bits:
+// K's 8 values in ka[i] (0-3) and kal[i] (4-7), Q's likewise in qa/qal, V's
+// 4 in v (0-1) and vl (2-3)); the staging splits them into bf16 hi + lo.
+// Splitting at the fetch would wait there for every load it issues, which
+// undoes the prefetch.
 
 // P fragments of output wave w (used from registers).
 struct OutputOperands {
@@ -688,10 +693,9 @@ GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int
         const int tok_c = tok < len ? tok : len - 1;
         const uint32_t o = uint32_t(tok_c) * uint32_t(cx.qk_stride);
         if constexpr (kF32) {
-            u16x8 h, r;
-            load_split8(static_cast<const float*>(cx.k) + qk0 + o, h, r);
-            op.ka[i] = __builtin_bit_cast(bf16x8, h);
-            op.kal[i] = __builtin_bit_cast(bf16x8, r);
+            const float* src = static_cast<const float*>(cx.k) + qk0 + o;
+            op.ka[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src));
+            op.kal[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src + 4));
         } else {
             op.ka[i] = load8(static_cast<const uint16_t*>(cx.k) + qk0 + o);
         }
@@ -705,10 +709,9 @@ GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int
         for (int i = 0; i < 4; ++i) {
             const int tok = 16 * w + 4 * i + (l >> 4);
             const int tok_c = tok < len ? tok : len - 1;
-            u16x8 h, r;
-            load_split8(static_cast<const float*>(cx.q) + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride), h, r);
-            op.qa[i] = __builtin_bit_cast(bf16x8, h);
-            op.qal[i] = __builtin_bit_cast(bf16x8, r);
+            const float* src = static_cast<const float*>(cx.q) + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride);
+            op.qa[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src));
+            op.qal[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src + 4));
         }
     } else {
         const int qtok = 16 * w + (l & 15), qtok_c = qtok < len ? qtok : len - 1;
@@ -722,14 +725,9 @@ GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int
     const int64_t vo = cx.t0(c) * cx.Hv * kHD + cx.h * kHD + cx.dv0 + 4 * (l & 3) +
                        uint32_t(tv_c) * uint32_t(cx.Hv * kHD);
     if constexpr (kF32) {
-        const float4 v4 = *reinterpret_cast<const float4*>(static_cast<const float*>(cx.v) + vo);
-        const float x[4] = {v4.x, v4.y, v4.z, v4.w};
-        uint16_t h[4], r[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) split_bf16(x[j], h[j], r[j]);
-        const uint2 ph = pack4(h), pr = pack4(r);
-        op.v = u32x2{ph.x, ph.y};
-        op.vl = u32x2{pr.x, pr.y};
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(cx.v) + vo);
+        op.v = u32x2{__float_as_uint(v4[0]), __float_as_uint(v4[1])};
+        op.vl = u32x2{__float_as_uint(v4[2]), __float_as_uint(v4[3])};
     } else {
         op.v = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(cx.v) + vo);
     }
@@ -784,13 +782,34 @@ GDN_DEV int kr_off(int r, int G) { return r * kHD + ((G ^ kswz(r)) << 3); }
 
 // Output waves: staged operands into LDS, in the layouts the state waves
 // read them with (and, for float32 input, their own Q rows).
+// The 8 floats whose bits a and b hold (4 each) as bf16 hi + lo.
+GDN_DEV void split8_bits(const bf16x8& a, const bf16x8& b, bf16x8& hi, bf16x8& lo) {
+    const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
+    u16x8 h, r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint16_t hj, rj;
+        split_bf16(j < 4 ? fa[j] : fb[j - 4], hj, rj);
+        h[j] = hj;
+        r[j] = rj;
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_bit_cast(bf16x8, r);
+}
+
 template <bool kF32>
 GDN_DEV void stage_k(const StagedOperands& op, StatePassLds<kF32>& sm, int buf, int w, int l) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int o = kr_off(16 * w + 4 * i + (l >> 4), l & 15);
-        *reinterpret_cast<bf16x8*>(sm.Kr[buf] + o) = op.ka[i];
-        if constexpr (kF32) *reinterpret_cast<bf16x8*>(sm.Kr_lo[buf] + o) = op.kal[i];
+        if constexpr (kF32) {
+            bf16x8 hi, lo;
+            split8_bits(op.ka[i], op.kal[i], hi, lo);
+            *reinterpret_cast<bf16x8*>(sm.Kr[buf] + o) = hi;
+            *reinterpret_cast<bf16x8*>(sm.Kr_lo[buf] + o) = lo;
+        } else {
+            *reinterpret_cast<bf16x8*>(sm.Kr[buf] + o) = op.ka[i];
+        }
     }
 }
 
@@ -801,16 +820,28 @@ GDN_DEV void stage_q(const StagedOperands& op, StatePassLds<kF32>& sm, int w, in
     const int o = (16 * w + (l >> 4)) * kQS + 8 * (l & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<bf16x8*>(sm.Qs + o + 4 * i * kQS) = op.qa[i];
-        *reinterpret_cast<bf16x8*>(sm.Qs_lo + o + 4 * i * kQS) = op.qal[i];
+        bf16x8 hi, lo;
+        split8_bits(op.qa[i], op.qal[i], hi, lo);
+        *reinterpret_cast<bf16x8*>(sm.Qs + o + 4 * i * kQS) = hi;
+        *reinterpret_cast<bf16x8*>(sm.Qs_lo + o + 4 * i * kQS) = lo;
     }
 }
 
 template <bool kF32>
 GDN_DEV void stage_v(const StagedOperands& op, StatePassLds<kF32>& sm, int w, int l) {
     const int o = (16 * w + (l >> 2)) * kSliceRows + 4 * (l & 3);
-    *reinterpret_cast<u32x2*>(sm.Vs + o) = op.v;
-    if constexpr (kF32) *reinterpret_cast<u32x2*>(sm.Vs_lo + o) = op.vl;
+    if constexpr (kF32) {
+        const float x[4] = {__uint_as_float(op.v[0]), __uint_as_float(op.v[1]), __uint_as_float(op.vl[0]),
+                            __uint_as_float(op.vl[1])};
+        uint16_t h[4], r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) split_bf16(x[j], h[j], r[j]);
+        const uint2 ph = pack4(h), pr = pack4(r);
+        *reinterpret_cast<u32x2*>(sm.Vs + o) = u32x2{ph.x, ph.y};
+        *reinterpret_cast<u32x2*>(sm.Vs_lo + o) = u32x2{pr.x, pr.y};
+    } else {
+        *reinterpret_cast<u32x2*>(sm.Vs + o) = op.v;
+    }
 }
 
 // Lanes 8-63 repeat lanes 0-7 for the decay words (same words, same values):
