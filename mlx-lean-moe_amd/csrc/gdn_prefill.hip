@@ -616,8 +616,6 @@ __global__ __launch_bounds__(256) void conv_state_empty_runs_kernel(RunLayout rl
 constexpr int kSS = kHD + 8;     // bf16 row stride of the S operand tile
 constexpr int kTS = kChunk + 8;  // bf16 row stride of token-minor operand tiles
 
-constexpr int kQS = kHD + 8;     // bf16 row stride of the Q tile (float32 input)
-
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -640,8 +638,7 @@ constexpr int kStateThreads = 512;
 // cache lines): 16 lanes per 256-byte K row, 8 per 128-byte Tb row.
 struct StagedOperands {
     bf16x8 ka[4];           // K row 16w + 4i + l/16, dk 8(l%16) .. +7
-    bf16x8 qa[4];           // Q: bf16 input, wave w's A fragments (row 16w + l%16, dk 32i + 8(l/16)
-                            // .. +7); float32 input, laid out as ka (staged in LDS)
+    bf16x8 qa[4];           // Q: wave w's A fragments (row 16w + l%16, dk 32i + 8(l/16) .. +7)
     bf16x8 tbh[2], tbl[2];  // Tb fragments (2w + s) (hi, lo): row 16w + l%16, tokens 32s + 8(l/16) .. +7
     u32x2 v;                // V (bf16) at token 16w + l/4, dv dv0 + 4(l%4) .. +3
     f32x4 e;                // words 32w + 4(l%8) .. +3 of the record's [exp(l) | exp(l_C - l)]
@@ -650,7 +647,8 @@ struct StagedOperands {
 };
 // Float32 input: the fetch keeps the loaded floats as they are (their bits:
 // K's 8 values in ka[i] (0-3) and kal[i] (4-7), Q's likewise in qa/qal, V's
-// 4 in v (0-1) and vl (2-3)); the staging splits them into bf16 hi + lo.
+// 4 in v (0-1) and vl (2-3)); the staging (Q: the projection) splits them
+// into bf16 hi + lo.
 // Splitting at the fetch would wait there for every load it issues, which
 // undoes the prefetch.
 
@@ -700,25 +698,23 @@ GDN_DEV void fetch_staged(StagedOperands& op, const StatePassCtx& cx, int c, int
             op.ka[i] = load8(static_cast<const uint16_t*>(cx.k) + qk0 + o);
         }
     }
-    // Q: output wave w reads only its own 16 rows. bf16: they load straight
-    // into its A fragments (no LDS). float32 (held as hi + lo): staged in LDS
-    // like K (kept in registers until the projection, the hi + lo fragments
-    // spill: 467 against 317 us at T=4096).
-    if constexpr (kF32) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tok = 16 * w + 4 * i + (l >> 4);
-            const int tok_c = tok < len ? tok : len - 1;
-            const float* src = static_cast<const float*>(cx.q) + qk0 + uint32_t(tok_c) * uint32_t(cx.qk_stride);
-            op.qa[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src));
-            op.qal[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src + 4));
-        }
-    } else {
+    // Q: output wave w reads only its own 16 rows; they load straight into
+    // its A fragments (no LDS; float32 input: the raw floats, split into hi +
+    // lo by the projection).
+    {
         const int qtok = 16 * w + (l & 15), qtok_c = qtok < len ? qtok : len - 1;
         const int64_t q0 = cx.t0(c) * cx.qk_stride + cx.hk * kHD + 8 * (l >> 4) +
                            uint32_t(qtok_c) * uint32_t(cx.qk_stride);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) op.qa[i] = load8(static_cast<const uint16_t*>(cx.q) + q0 + 32 * i);
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (kF32) {
+                const float* src = static_cast<const float*>(cx.q) + q0 + 32 * i;
+                op.qa[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src));
+                op.qal[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(src + 4));
+            } else {
+                op.qa[i] = load8(static_cast<const uint16_t*>(cx.q) + q0 + 32 * i);
+            }
+        }
     }
     const int tv = 16 * w + (l >> 2);
     const int tv_c = tv < len ? tv : len - 1;
@@ -754,12 +750,12 @@ GDN_DEV void fetch_output(OutputOperands& op, const StatePassCtx& cx, int c, int
     }
 }
 
-// kF32 (float32 q, k, v): K, Q and V also keep their bf16 residuals.
+// kF32 (float32 q, k, v): K and V also keep their bf16 residuals (Q stays
+// in the output waves' registers for either input).
 template <bool kF32>
 struct StatePassLds {
     uint16_t Ss_hi[kSliceRows * kSS], Ss_lo[kSliceRows * kSS];  // S[dv][dk]
     uint16_t Kr[2][kChunk * kHD];                                 // K[token][dk] (swizzled), two buffers
-    uint16_t Qs[kF32 ? kChunk * kQS : 8];                         // Q[token][dk] (float32 input)
     uint16_t Tb_hi[kChunk * kTS], Tb_lo[kChunk * kTS];            // Tb[token][token]
     uint16_t Vs[kChunk * kSliceRows];                             // V[token][dv]
     uint16_t Rs_hi[kSliceRows * kTS], Rs_lo[kSliceRows * kTS];    // R[dv][token]
@@ -767,7 +763,6 @@ struct StatePassLds {
     uint16_t D2_hi[kSliceRows * kTS], D2_lo[kSliceRows * kTS];    // D''[dv][token]
     float ex[2 * kChunk];                                         // exp(l), exp(l_C - l)
     uint16_t Kr_lo[kF32 ? 2 : 1][kF32 ? kChunk * kHD : 8];        // residuals (float32 input)
-    uint16_t Qs_lo[kF32 ? kChunk * kQS : 8];
     uint16_t Vs_lo[kF32 ? kChunk * kSliceRows : 8];
 };
 
@@ -810,20 +805,6 @@ GDN_DEV void stage_k(const StagedOperands& op, StatePassLds<kF32>& sm, int buf, 
         } else {
             *reinterpret_cast<bf16x8*>(sm.Kr[buf] + o) = op.ka[i];
         }
-    }
-}
-
-// Wave w's Q rows are read only by wave w (in output_project), so the next
-// chunk's may be written as soon as this wave's projection has read them.
-template <bool kF32>
-GDN_DEV void stage_q(const StagedOperands& op, StatePassLds<kF32>& sm, int w, int l) {
-    const int o = (16 * w + (l >> 4)) * kQS + 8 * (l & 15);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        bf16x8 hi, lo;
-        split8_bits(op.qa[i], op.qal[i], hi, lo);
-        *reinterpret_cast<bf16x8*>(sm.Qs + o + 4 * i * kQS) = hi;
-        *reinterpret_cast<bf16x8*>(sm.Qs_lo + o + 4 * i * kQS) = lo;
     }
 }
 
@@ -982,19 +963,19 @@ GDN_DEV void state_update(f32x4 (&acc)[2], const StatePassLds<kF32>& sm, int buf
 }
 
 // Output waves, part 1 (between the staging and R barriers): exp(l) Q S^T,
-// Q from the wave's registers (the chunk's operands; float32 input: LDS).
+// Q from the wave's registers (the chunk's operands).
 template <bool kF32>
 GDN_DEV f32x4 output_project(const StagedOperands& op, const StatePassLds<kF32>& sm, int w, int l) {
     const int lr = l & 15, lq = l >> 4, lg8 = 8 * lq;
-    const int qo = (16 * w + lr) * kQS + lg8;
     f32x4 xq = {0.f, 0.f, 0.f, 0.f}, xq2 = xq;
 #pragma unroll
     for (int s = 0; s < kHD / 32; ++s) {
-        const bf16x8 qa = kF32 ? load8(sm.Qs + qo + 32 * s) : op.qa[s];
+        bf16x8 qa = op.qa[s], ql;
+        if constexpr (kF32) split8_bits(op.qa[s], op.qal[s], qa, ql);
         const bf16x8 sh = load8(sm.Ss_hi + lr * kSS + 32 * s + lg8);
         xq = mfma16(qa, sh, xq);
         xq2 = mfma16(qa, load8(sm.Ss_lo + lr * kSS + 32 * s + lg8), xq2);
-        if constexpr (kF32) xq2 = mfma16(load8(sm.Qs_lo + qo + 32 * s), sh, xq2);
+        if constexpr (kF32) xq2 = mfma16(ql, sh, xq2);
     }
     xq += xq2;
     const float4 el = *reinterpret_cast<const float4*>(sm.ex + 16 * w + 4 * lq);
@@ -1088,7 +1069,6 @@ GDN_DEV void output_loop_2ahead(const StatePassCtx& cx, int nch, StatePassLds<kF
         fetch_output<kUpper>(on, cx, c + 1 < last ? c + 1 : last, w, l);
         __builtin_amdgcn_sched_barrier(0);  // the prefetches stay where they are issued
         __syncthreads();
-        if constexpr (kF32) stage_q(gn, sm, w, l);
         stage_k(gn, sm, buf ^ 1, w, l);
         stage_v(gn, sm, w, l);
         fetch_staged<kUpper, kF32>(gf, cx, c + 2 < last ? c + 2 : last, w, l);
@@ -1101,7 +1081,6 @@ GDN_DEV void output_loop_2ahead(const StatePassCtx& cx, int nch, StatePassLds<kF
     fetch_staged<kUpper, kF32>(gb, cx, 0, w, l);
     fetch_staged<kUpper, kF32>(ga, cx, 1 < last ? 1 : last, w, l);
     fetch_output<kUpper>(oa, cx, 0, w, l);
-    if constexpr (kF32) stage_q(gb, sm, w, l);
     stage_k(gb, sm, 0, w, l);
     stage_v(gb, sm, w, l);
     stage_tb_e<kUpper>(gb, sm, w, l);
