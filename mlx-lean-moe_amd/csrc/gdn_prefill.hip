@@ -88,6 +88,12 @@ GDN_DEV void load_split8(const float* p, u16x8& hi, u16x8& lo) {
     }
 }
 
+// A value loaded as its raw bits (the low 16 for bf16 and f16) as float.
+GDN_DEV float raw_to_f32(uint32_t raw, int dtype) {
+    if (dtype == GDN_F32) return __uint_as_float(raw);
+    return dtype == GDN_BF16 ? bf16_bits_to_f32(uint16_t(raw)) : f16_bits_to_f32(uint16_t(raw));
+}
+
 GDN_DEV bf16x8 zero8() {
     bf16x8 z;
 #pragma unroll
@@ -305,6 +311,18 @@ GDN_DEV void prefill_chunk_body(
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
     char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
 
+    // The gate inputs of wave 0 (lane = token) go out first, as raw words
+    // decoded where they are used, so that the gates' prefix sum does not
+    // wait behind the K and Q loads.
+    uint32_t ga_raw = 0, gb_raw = 0;
+    if (w == 0) {
+        const int lc = l < pos.len ? l : pos.len - 1;
+        const int64_t i = (pos.t0 + lc) * gate_stride + hv;
+        ga_raw = gate_mode == 1 || gb_dtype == GDN_F32 ? static_cast<const uint32_t*>(ga)[i]
+                                                       : static_cast<const uint16_t*>(ga)[i];
+        gb_raw = gb_dtype == GDN_F32 ? static_cast<const uint32_t*>(gb)[i] : static_cast<const uint16_t*>(gb)[i];
+    }
+
     // K and Q of the chunk: every load issued before the first LDS store
     // (rows past the run are read clamped and stored as zero).
     u16x8 kv[4], qv[4], kvl[4], qvl[4];
@@ -348,16 +366,15 @@ GDN_DEV void prefill_chunk_body(
     // Gates (wave 0, lane = token): l2 = inclusive prefix sum of log2 g
     // (exp2 of differences gives the decays).
     if (w == 0) {
-        const int lc = l < pos.len ? l : pos.len - 1;
-        const int64_t i = (pos.t0 + lc) * gate_stride + hv;
         float lg, beta;
+        const float gbv = raw_to_f32(gb_raw, gb_dtype);
         if (gate_mode == 0) {
-            lg = log_forget_gate(load_any(ga, i, gb_dtype), A_log[hv], dt_bias[hv]);
-            beta = beta_of(load_any(gb, i, gb_dtype), gb_dtype);
+            lg = log_forget_gate(raw_to_f32(ga_raw, gb_dtype), A_log[hv], dt_bias[hv]);
+            beta = beta_of(gbv, gb_dtype);
         } else {
-            const float gv = static_cast<const float*>(ga)[i];
+            const float gv = __uint_as_float(ga_raw);
             lg = gv > 0.f ? logf(gv) : kLogGateFloor;
-            beta = load_any(gb, i, gb_dtype);
+            beta = gbv;
         }
         lg = l < pos.len ? fmaxf(lg, kLogGateFloor) * kLog2e : 0.f;
         beta = l < pos.len ? beta : 0.f;
