@@ -832,13 +832,15 @@ def bench_also(dev, cpu=True):
     sm = bench_decode(dev, 64, 16, 32, False, steps=64, warmup=8)
     d1 = bench_decode_graph(dev, 1, 16, 32, True)
     d1n = bench_decode_graph(dev, 1, 16, 32, False)
-    pf = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3)
-    pv = bench_prefill(dev, 0, 0, 16, 32, steps=5, warmup=2, lens=VARLEN_LENS)
-    p32 = bench_prefill(dev, 1, 4096, 16, 32, steps=20, warmup=3, dtype=torch.float32,
+    # ~0.1-2 ms per call: enough steps that the clocks have settled (20
+    # steps after 3 read ~8 % slower than 256 after 20)
+    pf = bench_prefill(dev, 1, 4096, 16, 32, steps=100, warmup=20)
+    pv = bench_prefill(dev, 0, 0, 16, 32, steps=20, warmup=4, lens=VARLEN_LENS)
+    p32 = bench_prefill(dev, 1, 4096, 16, 32, steps=100, warmup=20, dtype=torch.float32,
                         compare_scan=True)
     sl = bench_decode_slots(dev, 64, 16, 32, steps=64, warmup=8)
     ld = bench_layer_decode(dev, 64, steps=64, warmup=8)
-    lp = bench_layer_prefill(dev, 4096, steps=20, warmup=3)
+    lp = bench_layer_prefill(dev, 4096, steps=50, warmup=10)
     return {
         "decode_b64": {
             "workload": DECODE_WORKLOADS[True], "tokens_per_s": sm["tokens_per_s"],
