@@ -25,7 +25,9 @@
 //
 // Few sequences (B * Hv below 256 workgroups, a single sequence above all)
 // leave most of the 256 CUs idle, so there a step without the gated norm
-// gives each head kSplit workgroups: split p reads, updates and stores rows
+// gives each head kSplit workgroups (and from kPairSplitHeads heads on, two:
+// half-tile workgroups need fewer registers, more of them stay resident and
+// the HBM stream runs closer to its ceiling): split p reads, updates and stores rows
 // [row0, row0 + 128 / kSplit), row0 = p * 128 / kSplit (rows r_i = row0 +
 // 8 i + 2 w + half, i < 16 / kSplit, and a reduce-scatter over 32 / kSplit
 // values per lane on the same butterfly). Each row's arithmetic is the
@@ -58,6 +60,11 @@ constexpr int kTaps = 4;  // conv kernel K
 #ifndef GDN_DECODE_MAX_SPLIT
 #define GDN_DECODE_MAX_SPLIT 8
 #endif
+// From this many (sequence, head) pairs a step without the norm runs two
+// workgroups per head (measured, Hv=32: B=64 49.3 -> 46.9 us, B=128 96.3 ->
+// 91.4, B=256 186.0 -> 178.5; B=32 unchanged, smaller batches slower with
+// more splits).
+constexpr int64_t kPairSplitHeads = 2048;
 constexpr int64_t kSplitGroups = GDN_DECODE_SPLIT_GROUPS;
 constexpr int kMaxSplit = GDN_DECODE_MAX_SPLIT;
 static_assert(kMaxSplit >= 1 && kMaxSplit <= 16 && (kMaxSplit & (kMaxSplit - 1)) == 0,
@@ -383,10 +390,11 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                  reinterpret_cast<uintptr_t>(conv_weight)) % 16 == 0,
                 "gdn_decode_step: state and conv weight must be 16-byte aligned");
     // Below kSplitGroups workgroups a step without the norm shares each head
-    // among up to kMaxSplit workgroups.
+    // among up to kMaxSplit workgroups; from kPairSplitHeads heads, two.
     const int64_t heads = int64_t(B) * Hv;
     int split = 1;
     while (!z && split < kMaxSplit && heads * split * 2 <= kSplitGroups) split *= 2;
+    if (!z && kMaxSplit >= 2 && heads >= kPairSplitHeads) split = 2;
     GDN_REQUIRE(heads * split <= INT32_MAX, "gdn_decode_step: B * Hv too large");
     const dim3 grid(unsigned(heads * split)), block(kDecodeThreads);
     hipStream_t s = as_stream(stream);

@@ -10,7 +10,9 @@ the whole tile would race with the other splits' in-place rows); the same
 comparison covers them. Also checked against the C oracle (gdn_ref.c) at B=1
 and B=4 over chained steps, and on a slot pool whose conv half bits the
 kernel flips (each slot's bit once per step, counted over all the
-workgroups of its heads)."""
+workgroups of its heads). From 2048 (sequence, head) pairs a step without
+the norm runs two workgroups per head again (B=64 at Hv=32): checked the
+same way against one workgroup per head, directly and through a pool."""
 
 from __future__ import annotations
 
@@ -151,3 +153,56 @@ def test_split_decode_on_a_pool_flips_each_slot_once_per_step(gpu):
         cur = torch.from_numpy(np.arange(P) + P * bits).to(gpu)
         np.testing.assert_array_equal(conv_buf[cur].float().cpu().numpy(), ref_conv)
         assert max_rel(state.cpu().numpy(), ref_state) < 1e-5, step
+
+
+def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu):
+    """B=64 (B * Hv = 2048 heads): a step without the gated norm gives each
+    head two workgroups. Over three chained in-place steps its output equals
+    sequences 0-7 decoded alone (256 heads, one workgroup each), and its conv
+    and ssm state equal the same steps taken with the gated norm (one
+    workgroup per head at every B), bit for bit. Then the same steps through
+    a 64-slot pool in reverse slot order, the kernel flipping each slot's conv
+    half bit once per step (2 * Hv arrivals per slot): the same outputs and
+    states, and the arrival counters back at zero."""
+
+    B, adt = 64, torch.bfloat16
+    c = _case(70, B, True)
+    params = _params(c, gpu)
+    st_split, cv_split = _dev(c["state"], gpu), _dev(c["conv"], gpu, adt)
+    st_norm, cv_norm = _dev(c["state"], gpu), _dev(c["conv"], gpu, adt)
+    st8, cv8 = _dev(c["state"][:8], gpu), _dev(c["conv"][:8], gpu, adt)
+    outs = []
+    for step, x in enumerate(c["steps"][:3]):
+        out, cv_split, _ = _step(x, slice(0, B), cv_split, st_split, params, gpu, adt, False,
+                                 y_dtype=adt)
+        _, cv_norm, _ = _step(x, slice(0, B), cv_norm, st_norm, params, gpu, adt, True)
+        out8, cv8, _ = _step(x, slice(0, 8), cv8, st8, params, gpu, adt, False, y_dtype=adt)
+        outs.append(out)
+        assert torch.equal(out[:8], out8), step
+        assert torch.equal(cv_split, cv_norm), step
+        assert torch.equal(st_split, st_norm), step
+
+    # sequence i in slot P - 1 - i of a pool of P = B slots
+    P = B
+    slot_of = np.arange(P)[::-1].copy()
+    bits0 = (np.arange(P) % 3 == 0).astype(np.int32)
+    conv_buf = torch.zeros((2 * P, 3, DIMS.conv_dim), dtype=adt, device=gpu)
+    pool = torch.empty((P, HV, D, D), dtype=torch.float32, device=gpu)
+    for i in range(B):
+        sl = int(slot_of[i])
+        conv_buf[sl + P * int(bits0[sl])] = _dev(c["conv"][i], gpu, adt)
+        pool[sl] = _dev(c["state"][i], gpu)
+    half = torch.from_numpy(bits0.copy()).to(gpu)
+    arrivals = torch.zeros(P, dtype=torch.int32, device=gpu)
+    slots = torch.from_numpy(slot_of.astype(np.int32)).to(gpu)
+    for step, x in enumerate(c["steps"][:3]):
+        out, _, _ = gdn.fused_decode_step(
+            _dev(x["qkv"], gpu, adt), None, _dev(x["a"], gpu, adt), _dev(x["b"], gpu, adt),
+            conv_buf, pool, *params[:3], None, 1e-6, DIMS, slots=slots, conv_half=half,
+            conv_arrivals=arrivals, y_dtype=adt)
+        assert torch.equal(out, outs[step]), step
+        np.testing.assert_array_equal(half.cpu().numpy(), bits0 ^ ((step + 1) & 1))
+        assert not arrivals.any()
+    cur = torch.from_numpy(slot_of + P * half.cpu().numpy()[slot_of]).to(gpu)
+    assert torch.equal(conv_buf[cur], cv_norm)
+    assert torch.equal(pool[torch.from_numpy(slot_of).to(gpu)], st_norm)
