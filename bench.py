@@ -26,10 +26,13 @@ Also measured in the same run (reported under "also"):
   --batch B active sequences, 64 by default)
   layer_prefill: the whole layer over a 4096-token prompt, 4-bit
   projections (--workload layer_prefill: the same alone)
+  decode_sizes (alone only): the decode kernel without the gated norm at
+  Hk=16, Hv=32 over B = 1 .. 256, and the headline configuration: kernel
+  time and fraction of HBM at each size
 
 python bench.py [--steps K] [--warmup W] [--batch B]
-                [--workload decode|decode_b64|decode_b1|decode_slots|layer_decode|layer_prefill|
-                            prefill|prefill_f32|prefill_varlen|qlinear|copy]
+                [--workload decode|decode_b64|decode_b1|decode_slots|decode_sizes|layer_decode|
+                            layer_prefill|prefill|prefill_f32|prefill_varlen|qlinear|copy]
 (--workload decode_large is the default decode workload under its older name.)
 """
 
@@ -886,7 +889,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_large", "decode_b64", "decode_b1", "decode_slots", "layer_decode",
+                    choices=["decode", "decode_large", "decode_b64", "decode_b1", "decode_slots", "decode_sizes",
+                             "layer_decode",
                              "layer_prefill", "prefill_f32",
                              "prefill", "prefill_varlen", "qlinear", "copy"])
     ap.add_argument("--layers", type=int, default=1,
@@ -903,6 +907,21 @@ def main(argv=None):
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.workload == "decode_sizes":
+        # the HBM fraction the decode kernel reaches as the batch grows (one
+        # launch per step, state in four rotating buffers)
+        sizes = {}
+        for B in (1, 8, 32, 64, 128, 256):
+            r = bench_decode(dev, B, 16, 32, False, steps=max(args.steps, 64), warmup=max(args.warmup, 8))
+            sizes[f"B={B} Hv=32"] = {"kernel_us": r["kernel_us"], "hbm_frac": r["hbm_frac"],
+                                     "bytes_per_step": r["bytes_per_step"]}
+        r = bench_decode(dev, 256, 16, 64, True, steps=max(args.steps, 64), warmup=max(args.warmup, 8))
+        sizes["B=256 Hv=64 + gated norm"] = {"kernel_us": r["kernel_us"], "hbm_frac": r["hbm_frac"],
+                                             "bytes_per_step": r["bytes_per_step"]}
+        print(json.dumps({"workload": "gdn_decode_step over batch sizes (Hk=16, fused conv roll)",
+                          "sizes": sizes}))
+        return 0
 
     if args.workload == "copy":
         # Plain 1 GiB device copy: the HBM read+write ceiling a copy reaches,
