@@ -155,7 +155,8 @@ def test_split_decode_on_a_pool_flips_each_slot_once_per_step(gpu):
         assert max_rel(state.cpu().numpy(), ref_state) < 1e-5, step
 
 
-def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu):
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu, act):
     """B=64 (B * Hv = 2048 heads): a step without the gated norm gives each
     head two workgroups. Over three chained in-place steps its output equals
     sequences 0-7 decoded alone (256 heads, one workgroup each), and its conv
@@ -165,8 +166,9 @@ def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu):
     half bit once per step (2 * Hv arrivals per slot): the same outputs and
     states, and the arrival counters back at zero."""
 
-    B, adt = 64, torch.bfloat16
-    c = _case(70, B, True)
+    bf16 = act == "bf16"
+    B, adt = 64, torch.bfloat16 if bf16 else torch.float32
+    c = _case(70 + bf16, B, bf16)
     params = _params(c, gpu)
     st_split, cv_split = _dev(c["state"], gpu), _dev(c["conv"], gpu, adt)
     st_norm, cv_norm = _dev(c["state"], gpu), _dev(c["conv"], gpu, adt)
@@ -174,9 +176,9 @@ def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu):
     outs = []
     for step, x in enumerate(c["steps"][:3]):
         out, cv_split, _ = _step(x, slice(0, B), cv_split, st_split, params, gpu, adt, False,
-                                 y_dtype=adt)
+                                 y_dtype=torch.bfloat16)
         _, cv_norm, _ = _step(x, slice(0, B), cv_norm, st_norm, params, gpu, adt, True)
-        out8, cv8, _ = _step(x, slice(0, 8), cv8, st8, params, gpu, adt, False, y_dtype=adt)
+        out8, cv8, _ = _step(x, slice(0, 8), cv8, st8, params, gpu, adt, False, y_dtype=torch.bfloat16)
         outs.append(out)
         assert torch.equal(out[:8], out8), step
         assert torch.equal(cv_split, cv_norm), step
@@ -199,7 +201,7 @@ def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu):
         out, _, _ = gdn.fused_decode_step(
             _dev(x["qkv"], gpu, adt), None, _dev(x["a"], gpu, adt), _dev(x["b"], gpu, adt),
             conv_buf, pool, *params[:3], None, 1e-6, DIMS, slots=slots, conv_half=half,
-            conv_arrivals=arrivals, y_dtype=adt)
+            conv_arrivals=arrivals, y_dtype=torch.bfloat16)
         assert torch.equal(out, outs[step]), step
         np.testing.assert_array_equal(half.cpu().numpy(), bits0 ^ ((step + 1) & 1))
         assert not arrivals.any()
