@@ -26,8 +26,9 @@
 // Few sequences (B * Hv below 256 workgroups, a single sequence above all)
 // leave most of the 256 CUs idle, so there a step without the gated norm
 // gives each head kSplit workgroups (and from kPairSplitHeads heads on, two:
-// half-tile workgroups need fewer registers, more of them stay resident and
-// the HBM stream runs closer to its ceiling): split p reads, updates and stores rows
+// two independently scheduled half-tile workgroups per head keep the HBM
+// stream closer to its ceiling than one; one 512-thread workgroup holding
+// both halves does not): split p reads, updates and stores rows
 // [row0, row0 + 128 / kSplit), row0 = p * 128 / kSplit (rows r_i = row0 +
 // 8 i + 2 w + half, i < 16 / kSplit, and a reduce-scatter over 32 / kSplit
 // values per lane on the same butterfly). Each row's arithmetic is the
