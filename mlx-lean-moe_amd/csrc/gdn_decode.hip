@@ -38,7 +38,11 @@
 // together: exchanging them between workgroups (a device-scope release and
 // acquire each) costs more than the split saves, and reading the whole tile
 // in every split races with the in-place update of the other splits' rows,
-// so a step with the norm keeps one workgroup per head.
+// so a step with the norm keeps one workgroup per head. With few heads
+// (at most kSubHeads) that workgroup has kSub = 2 row blocks of 256 threads,
+// each laid out as one workgroup of a two-way split (rows rb0 + 8 i + 2 w +
+// half): twice the loads in flight per CU, one front-end, the head's outputs
+// together in LDS for the norm.
 #include "gdn_common.h"
 #include "gdn_host.h"
 
@@ -66,6 +70,10 @@ constexpr int kTaps = 4;  // conv kernel K
 // 91.4, B=256 186.0 -> 178.5; B=32 unchanged, smaller batches slower with
 // more splits).
 constexpr int64_t kPairSplitHeads = 2048;
+// Up to this many heads a step with the norm runs 512-thread workgroups
+// (measured, Hv=32: B=1 5.65 -> 5.39 us, B=8 8.58 -> 7.90; B=16 slower, and
+// B=256, Hv=64 369 -> 389 us).
+constexpr int64_t kSubHeads = 256;
 constexpr int64_t kSplitGroups = GDN_DECODE_SPLIT_GROUPS;
 constexpr int kMaxSplit = GDN_DECODE_MAX_SPLIT;
 static_assert(kMaxSplit >= 1 && kMaxSplit <= 16 && (kMaxSplit & (kMaxSplit - 1)) == 0,
@@ -166,8 +174,8 @@ GDN_DEV void roll_taps(const ConvTaps& t, typename Act::storage* __restrict__ cs
     Act::store(cso, 2 * C + c, t.x3);
 }
 
-template <class Act, bool kNorm, int kSplit>
-__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
+template <class Act, bool kNorm, int kSplit, int kSub = 1>
+__global__ __launch_bounds__(kDecodeThreads * kSub) void decode_kernel(
     const typename Act::storage* __restrict__ qkv, const typename Act::storage* __restrict__ cs_in,
     typename Act::storage* __restrict__ cs_out, const float* __restrict__ conv_w,
     const typename Act::storage* __restrict__ a_in, const typename Act::storage* __restrict__ b_in,
@@ -178,8 +186,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     int64_t qkv_stride, int64_t z_stride, int64_t a_stride, int64_t b_stride) {
     static_assert(kSplit >= 1 && kSplit <= 16 && (kSplit & (kSplit - 1)) == 0, "kSplit: 1, 2, 4, 8 or 16");
     static_assert(!kNorm || kSplit == 1, "the gated norm runs one workgroup per head");
-    constexpr int kRows = kD / kSplit;  // state rows per workgroup
-    constexpr int kR = 16 / kSplit;     // state rows per thread
+    static_assert(kSub == 1 || (kSub == 2 && kSplit == 1), "kSub: 1, or 2 row blocks of a whole head");
+    constexpr int kRows = kD / kSplit;        // state rows per workgroup
+    constexpr int kR = 16 / (kSplit * kSub);  // state rows per thread
     constexpr int kN = 2 * kR;          // S.k and S.q partials per thread
     __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
     __shared__ float gate_g, gate_beta, norm_r;
@@ -191,7 +200,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const int b = bh / Hv, h = bh % Hv;
     const int r = Hv / Hk, hk = h / r;
     const int tid = threadIdx.x;
-    const int w = tid >> 6, l = tid & 63, half = l >> 5, l32 = l & 31;
+    const int wg = tid >> 6;  // the wave in the workgroup
+    // the thread's 256-thread row block: rows rb0 .. rb0 + kRows / kSub - 1
+    const int t8 = kSub == 1 ? tid : tid & (kDecodeThreads - 1);
+    const int rb0 = row0 + (kSub == 1 ? 0 : (tid >> 8) * (kRows / kSub));
+    const int w = t8 >> 6, l = t8 & 63, half = l >> 5, l32 = l & 31;
     typename Act::storage* yo = static_cast<typename Act::storage*>(out);
     // the state slot of batch row b (its state tile is read and written
     // there) and its conv state rows (read at ci, rolled into co): the slot
@@ -238,13 +251,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     const float4* Sb = reinterpret_cast<const float4*>(S_in + sh * kD * kD);
     float4 s[kR];
 #pragma unroll
-    for (int i = 0; i < kR; ++i) s[i] = load_state(&Sb[(row0 + 8 * i + 2 * w + half) * (kD / 4) + l32]);
+    for (int i = 0; i < kR; ++i) s[i] = load_state(&Sb[(rb0 + 8 * i + 2 * w + half) * (kD / 4) + l32]);
 
-    // B. front-end for this head's channels.
-    (tid < kD ? qs : ks)[e] = conv_silu<Act>(t1);
-    // q/k channels are shared by the r value heads of a key head: the first
-    // workgroup of the first of them rolls their conv state.
-    if (first && h % r == 0) roll_taps<Act>(t1, cso, C, c1);
+    // B. front-end for this head's channels (the first 256 threads).
+    if (kSub == 1 || tid < 2 * kD) {
+        (tid < kD ? qs : ks)[e] = conv_silu<Act>(t1);
+        // q/k channels are shared by the r value heads of a key head: the first
+        // workgroup of the first of them rolls their conv state.
+        if (first && h % r == 0) roll_taps<Act>(t1, cso, C, c1);
+    }
     // the two gates on two otherwise idle waves, in parallel
     if (tid < kD) {
         vs[e] = conv_silu<Act>(t2);
@@ -255,17 +270,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
         gate_beta = beta_of(bv, Act::code);
     }
     __syncthreads();
-    if (w < 2) {
+    if (wg < 2) {
         // rms_norm(x, 1e-6) rounded once from its exact value: the sum of
         // squares (exact in double for activation-dtype inputs), the
         // reciprocal root and the products in double; then the scale, whose
         // product with a 16-bit value is exact in float32
-        float* arr = w == 0 ? qs : ks;
+        float* arr = wg == 0 ? qs : ks;
         const float x0 = arr[l], x1 = arr[l + 64];
         const double ss = group_sum<kWave>(double(x0) * x0 + double(x1) * x1);
         const double rr = rsqrt(ss / kD + 1e-6);
         const float inv = 1.f / sqrtf(float(kD));
-        const float sc = Act::round(w == 0 ? inv * inv : inv);
+        const float sc = Act::round(wg == 0 ? inv * inv : inv);
         arr[l] = Act::round(sc * round_once(x0 * rr, Act::code));
         arr[l + 64] = Act::round(sc * round_once(x1 * rr, Act::code));
     }
@@ -290,7 +305,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     // rows, 16 / kR lanes hold each total and write the same value.
     {
         const int idx = l32 >> (5 - ilog2(kN));
-        const int row = row0 + 8 * (idx & (kR - 1)) + 2 * w + half;
+        const int row = rb0 + 8 * (idx & (kR - 1)) + 2 * w + half;
         const float tot = vals[0];
         const float delta = (vs[row] - g * tot) * beta;
         float delta_pair = delta, unused = delta;  // lanes >= 16: the partner's delta
@@ -310,7 +325,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
     float4* So = reinterpret_cast<float4*>(S_out + sh * kD * kD);
 #pragma unroll
     for (int i = 0; i < kR; ++i) {
-        const int row = row0 + 8 * i + 2 * w + half;
+        const int row = rb0 + 8 * i + 2 * w + half;
         const float d = deltas[row];
         float4 o;
         o.x = g * s[i].x + d * kk.x;
@@ -325,7 +340,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(
         if (tid < kRows) store_any(out, size_t(bh) * kD + row0 + tid, y_dtype, ys[row0 + tid]);
         return;
     }
-    if (w == 0) {
+    if (wg == 0) {
         const float y0 = Act::round(ys[l]), y1 = Act::round(ys[l + 64]);
         const float ss = group_sum<kWave>(y0 * y0 + y1 * y1);
         if (l == 0) norm_r = 1.f / sqrtf(ss / float(kD) + eps);
@@ -397,10 +412,11 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
     while (!z && split < kMaxSplit && heads * split * 2 <= kSplitGroups) split *= 2;
     if (!z && kMaxSplit >= 2 && heads >= kPairSplitHeads) split = 2;
     GDN_REQUIRE(heads * split <= INT32_MAX, "gdn_decode_step: B * Hv too large");
-    const dim3 grid(unsigned(heads * split)), block(kDecodeThreads);
+    const dim3 grid(unsigned(heads * split));
+    const bool two_blocks = z && heads <= kSubHeads;  // the norm's workgroup: 512 threads
     hipStream_t s = as_stream(stream);
-#define GDN_DECODE_LAUNCH(ACT, NORM, SPLIT)                                                   \
-    hipLaunchKernelGGL((decode_kernel<ACT, NORM, SPLIT>), grid, block, 0, s,                  \
+#define GDN_DECODE_LAUNCH(ACT, NORM, SPLIT, SUB)                                              \
+    hipLaunchKernelGGL((decode_kernel<ACT, NORM, SPLIT, SUB>), grid, dim3(kDecodeThreads * SUB), 0, s, \
                        static_cast<const ACT::storage*>(qkv),                                 \
                        static_cast<const ACT::storage*>(conv_state_in),                       \
                        static_cast<ACT::storage*>(conv_state_out), conv_weight,               \
@@ -410,16 +426,20 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
                        conv_arrivals, st[0], st[1], st[2], st[3])
 #define GDN_DECODE_SPLITS(ACT, NORM)                                   \
     switch (split) {                                                  \
-        case 1: GDN_DECODE_LAUNCH(ACT, NORM, 1); break;               \
-        case 2: GDN_DECODE_LAUNCH(ACT, NORM, 2); break;               \
-        case 4: GDN_DECODE_LAUNCH(ACT, NORM, 4); break;               \
-        case 8: GDN_DECODE_LAUNCH(ACT, NORM, 8); break;               \
-        default: GDN_DECODE_LAUNCH(ACT, NORM, 16); break;             \
+        case 1: GDN_DECODE_LAUNCH(ACT, NORM, 1, 1); break;            \
+        case 2: GDN_DECODE_LAUNCH(ACT, NORM, 2, 1); break;            \
+        case 4: GDN_DECODE_LAUNCH(ACT, NORM, 4, 1); break;            \
+        case 8: GDN_DECODE_LAUNCH(ACT, NORM, 8, 1); break;            \
+        default: GDN_DECODE_LAUNCH(ACT, NORM, 16, 1); break;          \
     }
     if (act_dtype == GDN_BF16) {
-        if (z) GDN_DECODE_LAUNCH(ActBF16, true, 1); else GDN_DECODE_SPLITS(ActBF16, false)
+        if (z && two_blocks) GDN_DECODE_LAUNCH(ActBF16, true, 1, 2);
+        else if (z) GDN_DECODE_LAUNCH(ActBF16, true, 1, 1);
+        else GDN_DECODE_SPLITS(ActBF16, false)
     } else {
-        if (z) GDN_DECODE_LAUNCH(ActF32, true, 1); else GDN_DECODE_SPLITS(ActF32, false)
+        if (z && two_blocks) GDN_DECODE_LAUNCH(ActF32, true, 1, 2);
+        else if (z) GDN_DECODE_LAUNCH(ActF32, true, 1, 1);
+        else GDN_DECODE_SPLITS(ActF32, false)
     }
 #undef GDN_DECODE_SPLITS
 #undef GDN_DECODE_LAUNCH

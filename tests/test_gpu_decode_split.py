@@ -1,12 +1,13 @@
 """GPU tests of the fused decode's row split. With few sequences (B * Hv up
 to 128) a step without the gated norm shares each value head among several
 workgroups, each reading, updating and storing its share of the 128 state
-rows: 8 at B=1, 4 at B=2 and 2 at B=4 for Hv=32. A batch of 8 (B * Hv =
-256) runs one workgroup per head, and decoding the same sequences in it
-gives the reference bits: the split launches must reproduce output, conv
-state and ssm state bit for bit, with the state updated in place. Steps
-with the gated norm keep one workgroup per head at every B (a split reading
-the whole tile would race with the other splits' in-place rows); the same
+rows: 8 at B=1, 4 at B=2 and 2 at B=4 for Hv=32. A batch of 16 (B * Hv =
+512) runs one 256-thread workgroup per head, and decoding the same
+sequences in it gives the reference bits: the split launches must
+reproduce output, conv state and ssm state bit for bit, with the state
+updated in place. Steps with the gated norm keep one workgroup per head at
+every B (a split reading the whole tile would race with the other splits'
+in-place rows), of 512 threads up to 256 heads (two row blocks); the same
 comparison covers them. Also checked against the C oracle (gdn_ref.c) at B=1
 and B=4 over chained steps, and on a slot pool whose conv half bits the
 kernel flips (each slot's bit once per step, counted over all the
@@ -67,19 +68,20 @@ def _step(x, rows, conv, state, params, gpu, adt, with_z, **kw):
 @pytest.mark.parametrize("act", ["bf16", "f32"])
 @pytest.mark.parametrize("with_z", [True, False])
 def test_split_launches_match_one_workgroup_per_head_bit_for_bit(gpu, act, with_z):
-    """Sequences 0..B-1 decoded alone (B = 1, 2, 4; without the norm split
-    8, 4, 2) against the same sequences inside the batch of 8, over four
-    chained in-place steps: output, rolled conv state and ssm state
-    identical."""
+    """Sequences 0..B-1 decoded alone (B = 1, 2, 4, 8; without the norm
+    split 8, 4, 2, 1; with it, 512-thread workgroups) against the same
+    sequences inside the batch of 16 (one 256-thread workgroup per head),
+    over four chained in-place steps: output, rolled conv state and ssm
+    state identical."""
 
     bf16 = act == "bf16"
     adt = torch.bfloat16 if bf16 else torch.float32
-    c = _case(40 + bf16 + 2 * with_z, 8, bf16)
+    c = _case(40 + bf16 + 2 * with_z, 16, bf16)
     params = _params(c, gpu)
     ref_state, ref_conv = _dev(c["state"], gpu), _dev(c["conv"], gpu, adt)
-    runs = {B: (_dev(c["state"][:B], gpu), _dev(c["conv"][:B], gpu, adt)) for B in (1, 2, 4)}
+    runs = {B: (_dev(c["state"][:B], gpu), _dev(c["conv"][:B], gpu, adt)) for B in (1, 2, 4, 8)}
     for step, x in enumerate(c["steps"]):
-        ref_out, ref_conv, _ = _step(x, slice(0, 8), ref_conv, ref_state, params, gpu, adt, with_z)
+        ref_out, ref_conv, _ = _step(x, slice(0, 16), ref_conv, ref_state, params, gpu, adt, with_z)
         for B, (state, conv) in runs.items():
             out, conv_new, _ = _step(x, slice(0, B), conv, state, params, gpu, adt, with_z)
             runs[B] = (state, conv_new)
