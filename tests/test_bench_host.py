@@ -36,3 +36,17 @@ def test_decode_bytes_of_the_measured_workloads():
 def test_prefill_flops_of_the_measured_workload():
     # T=4096, Hv=32: T Hv (10 64 d + 6 d^2), 23.62 GFLOP
     assert bench.prefill_flops(4096, 32) == 23_622_320_128
+
+
+def test_committed_traffic_figures_match_the_algorithmic_bytes():
+    """The rocprofv3 FETCH/WRITE totals the roofline lines carry: the decode
+    launches move within a few percent of their algorithmic bytes (no
+    re-reads); the prefill call's 2.6x is its records and the slices'
+    re-reads of K, Q and the records."""
+
+    b64 = bench.load_traffic("gdn_decode_step_b64_hv32_traffic.json")
+    b256 = bench.load_traffic("gdn_decode_step_b256_hv64_traffic.json")
+    prefill = bench.load_traffic("gdn_prefill_chunked_t4096_traffic.json")
+    assert 1.0 <= b64 / bench.decode_bytes(64, 16, 32, 128, 4, False)[2] < 1.05
+    assert 1.0 <= b256 / bench.decode_bytes(256, 16, 64, 128, 4, True)[2] < 1.05
+    assert 2.0 < prefill / 105e6 < 3.0
