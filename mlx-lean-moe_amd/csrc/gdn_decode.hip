@@ -191,7 +191,7 @@ __global__ __launch_bounds__(kDecodeThreads * kSub) void decode_kernel(
     constexpr int kR = 16 / (kSplit * kSub);  // state rows per thread
     constexpr int kN = 2 * kR;          // S.k and S.q partials per thread
     __shared__ float qs[kD], ks[kD], vs[kD], deltas[kD], ys[kD];
-    __shared__ float gate_g, gate_beta, norm_r;
+    __shared__ float gate_g, gate_beta;
 
     const int C = 2 * Hk * kD + Hv * kD;
     const int bh = blockIdx.x / kSplit;
@@ -340,15 +340,14 @@ __global__ __launch_bounds__(kDecodeThreads * kSub) void decode_kernel(
         if (tid < kRows) store_any(out, size_t(bh) * kD + row0 + tid, y_dtype, ys[row0 + tid]);
         return;
     }
-    if (wg == 0) {
+    // the two output waves each reduce all 128 outputs (the same lanes, the
+    // same order: the same bits), so no barrier hands the root between them
+    if (tid < kD) {
         const float y0 = Act::round(ys[l]), y1 = Act::round(ys[l + 64]);
         const float ss = group_sum<kWave>(y0 * y0 + y1 * y1);
-        if (l == 0) norm_r = 1.f / sqrtf(ss / float(kD) + eps);
-    }
-    __syncthreads();
-    if (tid < kD) {
+        const float nr = 1.f / sqrtf(ss / float(kD) + eps);
         const float yv = Act::round(ys[tid]);
-        const float normed = Act::round(yv * norm_r * nw);
+        const float normed = Act::round(yv * nr * nw);
         Act::store(yo, size_t(bh) * kD + tid, silu(zz) * normed);
     }
 }
