@@ -125,9 +125,10 @@ int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dt
 /*
  * gdn_decode_step - one fused decode token for B sequences: conv + SiLU +
  * conv-state roll, q/k scaling, gates, the recurrence, and optionally the
- * gated RMSNorm. One workgroup per (sequence, value head), or, without the
- * norm and when B * Hv is at most 128, 2-8 workgroups per head that each
- * take a share of its rows (the same arithmetic per row: the same state and
+ * gated RMSNorm. One workgroup per (sequence, value head) (with the norm and
+ * B * Hv at most 256, of 512 threads), or, without the norm, 2-8 workgroups
+ * per head when B * Hv is at most 128 and 2 from B * Hv = 2048, each taking
+ * a share of its rows (the same arithmetic per row: the same state and
  * output bits); the float32 Dv x Dk state tile is read once and written once.
  *   qkv:            (B, C) act_dtype (pre-conv projection output)
  *   conv_state_in:  (B, K-1, C) act_dtype; conv_state_out must not overlap it
@@ -157,7 +158,7 @@ int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dt
  *                   projection output are read in place.
  *   conv_arrivals:  NULL, or (pool) int32 counters, all zero between calls (needs
  *                   conv_half): the step flips conv_half[slots[b]] itself (the
- *                   last of row b's Hv workgroups to finish, counted here, flips
+ *                   last of row b's workgroups to finish, counted here, flips
  *                   it and resets the count), so no gdn_pool_advance follows.
  *   A row whose slot falls outside the pool writes NaN to its output and
  *   touches no state.
