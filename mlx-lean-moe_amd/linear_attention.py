@@ -613,6 +613,20 @@ class DecodeGraph:
         self.x = x_example.detach().clone()
         self.residual = None if residual_example is None else residual_example.detach().clone()
         self._idx = np.asarray(self.slots, dtype=np.int64)
+        # One eager step first, on a throwaway pool of the same shapes, so
+        # that everything the step creates lazily (the vendor BLAS handle and
+        # its kernels, torch's workspaces, the first launch of each kernel)
+        # exists before capture: library set-up under stream capture is not
+        # allowed, and the process can end inside it without a Python error.
+        # The real pool is not touched.
+        n = len(self.slots)
+        warm = RecurrentStatePool(n, pool.conv_buf.shape[1] + 1, pool.conv_buf.shape[2],
+                                  pool.ssm_state.shape[1], pool.ssm_state.shape[2],
+                                  pool.ssm_state.shape[3], dtype=pool.conv_buf.dtype,
+                                  device=self.x.device)
+        layer.decode_batch(self.x, warm, slots=list(range(n)), residual=self.residual)
+        torch.cuda.synchronize(self.x.device)
+        del warm
         # the slot array must exist before capture (no host copy in the
         # graph), and the graph holds it: the pool's cache of slot arrays may
         # drop it later, and a replay must not read freed (reused) memory

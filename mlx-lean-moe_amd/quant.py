@@ -64,8 +64,9 @@ def _dense_rows(rows: int, N: int, K: int) -> bool:
 
 @dataclass(frozen=True)
 class QuantScheme:
-    """One MLX quantization scheme, including its packing mode (the
-    reference's validation: config.py:17-33)."""
+    """Bit width, group size and packing mode of a quantized projection;
+    construction rejects the combinations MLX does not define (the checks
+    of config.py:17-33)."""
 
     bits: int
     group_size: int

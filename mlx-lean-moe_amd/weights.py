@@ -182,7 +182,10 @@ def projection_is_quantized(index: dict[str, TensorSpan], name: str, scheme: Qua
     not shaped like the scales; weight and scales disagreeing in their leading
     (row) dimensions; a packed row width other than the scale groups'
     ``groups * group_size * bits / 32`` words. These are the conditions the
-    reference's loader enforces (expert_loader.py:95-141)."""
+    reference's loader enforces (expert_loader.py:95-141) with one more:
+    that loader only shape-checks biases stored beside float-scheme codes
+    and hands them to the matmul, whose float modes have no bias term; here
+    such a checkpoint is refused when it is read."""
 
     weight = index.get(f"{name}.weight")
     scales = index.get(f"{name}.scales")

@@ -243,8 +243,6 @@ def test_decode_graph_replays_equal_eager_decode(gpu):
     assert graphed.conv_half_dev.cpu().tolist() == graphed.conv_half.tolist()
 
 
-@pytest.mark.skip(reason="its first GPU run ended the test process without a result or "
-                         "a reported GPU fault; kept off the GPU until the cause is found")
 def test_decode_graph_outlives_the_pools_slot_cache(gpu):
     """The pool keeps at most 64 slot arrays and drops them all when a 65th
     set arrives; a captured step holds its own, so after 65 other slot sets
@@ -309,3 +307,50 @@ def test_decode_graph_with_a_residual(gpu):
     torch.testing.assert_close(graphed.ssm_state, eager.ssm_state, rtol=0, atol=0)
     with pytest.raises(ValueError, match="without a residual"):
         gdn.DecodeGraph(layer, graphed, [0], mk()[:1]).step(residual=mk()[:1])
+
+
+_FRESH_PROCESS_GRAPH = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+import mlx_lean_moe_amd as gdn
+from tests.test_gpu_layer import HIDDEN, _build
+from tests.test_gpu_slots import DIMS
+
+dev = torch.device("cuda:0")
+print("fresh process: DecodeGraph before any other GPU work", flush=True)
+layer, _ = _build(9, DIMS, dev, dtype=torch.bfloat16)
+rng = np.random.default_rng(109)
+slots = [2, 0]
+pools = [gdn.RecurrentStatePool(3, 4, DIMS.conv_dim, DIMS.num_value_heads, 128, 128,
+                                dtype=torch.bfloat16, device=dev) for _ in range(2)]
+mk = lambda: torch.tensor(rng.standard_normal((2, HIDDEN)), dtype=torch.bfloat16, device=dev)
+step = gdn.DecodeGraph(layer, pools[1], slots, mk())
+for _ in range(2):
+    x = mk()
+    ref = layer.decode_batch(x, pools[0], slots=slots)
+    assert torch.equal(step.step(x), ref)
+assert torch.equal(pools[1].ssm_state, pools[0].ssm_state)
+assert not pools[0].ssm_state[1].any()
+print("OK", flush=True)
+"""
+
+
+def test_decode_graph_captured_first_in_a_fresh_process(gpu, tmp_path):
+    """A DecodeGraph built before any other GPU work of its process (so
+    that the vendor BLAS is first used by the step being captured) replays
+    equal to eager decode_batch on a twin pool. Run in a child process: the
+    parent's earlier tests have set the libraries up already."""
+
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "fresh_graph.py"
+    script.write_text(_FRESH_PROCESS_GRAPH)
+    proc = subprocess.run([sys.executable, "-u", str(script), root], cwd=root, capture_output=True,
+                          text=True, timeout=240)
+    assert proc.returncode == 0 and proc.stdout.strip().endswith("OK"), (
+        f"child exited {proc.returncode}\nstdout:\n{proc.stdout[-2000:]}\nstderr:\n{proc.stderr[-2000:]}")
