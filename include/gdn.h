@@ -51,7 +51,8 @@ typedef enum {
  * workspace and the decode step's conv_arrivals, 7 the quantized matmul's
  * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride,
  * 10 the gated norm's z layout, 11 gdn_quantized_matmul_noalloc, 12 the
- * prefill's float32 q/k/v, 13 gdn_prefill_fused, 14 gdn_dequantize's mode). */
+ * prefill's float32 q/k/v, 13 gdn_prefill_fused, 14 gdn_dequantize's mode, 15
+ * gdn_quantized_matmul_scheme and its workspace size). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -358,6 +359,34 @@ int64_t gdn_quantized_matmul_workspace_size(int x_dtype, int sb_dtype, int M, in
  */
 int gdn_dequantize(const void *w, const void *scales, const void *biases, int sb_dtype, void *out,
                    int out_dtype, int N, int K, int bits, int group_size, int mode, void *stream);
+
+/*
+ * gdn_quantized_matmul_scheme - y = x W^T (+ residual) at decode sizes for
+ * every scheme gdn_dequantize accepts (w, scales, biases, mode as there),
+ * multiplied straight from the packed codes: the weight is read once at its
+ * packed size and never expanded in memory. x: (M, K) bf16, 16-byte aligned,
+ * M <= 64; y, residual: (M, N) y_dtype (residual may be NULL or equal y, as
+ * in gdn_quantized_matmul). K a multiple of 32 and of group_size. float32
+ * partial sums per 32-k block: affine adds s * sum(x q) + b * sum(x), the
+ * float formats sum x times the exact product of code and scale. Where the
+ * 64-column tiles are too few to fill the GPU, K is split over workgroups
+ * whose float32 partial blocks (workspace, 16-byte aligned, at least
+ * gdn_quantized_matmul_scheme_workspace_size bytes for the full split; a
+ * smaller or NULL one splits less) are added in split order by a second
+ * kernel. Returns GDN_EINVAL for sizes or schemes outside these.
+ * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True,
+ * group_size, bits, mode) at decode sizes (model/moe_block.py:44-55) for the
+ * schemes gdn_quantized_matmul does not take (affine 2, 3, 5, 6 bits and the
+ * float formats).
+ */
+int gdn_quantized_matmul_scheme(const void *x, const void *w, const void *scales, const void *biases,
+                                int sb_dtype, void *y, int y_dtype, const void *residual, int M, int N,
+                                int K, int bits, int group_size, int mode, void *workspace,
+                                int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes gdn_quantized_matmul_scheme splits K with for these sizes
+ * (0: no split). No reference counterpart: MLX's kernels allocate their own. */
+int64_t gdn_quantized_matmul_scheme_workspace_size(int M, int N, int K);
 
 #ifdef __cplusplus
 }

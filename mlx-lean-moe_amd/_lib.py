@@ -16,7 +16,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgdn.so")
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 GDN_F32, GDN_BF16, GDN_F16 = 0, 1, 2
 GDN_EINVAL, GDN_EUNSUPPORTED = -1, -2
@@ -73,6 +73,10 @@ _SIGNATURES = {
                                                      _c_int]),
     "gdn_dequantize": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int,
                                 _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+    "gdn_quantized_matmul_scheme": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
+                                             _c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _c_int, _c_void_p, _c_i64, _c_void_p]),
+    "gdn_quantized_matmul_scheme_workspace_size": (_c_i64, [_c_int, _c_int, _c_int]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -1259,6 +1259,373 @@ __global__ __launch_bounds__(256) void dequantize_scheme_kernel(
     }
 }
 
+// ---- every scheme at decode sizes ---------------------------------------
+//
+// A lane's codes for one "super block" of 32 kU k (kU MFMA k blocks): lane
+// l takes the 8 kU consecutive codes from k_sb + 8 kU (l / 16) of column
+// l % 16 and gives codes 8u .. 8u + 7 to MFMA u; x's A operand takes the
+// same k order (its 8 kU values from the same k, 16 kU contiguous bytes per
+// row), so each MFMA still sums x times W over 32 k. The lane's codes are
+// one run of kLen = 8 kU kBits bits from bit kBits k_lane of the row. Runs
+// of a super block start kLen bits apart, so a run starts kLen g % 32 bits
+// into a word (lane group g); kNW words hold the run at the largest such
+// offset. Runs starting on a word (kAligned) are whole words; the others are
+// shifted into place first (a funnel shift per word). All but the last of
+// the kNW words hold bits of the run; the last may lie past the row for the
+// row's final run, and its index is clamped.
+template <int kBits, int kU>
+struct SchemeRun {
+    static constexpr int kLen = 8 * kU * kBits;
+    static constexpr int kShMax = (kLen % 32) > (2 * kLen % 32)
+                                      ? ((kLen % 32) > (3 * kLen % 32) ? kLen % 32 : 3 * kLen % 32)
+                                      : ((2 * kLen % 32) > (3 * kLen % 32) ? 2 * kLen % 32 : 3 * kLen % 32);
+    static constexpr bool kAligned = kShMax == 0;
+    static constexpr int kNW = (kShMax + kLen + 31) / 32;
+};
+
+// Code c of a lane's run (c a compile-time constant after unrolling).
+template <int kBits>
+GDN_DEV uint32_t run_code(const uint32_t* wd, int c) {
+    const int p = kBits * c, w = p >> 5, s = p & 31;
+    const uint32_t v = s + kBits <= 32 ? wd[w] >> s : __builtin_amdgcn_alignbit(wd[w + 1], wd[w], s);
+    return v & ((1u << kBits) - 1u);
+}
+
+// Codes 8u .. 8u + 7 of a lane's run as the MFMA's bf16 B operand:
+//   affine, 2-6 bits: the bf16 bits 0x4300 | q, i.e. 128 + q (exact; the
+//     host's bias is b - 128 s); 8 bits: q;
+//   mxfp4 / mxfp8: the e2m1 / e4m3 values times the group's scale 2^(e - 127)
+//     (gfx950's scaled conversions, which take the scale's exponent: exact);
+//   nvfp4: e2m1 values times the e4m3 scale of each code's 16-code group
+//     (sc0 for codes 0-15 of the run, sc1 for 16-31), exact in bf16.
+template <int kMode, int kBits>
+GDN_DEV bf16x8 run_fragment(const uint32_t* wd, int u, float sc0, float sc1) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 d;
+    if constexpr (kMode == GDN_QUANT_AFFINE && kBits <= 6) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            d[i] = (run_code<kBits>(wd, 8 * u + 2 * i) | run_code<kBits>(wd, 8 * u + 2 * i + 1) << 16) | 0x43004300u;
+    } else if constexpr (kMode == GDN_QUANT_AFFINE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            d[i] = pack_bf16x2(float(run_code<kBits>(wd, 8 * u + 2 * i)), float(run_code<kBits>(wd, 8 * u + 2 * i + 1)));
+    } else if constexpr (kMode == GDN_QUANT_MXFP4) {
+        // byte i of the word: its low nibble to the low half
+        const uint32_t q = wd[u];
+        d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc0, 0));
+        d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc0, 1));
+        d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc0, 2));
+        d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc0, 3));
+    } else if constexpr (kMode == GDN_QUANT_MXFP8) {
+        // 16-bit half of a word: its low byte to the low half
+        const uint32_t q0 = wd[2 * u], q1 = wd[2 * u + 1];
+        d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q0, sc0, false));
+        d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q0, sc0, true));
+        d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q1, sc0, false));
+        d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q1, sc0, true));
+    } else {
+        const float sc = u < 2 ? sc0 : sc1;
+        const uint32_t q = wd[u];
+        const auto f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, 1.0f, 0);
+        const auto f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, 1.0f, 1);
+        const auto f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, 1.0f, 2);
+        const auto f3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, 1.0f, 3);
+        d[0] = pack_bf16x2(f0[0] * sc, f0[1] * sc);
+        d[1] = pack_bf16x2(f1[0] * sc, f1[1] * sc);
+        d[2] = pack_bf16x2(f2[0] * sc, f2[1] * sc);
+        d[3] = pack_bf16x2(f3[0] * sc, f3[1] * sc);
+    }
+    return __builtin_bit_cast(bf16x8, d);
+}
+
+constexpr int kSchemeWaves = 8;   // waves of a workgroup, dealt the super blocks in turn
+constexpr int kSchemeMaxSplits = 16;
+// groups of a column one split may span: (s, b) float pairs for affine
+// codes, one float for the others; rows of the LDS table are one entry
+// longer (fewer bank conflicts)
+constexpr int kSchemeGroupsAffine = 128;
+constexpr int kSchemeGroupsFloat = 256;
+static_assert((kSchemeGroupsFloat + 1) * 4 <= (kSchemeGroupsAffine + 1) * 8, "LDS share of the scales");
+
+// Output columns of a workgroup: 64 (four MFMA column tiles), or 32 where
+// 64-column tiles would number fewer than 128 (K is then split more finely
+// instead: measured on 2048 x 4096 weights, 32 columns in 4 splits take
+// 7.5-8.8 us at one row and 14-16 us at 64 rows against 8-13 and 19-22 us
+// for 64 columns in 8; on 12352 x 2048, 64 columns take 22 us at 64 rows
+// against 31 us for 32).
+int scheme_cols(int N) { return (N + 63) / 64 < 128 ? 32 : 64; }
+
+// y = x W^T for M <= 64 bf16 rows and the packed codes of any scheme
+// (mx.quantized_matmul at decode sizes, model/moe_block.py:44-55), reading
+// the weight once at its packed size. A workgroup of 8 waves takes kCols
+// columns (16-column MFMA tiles) and the k range of split blockIdx.y
+// (all of K with one split). Its columns' scales (and biases) for the range
+// are first converted to float in LDS; the range's super blocks are then
+// dealt to the waves in turn, each lane loading its run of codes per column
+// tile and its x values per row tile (rows clamped to M - 1, never stored)
+// straight into registers, two super blocks in flight. Per super block and
+// output (m, n), with the run's bf16 values v (run_fragment):
+//   affine:       y += s P + b' X, P = sum x v, X = sum x (a product against
+//                 ones), b' = b - 128 s for 2-6-bit codes: float32 sums
+//                 with scale and bias per super block (within one group),
+//                 as MLX's matrix-vector kernels apply them per group;
+//   mxfp4, mxfp8, nvfp4: y += sum x v, the scale being in v.
+// The 8 waves' float32 blocks are added in LDS in wave order. With S > 1
+// splits the sum goes to partial[split][M][N] (qlinear_split_sum_kernel adds
+// the splits in order), else to y with the residual. The host guarantees:
+// K / 32 / S a multiple of kU, 32 kU <= group_size for affine codes, the
+// split's groups within the LDS share, 16-byte aligned x.
+template <int kMode, int kBits, int kMT, int kU, int kCols>
+__global__ __launch_bounds__(512) void qlinear_scheme_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w, const void* __restrict__ scales,
+    const void* __restrict__ biases, int sb_dtype, void* y, int y_dtype, const void* residual,
+    float* __restrict__ partial, int M, int N, int K, int group_size) {
+    using Run = SchemeRun<kBits, kU>;
+    constexpr bool kAffine = kMode == GDN_QUANT_AFFINE;
+    constexpr int kCT = kCols / 16;
+    constexpr int kSlots = kMT * kCT;  // float4 accumulators per lane
+    constexpr int kRedBytes = kSchemeWaves * kSlots * 64 * 16;
+    constexpr int kSBBytes = kCols * (kSchemeGroupsAffine + 1) * 8;
+    constexpr int kLds = kRedBytes > kSBBytes ? kRedBytes : kSBBytes;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
+    float* sbl = reinterpret_cast<float*>(lds);  // [kCols][G + 1] floats or float pairs
+
+    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, g = l >> 4, n = l & 15;
+    const int n0 = blockIdx.x * kCols;
+    const int64_t row_words = int64_t(K) * kBits / 32;
+    const int gpr = K / group_size;
+    const int kspan = K / gridDim.y, kbase = blockIdx.y * kspan;  // this split's k range
+    const int G = kspan / group_size, gstride = G + 1;            // its groups per column
+
+    // the split's scales (and biases) of the workgroup's columns, as float
+    for (int e = tid; e < kCols * G; e += 512) {
+        const int c = e / G, gi = e - c * G;
+        const int col = n0 + c < N ? n0 + c : N - 1;
+        const int64_t src = int64_t(col) * gpr + kbase / group_size + gi;
+        if constexpr (kAffine) {
+            const float s = load_any(scales, src, sb_dtype), b = load_any(biases, src, sb_dtype);
+            const float b2 = kBits <= 6 ? __builtin_fmaf(-128.f, s, b) : b;
+            *reinterpret_cast<float2*>(sbl + 2 * (c * gstride + gi)) = float2{s, b2};
+        } else {
+            const uint32_t code = static_cast<const uint8_t*>(scales)[src];
+            // mx: the float whose exponent field is the e8m0 code (the
+            // conversions read only the exponent)
+            sbl[c * gstride + gi] = kMode == GDN_QUANT_NVFP4 ? e4m3_value(code) : __uint_as_float(code << 23);
+        }
+    }
+
+    const uint32_t* wrow[kCT];
+#pragma unroll
+    for (int ct = 0; ct < kCT; ++ct) {
+        const int c = n0 + 16 * ct + n < N ? n0 + 16 * ct + n : N - 1;
+        wrow[ct] = w + c * row_words;
+    }
+    const uint16_t* xrow[kMT];
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt) xrow[mt] = x + int64_t(16 * mt + n < M ? 16 * mt + n : M - 1) * K;
+
+    // this split's super blocks; the wave's are wv + 8 i, i < nbw
+    const int nsb = kspan / (32 * kU);
+    const int nbw = nsb > wv ? (nsb - wv + kSchemeWaves - 1) / kSchemeWaves : 0;
+    const int last = nbw > 0 ? wv + kSchemeWaves * (nbw - 1) : 0;
+
+    struct Slot {
+        uint32_t wd[kCT][Run::kNW];
+        u16x8 xv[kMT][kU];
+        int k;  // the lane's first k (from the split's start)
+    };
+    auto load = [&](Slot& sl, int i) {
+        const int sb = wv + kSchemeWaves * i < last ? wv + kSchemeWaves * i : last;
+        const int kl = 32 * kU * sb + 8 * kU * g;
+        sl.k = kl;
+        const int64_t off = int64_t(kBits) * (kbase + kl), wi = off >> 5;
+        const int64_t wl = wi + Run::kNW - 1, wlc = Run::kAligned || wl < row_words ? wl : row_words - 1;
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) {
+#pragma unroll
+            for (int j = 0; j + 1 < Run::kNW; ++j) sl.wd[ct][j] = wrow[ct][wi + j];
+            sl.wd[ct][Run::kNW - 1] = wrow[ct][wlc];
+        }
+#pragma unroll
+        for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+            for (int u = 0; u < kU; ++u) sl.xv[mt][u] = *reinterpret_cast<const u16x8*>(xrow[mt] + kbase + kl + 8 * u);
+    };
+
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[kMT][kCT];
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) acc[mt][ct] = zero;
+    bf16x8 ones;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = static_cast<__bf16>(1.0f);
+
+    auto compute = [&](Slot& sl) {
+        const int sh = int((int64_t(kBits) * (kbase + sl.k)) & 31);
+        const int gl = sl.k / group_size;  // the run's (first) group in the split
+        f32x4 X[kMT];
+        if constexpr (kAffine) {
+#pragma unroll
+            for (int mt = 0; mt < kMT; ++mt) {
+                X[mt] = zero;
+#pragma unroll
+                for (int u = 0; u < kU; ++u) X[mt] = mfma_bf16(__builtin_bit_cast(bf16x8, sl.xv[mt][u]), ones, X[mt]);
+            }
+        }
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) {
+            uint32_t* wd = sl.wd[ct];
+            if constexpr (!Run::kAligned) {
+#pragma unroll
+                for (int j = 0; j + 1 < Run::kNW; ++j) wd[j] = __builtin_amdgcn_alignbit(wd[j + 1], wd[j], sh);
+                wd[Run::kNW - 1] >>= sh;  // the run's bits in the last word
+            }
+            const float* se = sbl + (kAffine ? 2 : 1) * ((16 * ct + n) * gstride + gl);
+            float sc0 = 0.f, sc1 = 0.f, s = 0.f, b = 0.f;
+            if constexpr (kAffine) {
+                const float2 sbv = *reinterpret_cast<const float2*>(se);
+                s = sbv.x;
+                b = sbv.y;
+            } else {
+                sc0 = se[0];
+                if constexpr (kMode == GDN_QUANT_NVFP4) sc1 = kU == 4 ? se[1] : sc0;
+            }
+            bf16x8 bq[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) bq[u] = run_fragment<kMode, kBits>(wd, u, sc0, sc1);
+#pragma unroll
+            for (int mt = 0; mt < kMT; ++mt) {
+                if constexpr (kAffine) {
+                    f32x4 P = zero;
+#pragma unroll
+                    for (int u = 0; u < kU; ++u) P = mfma_bf16(__builtin_bit_cast(bf16x8, sl.xv[mt][u]), bq[u], P);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[mt][ct][i] = __builtin_fmaf(b, X[mt][i], __builtin_fmaf(s, P[i], acc[mt][ct][i]));
+                } else {
+#pragma unroll
+                    for (int u = 0; u < kU; ++u)
+                        acc[mt][ct] = mfma_bf16(__builtin_bit_cast(bf16x8, sl.xv[mt][u]), bq[u], acc[mt][ct]);
+                }
+            }
+        }
+    };
+
+    // two super blocks in flight: block i in slot i % 2; loads past the
+    // wave's last block repeat it (never computed), so every round issues
+    // the same loads
+    Slot ring[2];
+    load(ring[0], 0);
+    load(ring[1], 1);
+    __syncthreads();  // the scales are in LDS
+    for (int i0 = 0; i0 < nbw; i0 += 2) {
+        compute(ring[0]);
+        load(ring[0], i0 + 2);
+        if (i0 + 1 < nbw) compute(ring[1]);
+        load(ring[1], i0 + 3);
+    }
+
+    // the waves' blocks added in wave order; thread t then owns accumulator
+    // slots t, t + 512, ... (slot = (mt kCT + ct) 64 + lane)
+    __syncthreads();  // every wave is done with the scales
+    f32x4* red = reinterpret_cast<f32x4*>(lds);
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) red[(wv * kSlots + mt * kCT + ct) * 64 + l] = acc[mt][ct];
+    __syncthreads();
+    for (int q = tid; q < kSlots * 64; q += 512) {
+        f32x4 v = red[q];
+#pragma unroll
+        for (int ww = 1; ww < kSchemeWaves; ++ww) v += red[ww * kSlots * 64 + q];
+        const int slot = q >> 6, lane = q & 63, mt = slot / kCT, ct = slot % kCT;
+        const int col = n0 + 16 * ct + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * mt + 4 * (lane >> 4) + i;
+            if (row < M && col < N) {
+                const int64_t o = int64_t(row) * N + col;
+                if (partial) partial[int64_t(blockIdx.y) * M * N + o] = v[i];
+                else store_any(y, o, y_dtype, plus_residual(v[i], residual, o, y_dtype));
+            }
+        }
+    }
+}
+
+// Splits of K for `tiles` column tiles and nb 32-k blocks: the largest
+// power of two S <= 16 leaving each split a multiple of 4 blocks and at
+// least kSchemeMinBlocks of them, at most 256 workgroups (one per CU) and
+// S M N floats of workspace.
+constexpr int kSchemeMinBlocks = 16;
+int scheme_splits(int tiles, int nb, int M, int N, int64_t ws_bytes) {
+    int best = 1;
+    for (int sp = 2; sp <= kSchemeMaxSplits; sp *= 2) {
+        if (nb % (4 * sp) != 0 || nb / sp < kSchemeMinBlocks || int64_t(tiles) * sp > kCUs ||
+            int64_t(sp) * M * N * 4 > ws_bytes)
+            break;
+        best = sp;
+    }
+    return best;
+}
+
+template <int kMode, int kBits>
+int launch_scheme(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
+                  void* y, int y_dtype, const void* residual, int M, int N, int K, int group_size,
+                  void* workspace, int64_t ws_bytes, hipStream_t s) {
+    const int cols = scheme_cols(N), tiles = (N + cols - 1) / cols, nb = K / 32;
+    const int splits = scheme_splits(tiles, nb, M, N, workspace ? ws_bytes : 0);
+    const int groups = K / splits / group_size;
+    GDN_REQUIRE(groups <= (kMode == GDN_QUANT_AFFINE ? kSchemeGroupsAffine : kSchemeGroupsFloat),
+                "gdn_quantized_matmul_scheme: %d groups of a column in one split (K too long for the "
+                "workspace given)", groups);
+    float* partial = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    if (partial)
+        GDN_REQUIRE(!overlaps(partial, int64_t(splits) * M * N * 4, y, int64_t(M) * N * dtype_size(y_dtype)) &&
+                        !overlaps(partial, int64_t(splits) * M * N * 4, x, int64_t(M) * K * 2) &&
+                        (!residual || !overlaps(partial, int64_t(splits) * M * N * 4, residual,
+                                                int64_t(M) * N * dtype_size(y_dtype))),
+                    "gdn_quantized_matmul_scheme: workspace overlaps x, y or residual");
+    // super blocks of kU MFMA blocks: up to 4 (2 with 64 rows: registers),
+    // within one group for affine codes, dividing the split's blocks
+    const int per_split = nb / splits;
+    int ku = M > 16 ? 2 : 4;
+    if (kMode == GDN_QUANT_AFFINE) ku = ku < group_size / 32 ? ku : group_size / 32;
+    while (per_split % ku != 0) ku /= 2;
+    const dim3 grid{unsigned(tiles), unsigned(splits)};
+    const auto* xp = static_cast<const uint16_t*>(x);
+#define GDN_SCHEME_C(MT, U, C)                                                                              \
+    hipLaunchKernelGGL((qlinear_scheme_kernel<kMode, kBits, MT, U, C>), grid, dim3(512), 0, s, xp, w, scales, \
+                       biases, sb_dtype, y, y_dtype, residual, partial, M, N, K, group_size)
+#define GDN_SCHEME(MT, U)              \
+    do {                               \
+        if (cols == 32)                \
+            GDN_SCHEME_C(MT, U, 32);   \
+        else                           \
+            GDN_SCHEME_C(MT, U, 64);   \
+    } while (0)
+    if (M <= 16) {
+        if (ku == 4) GDN_SCHEME(1, 4);
+        else if (ku == 2) GDN_SCHEME(1, 2);
+        else GDN_SCHEME(1, 1);
+    } else if constexpr (kMode == GDN_QUANT_AFFINE && kBits == 8) {
+        GDN_SCHEME(4, 1);  // two 8-bit super blocks in flight would spill
+    } else {
+        if (ku == 2) GDN_SCHEME(4, 2);
+        else GDN_SCHEME(4, 1);
+    }
+#undef GDN_SCHEME
+#undef GDN_SCHEME_C
+    if (partial) {
+        const int64_t count = int64_t(M) * N;
+        hipLaunchKernelGGL(qlinear_split_sum_kernel, dim3(unsigned((count + 255) / 256)), dim3(256), 0, s, partial,
+                           splits, count, y, y_dtype, residual);
+    }
+    return check_launch("gdn_quantized_matmul_scheme");
+}
+
 }  // namespace
 }  // namespace gdn
 
@@ -1299,4 +1666,64 @@ extern "C" int gdn_dequantize(const void* w, const void* scales, const void* bia
                        static_cast<const uint32_t*>(w), scales, biases, sb_dtype, out, out_dtype, N, K, bits,
                        group_size, mode);
     return check_launch("gdn_dequantize");
+}
+
+extern "C" int64_t gdn_quantized_matmul_scheme_workspace_size(int M, int N, int K) {
+    if (M <= 0 || M > 64 || N <= 0 || K <= 0 || K % 32 != 0) return 0;
+    const int cols = scheme_cols(N);
+    const int splits = scheme_splits((N + cols - 1) / cols, K / 32, M, N, INT64_MAX);
+    return splits > 1 ? int64_t(splits) * M * N * 4 : 0;
+}
+
+extern "C" int gdn_quantized_matmul_scheme(const void* x, const void* w, const void* scales, const void* biases,
+                                           int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N,
+                                           int K, int bits, int group_size, int mode, void* workspace,
+                                           int64_t workspace_bytes, void* stream) {
+    bool ok;
+    switch (mode) {  // the schemes of the reference's QuantScheme (config.py:17-33)
+        case GDN_QUANT_AFFINE:
+            ok = (bits >= 2 && bits <= 8 && bits != 7) && (group_size == 32 || group_size == 64 || group_size == 128);
+            break;
+        case GDN_QUANT_MXFP4: ok = bits == 4 && group_size == 32; break;
+        case GDN_QUANT_MXFP8: ok = bits == 8 && group_size == 32; break;
+        case GDN_QUANT_NVFP4: ok = bits == 4 && group_size == 16; break;
+        default: ok = false;
+    }
+    GDN_REQUIRE(ok, "gdn_quantized_matmul_scheme: mode %d with bits=%d, group_size=%d is not a scheme", mode,
+                bits, group_size);
+    GDN_REQUIRE(M >= 0 && M <= 64, "gdn_quantized_matmul_scheme: M=%d (1 to 64 rows)", M);
+    GDN_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K % group_size == 0,
+                "gdn_quantized_matmul_scheme: K=%d must be a multiple of 32 and of group_size", K);
+    GDN_REQUIRE(int64_t(N) * K * bits / 8 < (int64_t(1) << 31), "gdn_quantized_matmul_scheme: weight too large");
+    GDN_REQUIRE(valid_dtype(y_dtype), "gdn_quantized_matmul_scheme: bad y dtype");
+    GDN_REQUIRE(mode != GDN_QUANT_AFFINE || valid_dtype(sb_dtype), "gdn_quantized_matmul_scheme: bad scales dtype");
+    if (M == 0) return 0;
+    GDN_REQUIRE(x && w && scales && y && (mode != GDN_QUANT_AFFINE || biases),
+                "gdn_quantized_matmul_scheme: null pointer");
+    GDN_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 == 0,
+                "gdn_quantized_matmul_scheme: x and w must be 16-byte aligned");
+    const int64_t y_bytes = int64_t(M) * N * dtype_size(y_dtype);
+    GDN_REQUIRE(!overlaps(x, int64_t(M) * K * 2, y, y_bytes), "gdn_quantized_matmul_scheme: y overlaps x");
+    GDN_REQUIRE(!residual || residual == y || !overlaps(residual, y_bytes, y, y_bytes),
+                "gdn_quantized_matmul_scheme: residual partially overlaps y");
+    hipStream_t s = as_stream(stream);
+    const auto* wp = static_cast<const uint32_t*>(w);
+    GDN_REQUIRE(!workspace || reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+                "gdn_quantized_matmul_scheme: workspace must be 16-byte aligned");
+#define GDN_ARGS x, wp, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, workspace, workspace_bytes, s
+    switch (mode) {
+        case GDN_QUANT_MXFP4: return launch_scheme<GDN_QUANT_MXFP4, 4>(GDN_ARGS);
+        case GDN_QUANT_MXFP8: return launch_scheme<GDN_QUANT_MXFP8, 8>(GDN_ARGS);
+        case GDN_QUANT_NVFP4: return launch_scheme<GDN_QUANT_NVFP4, 4>(GDN_ARGS);
+        default: break;
+    }
+    switch (bits) {
+        case 2: return launch_scheme<GDN_QUANT_AFFINE, 2>(GDN_ARGS);
+        case 3: return launch_scheme<GDN_QUANT_AFFINE, 3>(GDN_ARGS);
+        case 4: return launch_scheme<GDN_QUANT_AFFINE, 4>(GDN_ARGS);
+        case 5: return launch_scheme<GDN_QUANT_AFFINE, 5>(GDN_ARGS);
+        case 6: return launch_scheme<GDN_QUANT_AFFINE, 6>(GDN_ARGS);
+        default: return launch_scheme<GDN_QUANT_AFFINE, 8>(GDN_ARGS);
+    }
+#undef GDN_ARGS
 }

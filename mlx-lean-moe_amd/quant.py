@@ -111,6 +111,17 @@ def _on_kernels(quant: QuantScheme) -> bool:
     return quant.mode == "affine" and quant.bits in _KERNEL_BITS
 
 
+def _scheme_kernel_takes(x: torch.Tensor, rows: int, K: int, quant: QuantScheme) -> bool:
+    """Whether gdn_quantized_matmul_scheme multiplies a scheme outside
+    ``_on_kernels`` directly from its codes: bf16 ``x`` of at most 64 rows,
+    ``K`` a multiple of 32 and at most 128 affine groups (256 of the float
+    formats) per row, the scales its workgroups hold (decode sizes)."""
+
+    groups = K // quant.group_size
+    return (x.dtype == torch.bfloat16 and rows <= 64 and K % 32 == 0
+            and groups <= (128 if quant.mode == "affine" else 256))
+
+
 def _check_quantized(tensors: dict, quant: QuantScheme, K: int | None):
     w, scales = tensors["weight"], tensors["scales"]
     biases = tensors.get("biases")
@@ -214,13 +225,15 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None,
     w, scales, biases, N, K = _check_quantized(tensors, quant, x.shape[-1])
     if x.device.type != "cuda":
         raise RuntimeError(f"quantized projections run on ROCm devices only; got {x.device}")
-    if not _on_kernels(quant):
-        # the other schemes: their exact weights in x's dtype (bf16 for the
-        # float schemes is exact), then the vendor BLAS
-        wd = dense if dense is not None else dequantize(tensors, quant, x.dtype)
-        return with_residual(x @ wd.to(x.dtype).T)
     lead = x.shape[:-1]
     rows = x.reshape(-1, K).shape[0]
+    if not _on_kernels(quant):
+        if _scheme_kernel_takes(x, rows, K, quant):
+            return _scheme_matmul(x, w, scales, biases, quant, N, K, residual)
+        # above decode sizes: their exact weights in x's dtype (bf16 for
+        # the float schemes is exact), then the vendor BLAS
+        wd = dense if dense is not None else dequantize(tensors, quant, x.dtype)
+        return with_residual(x @ wd.to(x.dtype).T)
     x_f32 = (x.dtype == torch.float32 and rows <= 32
              and decode_kernel_takes(rows, K, quant.bits, quant.group_size, scales.dtype))
     if x.dtype != torch.bfloat16 and not x_f32:
@@ -235,12 +248,7 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None,
         x2 = x2.clone()
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
-    r = None
-    if residual is not None:
-        _check_residual(residual, (*lead, N), x.dtype)
-        if residual.device != x.device:
-            raise ValueError("residual must be on the projection's device")
-        r = _c(residual.reshape(M, N))
+    r = _residual_rows(residual, x, lead, M, N)
     w, scales, biases = _c(w), _c(scales), _c(biases)
     ws_bytes = workspace_bytes(x2.dtype, scales.dtype, M, N, K, quant.bits, quant.group_size)
     # a transient from the caching allocator (graph-capture safe); the split
@@ -250,6 +258,45 @@ def quantized_linear(x: torch.Tensor, tensors, quant: QuantScheme | None = None,
               _lib.ptr(biases), _lib.dtype_code(scales.dtype), _lib.ptr(y),
               _lib.dtype_code(y.dtype), _lib.ptr(r), M, N, K, quant.bits, quant.group_size, _lib.ptr(ws),
               ws_bytes, _lib.stream_ptr(x.device))
+    return y.reshape(*lead, N)
+
+
+def _residual_rows(residual, x: torch.Tensor, lead, M: int, N: int):
+    """The residual as ``(M, N)`` rows for a kernel's fused add (None
+    without one), after checking its shape, dtype and device."""
+
+    if residual is None:
+        return None
+    _check_residual(residual, (*lead, N), x.dtype)
+    if residual.device != x.device:
+        raise ValueError("residual must be on the projection's device")
+    return _c(residual.reshape(M, N))
+
+
+def _scheme_matmul(x, w, scales, biases, quant: QuantScheme, N: int, K: int, residual):
+    """``x @ W.T`` (+ residual) for affine 2/3/5/6-bit, mxfp4, mxfp8 and
+    nvfp4 codes at decode sizes (gdn_quantized_matmul_scheme): the packed
+    codes are multiplied where they lie, with float32 per-group sums, so a
+    call reads the weight at its packed size."""
+
+    lead = x.shape[:-1]
+    x2 = _c(x.reshape(-1, K))
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    r = _residual_rows(residual, x, lead, M, N)
+    w, scales = _c(w), _c(scales)
+    if w.data_ptr() % 16:
+        w = w.clone()
+    affine = quant.mode == "affine"
+    biases = _c(biases) if affine else None
+    ws_bytes = scheme_workspace_bytes(M, N, K)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    _lib.call("gdn_quantized_matmul_scheme", _lib.ptr(x2), _lib.ptr(w), _lib.ptr(scales), _lib.ptr(biases),
+              _lib.dtype_code(scales.dtype) if affine else 0, _lib.ptr(y), _lib.dtype_code(y.dtype),
+              _lib.ptr(r), M, N, K, quant.bits, quant.group_size, _MODES[quant.mode], _lib.ptr(ws), ws_bytes,
+              _lib.stream_ptr(x.device))
     return y.reshape(*lead, N)
 
 
@@ -276,7 +323,8 @@ def quantized_linear_split(x: torch.Tensor, weights: LinearWeights, sizes) -> li
     K = x.shape[-1]
     rows = x.reshape(-1, K).shape[0]
     if (x.dtype == torch.bfloat16 and x.device.type == "cuda"
-            and (_dense_rows(rows, tensors["weight"].shape[0], K) or not _on_kernels(quant))):
+            and (_dense_rows(rows, tensors["weight"].shape[0], K)
+                 or not (_on_kernels(quant) or _scheme_kernel_takes(x, rows, K, quant)))):
         _check_quantized(tensors, quant, K)
         lead = x.shape[:-1]
         x2 = _c(x.reshape(-1, K))
@@ -292,6 +340,13 @@ def _check_residual(residual: torch.Tensor, shape, dtype: torch.dtype) -> None:
     if tuple(residual.shape) != tuple(shape) or residual.dtype != dtype:
         raise ValueError(f"residual must be {tuple(shape)} {dtype}, got {tuple(residual.shape)} "
                          f"{residual.dtype}")
+
+
+@functools.lru_cache(maxsize=256)
+def scheme_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Workspace gdn_quantized_matmul_scheme splits K with (0: none)."""
+
+    return int(_lib.load().gdn_quantized_matmul_scheme_workspace_size(M, N, K))
 
 
 @functools.lru_cache(maxsize=256)

@@ -150,3 +150,36 @@ def test_fused_prefill_workspace_and_argument_checks():
     assert call(qkv=ctypes.c_void_p((1 << 32) + 8)) == _lib.GDN_EINVAL and "aligned" in _err(lib)
     assert call(gs=Hv - 1) == _lib.GDN_EINVAL and "gate_stride" in _err(lib)
     assert call(N=2, T=T + 1) == _lib.GDN_EINVAL and "divisible" in _err(lib)
+
+
+def test_scheme_matmul_argument_checks():
+    """gdn_quantized_matmul_scheme refuses what it does not multiply before
+    anything runs: schemes MLX does not define, more than 64 rows, K that is
+    no multiple of 32 or of the group, misaligned operands; no rows is a
+    no-op."""
+
+    lib = _lib.load()
+    bf = _lib.GDN_BF16
+    p, y = ctypes.c_void_p(1 << 30), ctypes.c_void_p(1 << 31)
+
+    def call(M=1, N=64, K=512, bits=3, gs=64, mode=0, x=p, sb=bf):
+        return lib.gdn_quantized_matmul_scheme(x, p, p, p, sb, y, bf, None, M, N, K, bits, gs, mode, None, 0,
+                                               None)
+
+    for bits, gs, mode in [(7, 64, 0), (3, 16, 0), (4, 16, 1), (8, 16, 2), (4, 32, 3), (4, 32, 9)]:
+        assert call(bits=bits, gs=gs, mode=mode) == _lib.GDN_EINVAL and "scheme" in _err(lib)
+    assert call(M=65) == _lib.GDN_EINVAL and "64 rows" in _err(lib)
+    assert call(K=496, bits=4, gs=16, mode=3) == _lib.GDN_EINVAL and "multiple" in _err(lib)
+    assert call(K=480, gs=64) == _lib.GDN_EINVAL and "multiple" in _err(lib)
+    assert call(x=ctypes.c_void_p((1 << 30) + 8)) == _lib.GDN_EINVAL and "aligned" in _err(lib)
+    assert call(sb=7) == _lib.GDN_EINVAL and "scales dtype" in _err(lib)
+    assert call(M=0) == 0
+    # K is split where the column tiles are few: out_proj (N = 2048: 64
+    # tiles of 32 columns) 4 ways, the stacked input projection (193 tiles
+    # of 64 columns) not at all
+    size = lib.gdn_quantized_matmul_scheme_workspace_size
+    assert size(64, 2048, 4096) == 4 * 64 * 2048 * 4
+    assert size(1, 12352, 2048) == 0
+    assert size(1, 96, 512) == 0               # 16 blocks of 32 k: too few to split
+    assert size(1, 96, 2048) == 4 * 96 * 4     # 64 blocks: 4 splits of 16
+    assert size(65, 2048, 4096) == 0 and size(1, 2048, 4080) == 0

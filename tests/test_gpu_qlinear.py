@@ -10,7 +10,7 @@ import torch
 
 import mlx_lean_moe_amd as gdn
 from mlx_lean_moe_amd import _lib
-from mlx_lean_moe_amd.quant import decode_kernel_takes
+from mlx_lean_moe_amd.quant import decode_kernel_takes, quantized_linear_split
 from oracle import quant_ref as Q
 from oracle import gated_delta_ref as R
 from tests.helpers import assert_bf16_out_close, layer_inputs, layer_params
@@ -357,10 +357,13 @@ def test_dequantize_float_schemes_is_bit_exact(gpu, mode, gs, K):
 @pytest.mark.parametrize("M", [1, 64, 600])
 @pytest.mark.parametrize("scheme", [(3, 64, "affine"), (6, 32, "affine"), (2, 128, "affine"),
                                     (4, 32, "mxfp4"), (8, 32, "mxfp8"), (4, 16, "nvfp4")])
-def test_quantized_linear_every_scheme_matches_oracle(gpu, scheme, M):
-    """The schemes outside the quantized matmul kernels (dequantize, then
-    the vendor BLAS) through quantized_linear, bf16 x, with and without the
-    residual, against x @ W.T in float64."""
+def test_quantized_linear_every_scheme_matches_oracle(gpu, scheme, M, monkeypatch):
+    """The schemes outside gdn_quantized_matmul's kernels through
+    quantized_linear, bf16 x, with and without the residual, against x @ W.T
+    in float64. Up to 64 rows gdn_quantized_matmul_scheme multiplies the
+    packed codes (nothing is dequantized; the exact weights s * q + b, float32
+    sums: within the output's bf16 rounding); above, the weights are
+    dequantized to bf16 for the vendor BLAS."""
 
     bits, gs, mode = scheme
     rng = np.random.default_rng(bits + gs + M)
@@ -368,16 +371,77 @@ def test_quantized_linear_every_scheme_matches_oracle(gpu, scheme, M):
     if mode == "affine":
         words, s, b = _weights(rng, N, K, bits, gs, "bf16")
         W = _dev_weights(gpu, words, s, b, "bf16")
-        w = Q.dequantize(words, s, b, bits, gs, out="bf16")  # the bf16 weights multiplied
+        # the exact weights (decode sizes) or the bf16 ones the BLAS multiplies
+        w = Q.dequantize(words, s, b, bits, gs, out="f32" if M <= 64 else "bf16")
     else:
         W, w = _fp_weights(rng, gpu, N, K, mode, gs)  # exact in bf16
+    calls = []
+    call = _lib.call
+    monkeypatch.setattr(_lib, "call", lambda name, *a: (calls.append(name), call(name, *a))[1])
     x = R.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
     xt = torch.tensor(x, device=gpu).to(torch.bfloat16)
     q = gdn.QuantScheme(bits, gs, mode)
     y = gdn.quantized_linear(xt, gdn.LinearWeights(W, q))
     ref = x.astype(np.float64) @ w.astype(np.float64).T
     assert y.dtype == torch.bfloat16 and y.shape == (M, N)
-    assert np.abs(y.float().cpu().numpy() - ref).max() <= 1e-2 * np.abs(ref).max()
+    err = np.abs(y.float().cpu().numpy() - ref)
+    if M <= 64:
+        assert calls == ["gdn_quantized_matmul_scheme"], calls
+        assert (err <= 2.0 ** -8 * np.abs(ref) + 1e-4 * np.abs(ref).max()).all(), err.max()
+    else:
+        assert "gdn_dequantize" in calls
+        assert err.max() <= 1e-2 * np.abs(ref).max()
     r = torch.randn(M, N, device=gpu).to(torch.bfloat16)
     yr = gdn.quantized_linear(xt, gdn.LinearWeights(W, q), residual=r)
     assert torch.equal(yr, y + r)
+    parts = quantized_linear_split(xt, gdn.LinearWeights(W, q), [40, 56])
+    assert torch.equal(torch.cat(parts, dim=-1), y)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("scheme,N,K", [((5, 32, "affine"), 200, 480), ((3, 128, "affine"), 70, 768),
+                                        ((8, 64, "affine"), 64, 256), ((4, 32, "affine"), 33, 2048),
+                                        ((2, 32, "affine"), 96, 352), ((3, 32, "affine"), 80, 224),
+                                        ((3, 64, "affine"), 65, 2560), ((5, 64, "affine"), 40, 640),
+                                        ((6, 64, "affine"), 48, 192), ((2, 64, "affine"), 17, 4096),
+                                        ((6, 128, "affine"), 64, 1024), ((8, 128, "affine"), 96, 512),
+                                        ((4, 16, "nvfp4"), 130, 288), ((4, 32, "mxfp4"), 64, 1056),
+                                        ((8, 32, "mxfp8"), 129, 320), ((4, 16, "nvfp4"), 24, 4096),
+                                        ((8, 32, "mxfp8"), 2048, 1024)])
+def test_scheme_matmul_shapes_and_outputs(gpu, scheme, N, K, M):
+    """gdn_quantized_matmul_scheme through the C ABI at ragged sizes: every
+    row-tile kernel (1-16 rows, 17-64 rows), each code width with runs of
+    1, 2 and 4 MFMA blocks per lane (group sizes 32, 64, 128: runs starting
+    on a word and runs shifted into place), K split over workgroups (long K,
+    few columns), column counts that leave a block part-empty, and the output
+    in bfloat16, float16 and float32 with the residual aliasing y; against
+    the exact weights in float64 (float32 output: float32 sums)."""
+
+    bits, gs, mode = scheme
+    rng = np.random.default_rng(M * 7 + N + K)
+    if mode == "affine":
+        words, s, b = _weights(rng, N, K, bits, gs, "f16" if bits == 5 else "bf16")
+        W = _dev_weights(gpu, words, s, b, "f16" if bits == 5 else "bf16")
+        w = Q.dequantize(words, s, b, bits, gs, out="f32")
+        sb = _lib.dtype_code(W["scales"].dtype)
+    else:
+        W, w = _fp_weights(rng, gpu, N, K, mode, gs)
+        sb = 0
+    x = R.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    xt = torch.tensor(x, device=gpu).to(torch.bfloat16)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    mode_code = {"affine": 0, "mxfp4": 1, "mxfp8": 2, "nvfp4": 3}[mode]
+    nb = _lib.load().gdn_quantized_matmul_scheme_workspace_size(M, N, K)
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=gpu)
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        if dt == torch.float16 and np.abs(ref).max() > 3e4:
+            continue  # beyond float16's range (the float formats' large scales)
+        r = torch.randn(M, N, device=gpu).to(dt)
+        y = r.clone()
+        _lib.call("gdn_quantized_matmul_scheme", _lib.ptr(xt), _lib.ptr(W["weight"]), _lib.ptr(W["scales"]),
+                  _lib.ptr(W.get("biases")), sb, _lib.ptr(y), _lib.dtype_code(dt), _lib.ptr(y), M, N, K,
+                  bits, gs, mode_code, _lib.ptr(ws), nb, _lib.stream_ptr(gpu))
+        got = (y.double() - r.double()).cpu().numpy()
+        rel = 2.0 ** -20 if dt == torch.float32 else 2.0 ** -7
+        assert (np.abs(got - ref) <= rel * (np.abs(ref) + np.abs(r.double().cpu().numpy()))
+                + 1e-5 * np.abs(ref).max()).all(), (dt, np.abs(got - ref).max())
