@@ -26,13 +26,17 @@ Also measured in the same run (reported under "also"):
   --batch B active sequences, 64 by default)
   layer_prefill: the whole layer over a 4096-token prompt, 4-bit
   projections (--workload layer_prefill: the same alone)
+  qlinear_schemes (alone only): gdn_quantized_matmul_scheme for affine
+  2/3/5/6-bit, mxfp4, mxfp8 and nvfp4 codes on the layer's two projection
+  shapes at one and 64 rows, weights read from HBM
   decode_sizes (alone only): the decode kernel without the gated norm at
   Hk=16, Hv=32 over B = 1 .. 256, and the headline configuration: kernel
   time and fraction of HBM at each size
 
 python bench.py [--steps K] [--warmup W] [--batch B]
                 [--workload decode|decode_b64|decode_b1|decode_slots|decode_sizes|layer_decode|
-                            layer_prefill|prefill|prefill_f32|prefill_varlen|qlinear|copy]
+                            layer_prefill|prefill|prefill_f32|prefill_varlen|qlinear|
+                            qlinear_schemes|copy]
 (--workload decode_large is the default decode workload under its older name.)
 """
 
@@ -562,6 +566,87 @@ class QLinearWorkload:
             raise RuntimeError(f"gdn_quantized_matmul failed with {rc}")
 
 
+class SchemeWorkload:
+    """A decode-size projection of M bf16 rows with the codes of one of the
+    schemes gdn_quantized_matmul_scheme multiplies directly (affine 2-8 bits,
+    mxfp4, mxfp8, nvfp4): random codes; affine scales and biases as in
+    QLinearWorkload, e8m0 scale codes for 2^-10 .. 2^-4 (mx formats), e4m3
+    scale codes (nvfp4). The weights cycle through over 320 MB of copies, so
+    every launch reads them from HBM."""
+
+    MODES = {"affine": 0, "mxfp4": 1, "mxfp8": 2, "nvfp4": 3}
+
+    def __init__(self, dev, M, N, K, bits, group_size, mode, seed=0):
+        from mlx_lean_moe_amd import _lib
+
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        affine = mode == "affine"
+        groups = N * (K // group_size)
+        wbytes = N * K * bits // 8 + (4 * groups if affine else groups)
+        self.copies = -(-320_000_000 // wbytes)
+        self.weights = []
+        for _ in range(self.copies):
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K * bits // 32), generator=g,
+                              device=dev, dtype=torch.int32)
+            if affine:
+                sc = (torch.rand(N, K // group_size, generator=g, device=dev) * 0.009
+                      + 0.001).to(torch.bfloat16)
+                bi = ((torch.rand(N, K // group_size, generator=g, device=dev) - 0.5)
+                      * 0.1).to(torch.bfloat16)
+            else:
+                lo, hi = (0x20, 0x40) if mode == "nvfp4" else (117, 124)
+                sc = torch.randint(lo, hi, (N, K // group_size), generator=g, device=dev,
+                                   dtype=torch.uint8)
+                bi = None
+            self.weights.append((w, sc, bi))
+        self.y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        self.bytes = wbytes + M * K * 2 + M * N * 2
+        self.weight_bytes = wbytes
+        lib = _lib.load()
+        self._fn = lib.gdn_quantized_matmul_scheme
+        ws_bytes = int(lib.gdn_quantized_matmul_scheme_workspace_size(M, N, K))
+        self.ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        stream = torch.cuda.current_stream().cuda_stream
+        self._args = [(self.x.data_ptr(), w.data_ptr(), sc.data_ptr(),
+                       None if bi is None else bi.data_ptr(), _lib.GDN_BF16 if affine else 0,
+                       self.y.data_ptr(), _lib.GDN_BF16, None, M, N, K, bits, group_size,
+                       self.MODES[mode], self.ws.data_ptr(), ws_bytes, stream)
+                      for w, sc, bi in self.weights]
+
+    def step(self, s):
+        rc = self._fn(*self._args[s % self.copies])
+        if rc != 0:
+            raise RuntimeError(f"gdn_quantized_matmul_scheme failed with {rc}")
+
+
+# the layer's stacked input projection and out_proj, each scheme at one and
+# 64 rows
+SCHEME_CASES = [(bits, gs, mode) for bits, gs, mode in
+                [(3, 64, "affine"), (5, 64, "affine"), (6, 64, "affine"), (2, 64, "affine"),
+                 (4, 32, "mxfp4"), (8, 32, "mxfp8"), (4, 16, "nvfp4")]]
+SCHEME_SHAPES = [(12352, 2048), (2048, 4096)]
+
+
+def bench_schemes(dev, steps, warmup):
+    out = []
+    for N, K in SCHEME_SHAPES:
+        for bits, gs, mode in SCHEME_CASES:
+            for M in (1, 64):
+                w = SchemeWorkload(dev, M, N, K, bits, gs, mode)
+                total_ms, isolated_ms = time_steps(w.step, steps, warmup)
+                us = total_ms / steps * 1e3
+                out.append({"N": N, "K": K, "M": M, "scheme": f"{mode} {bits}-bit group {gs}",
+                            "call_us": us, "isolated_call_us": isolated_ms * 1e3,
+                            "weight_bytes": w.weight_bytes, "bytes_per_call": w.bytes,
+                            "hbm_gbs": w.bytes / us / 1e3,
+                            "hbm_frac": w.bytes / us / 1e3 / HBM_PEAK_GBS})
+                print(f"# N={N} K={K} M={M} {mode} {bits}/{gs}: {us:.2f} us", file=sys.stderr,
+                      flush=True)
+                del w
+    return out
+
+
 def bench_qlinear(dev, M, steps, warmup, rotate=True, layer_path=False):
     w = QLinearWorkload(dev, M, rotate=rotate)
     total_ms, isolated_ms = time_steps(w.step, steps, warmup)
@@ -892,7 +977,7 @@ def main(argv=None):
                     choices=["decode", "decode_large", "decode_b64", "decode_b1", "decode_slots", "decode_sizes",
                              "layer_decode",
                              "layer_prefill", "prefill_f32",
-                             "prefill", "prefill_varlen", "qlinear", "copy"])
+                             "prefill", "prefill_varlen", "qlinear", "qlinear_schemes", "copy"])
     ap.add_argument("--layers", type=int, default=1,
                     help="layer_decode: also time this many layers chained in one graph")
     ap.add_argument("--batch", type=int, default=64,
@@ -1048,6 +1133,24 @@ def main(argv=None):
                 "flops_per_launch": pre["flops_per_launch"],
                 "layer_path_us": pre["layer_path_us"],
                 "layer_path_mfma_frac": pre["layer_path_tflops"] / BF16_PEAK_TFLOPS}}}))
+        return 0
+
+    if args.workload == "qlinear_schemes":
+        cases = bench_schemes(dev, args.steps, args.warmup)
+        head = cases[0 if cases[0]["M"] == 64 else 1]
+        print(json.dumps({
+            "metric": "decode-size quantized projections of every scheme (no dequantization)",
+            "value": 64 / (head["call_us"] * 1e-6), "unit": "tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["call_us"] * 1e-3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic",
+            "config": {"workload": "gdn_quantized_matmul_scheme at N=12352 K=2048 and N=2048 "
+                                   "K=4096, M=1 and 64; value: M=64 N=12352 " + head["scheme"]},
+            "roofline": {"bound": "hbm", "achieved": head["hbm_gbs"], "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": head["hbm_frac"], "traffic": None,
+                         "kernel": "gdn_quantized_matmul_scheme", "kernel_us": head["call_us"],
+                         "algorithmic_bytes_per_launch": head["bytes_per_call"]},
+            "cases": cases}))
         return 0
 
     if args.workload in ("prefill", "prefill_varlen", "prefill_f32"):

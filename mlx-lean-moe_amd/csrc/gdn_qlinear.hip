@@ -1398,22 +1398,64 @@ __global__ __launch_bounds__(512) void qlinear_scheme_kernel(
     const int kspan = K / gridDim.y, kbase = blockIdx.y * kspan;  // this split's k range
     const int G = kspan / group_size, gstride = G + 1;            // its groups per column
 
-    // the split's scales (and biases) of the workgroup's columns, as float
-    for (int e = tid; e < kCols * G; e += 512) {
-        const int c = e / G, gi = e - c * G;
+    // the split's scales (and biases) of the workgroup's columns, as float:
+    // 512 / kCols threads per column take its groups in turn, requesting 8
+    // entries at a time (one memory latency per 8, not per entry); the
+    // scales' dtype is resolved outside the loop
+    auto stage_scales = [&]() {
+        constexpr int kTPC = 512 / kCols, kB = 8;
+        const int c = tid / kTPC, j0 = tid % kTPC;
         const int col = n0 + c < N ? n0 + c : N - 1;
-        const int64_t src = int64_t(col) * gpr + kbase / group_size + gi;
+        const int64_t src0 = int64_t(col) * gpr + kbase / group_size;
+        float* row = sbl + (kAffine ? 2 : 1) * c * gstride;
+        auto stage = [&](auto to_float) {
+            for (int g0 = j0; g0 < G; g0 += kTPC * kB) {
+                decltype(to_float(0)) sv[kB], bv[kB];
+#pragma unroll
+                for (int j = 0; j < kB; ++j) {
+                    const int gi = g0 + kTPC * j;
+                    if (gi < G) {
+                        sv[j] = to_float(src0 + gi);
+                        if constexpr (kAffine) bv[j] = to_float(~(src0 + gi));
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < kB; ++j) {
+                    const int gi = g0 + kTPC * j;
+                    if (gi < G) {
+                        if constexpr (kAffine) {
+                            const float sf = float(sv[j]), bf = float(bv[j]);
+                            const float b2 = kBits <= 6 ? __builtin_fmaf(-128.f, sf, bf) : bf;
+                            *reinterpret_cast<float2*>(row + 2 * gi) = float2{sf, b2};
+                        } else {
+                            row[gi] = float(sv[j]);
+                        }
+                    }
+                }
+            }
+        };
+        // entry i of the scales, or of the biases when passed ~i
         if constexpr (kAffine) {
-            const float s = load_any(scales, src, sb_dtype), b = load_any(biases, src, sb_dtype);
-            const float b2 = kBits <= 6 ? __builtin_fmaf(-128.f, s, b) : b;
-            *reinterpret_cast<float2*>(sbl + 2 * (c * gstride + gi)) = float2{s, b2};
+            const auto* s32 = static_cast<const float*>(scales);
+            const auto* b32 = static_cast<const float*>(biases);
+            const auto* s16 = static_cast<const uint16_t*>(scales);
+            const auto* b16 = static_cast<const uint16_t*>(biases);
+            if (sb_dtype == GDN_F32)
+                stage([&](int64_t i) { return i >= 0 ? s32[i] : b32[~i]; });
+            else if (sb_dtype == GDN_BF16)
+                stage([&](int64_t i) { return bf16_bits_to_f32(i >= 0 ? s16[i] : b16[~i]); });
+            else
+                stage([&](int64_t i) { return f16_bits_to_f32(i >= 0 ? s16[i] : b16[~i]); });
         } else {
-            const uint32_t code = static_cast<const uint8_t*>(scales)[src];
             // mx: the float whose exponent field is the e8m0 code (the
             // conversions read only the exponent)
-            sbl[c * gstride + gi] = kMode == GDN_QUANT_NVFP4 ? e4m3_value(code) : __uint_as_float(code << 23);
+            const auto* s8 = static_cast<const uint8_t*>(scales);
+            stage([&](int64_t i) {
+                const uint32_t code = s8[i];
+                return kMode == GDN_QUANT_NVFP4 ? e4m3_value(code) : __uint_as_float(code << 23);
+            });
         }
-    }
+    };
 
     const uint32_t* wrow[kCT];
 #pragma unroll
@@ -1517,9 +1559,12 @@ __global__ __launch_bounds__(512) void qlinear_scheme_kernel(
     // two super blocks in flight: block i in slot i % 2; loads past the
     // wave's last block repeat it (never computed), so every round issues
     // the same loads
+    // the first two super blocks' operands are requested before the scales,
+    // so that one memory latency covers both
     Slot ring[2];
     load(ring[0], 0);
     load(ring[1], 1);
+    stage_scales();
     __syncthreads();  // the scales are in LDS
     for (int i0 = 0; i0 < nbw; i0 += 2) {
         compute(ring[0]);
