@@ -1556,22 +1556,30 @@ __global__ __launch_bounds__(512) void qlinear_scheme_kernel(
         }
     };
 
-    // two super blocks in flight: block i in slot i % 2; loads past the
-    // wave's last block repeat it (never computed), so every round issues
-    // the same loads
-    // the first two super blocks' operands are requested before the scales,
-    // so that one memory latency covers both
+    // Two super blocks in flight: block i in slot i % 2. The first two
+    // blocks' operands are requested before the scales, so that one memory
+    // latency covers both. Requests carry no condition (a slot's registers
+    // are then free between its compute and its next load) and never
+    // re-request a block read earlier (that can miss L2 again): past the
+    // wave's last block, load's clamp gives the last block, which the other
+    // slot requested just before, so the two misses meet in L2.
     Slot ring[2];
     load(ring[0], 0);
     load(ring[1], 1);
     stage_scales();
     __syncthreads();  // the scales are in LDS
-    for (int i0 = 0; i0 < nbw; i0 += 2) {
+    int i0 = 0;
+    for (; i0 + 2 < nbw; i0 += 2) {
+        // the fences keep each load after the compute that frees its slot
         compute(ring[0]);
+        __builtin_amdgcn_sched_barrier(0);
         load(ring[0], i0 + 2);
-        if (i0 + 1 < nbw) compute(ring[1]);
+        compute(ring[1]);
+        __builtin_amdgcn_sched_barrier(0);
         load(ring[1], i0 + 3);
     }
+    if (i0 < nbw) compute(ring[0]);
+    if (i0 + 1 < nbw) compute(ring[1]);
 
     // the waves' blocks added in wave order; thread t then owns accumulator
     // slots t, t + 512, ... (slot = (mt kCT + ct) 64 + lane)

@@ -445,3 +445,50 @@ def test_scheme_matmul_shapes_and_outputs(gpu, scheme, N, K, M):
         rel = 2.0 ** -20 if dt == torch.float32 else 2.0 ** -7
         assert (np.abs(got - ref) <= rel * (np.abs(ref) + np.abs(r.double().cpu().numpy()))
                 + 1e-5 * np.abs(ref).max()).all(), (dt, np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("mode,gs,M", [("mxfp4", 32, 1), ("mxfp4", 32, 40), ("mxfp8", 32, 1), ("nvfp4", 16, 64)])
+def test_scheme_matmul_special_scale_codes(gpu, mode, gs, M):
+    """Scale codes at the ends of their formats through
+    gdn_quantized_matmul_scheme: e8m0 255 (NaN) and e4m3 0x7F (NaN) make
+    their column NaN, as x times a NaN weight does in the oracle; e8m0 0
+    (2^-127) and 1 (2^-126) give their groups weights of at most 6 * 2^-126
+    or 448 * 2^-126, whose products vanish beside the other groups'; mxfp8's
+    NaN weight codes (0x7F, 0xFF) make their column NaN."""
+
+    rng = np.random.default_rng(17 + M)
+    N, K = 64, 256
+    bits = 8 if mode == "mxfp8" else 4
+    q = rng.integers(0, 2 ** bits, (N, K))
+    if mode == "mxfp8":
+        q[(q & 0x7F) == 0x7F] = 0x7E
+        q[9, 100] = 0x7F
+        q[10, 3] = 0xFF
+    if mode == "nvfp4":
+        scales = rng.integers(0x20, 0x40, (N, K // gs))
+        scales[3, 2], scales[4, 0] = 0x7F, 0xFF  # NaN
+        scales[5, 1], scales[6, 7] = 0x00, 0x01  # zero, the smallest subnormal
+    else:
+        scales = rng.integers(120, 130, (N, K // gs))
+        scales[3, 2] = 255  # NaN
+        scales[5, 1], scales[6, 7] = 0, 1
+    scales = scales.astype(np.uint8)
+    words = Q.pack(q, bits)
+    w = Q.dequantize_fp(words, scales, mode, gs)
+    x = R.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = x.astype(np.float64) @ w.T
+    xt = torch.tensor(x, device=gpu).to(torch.bfloat16)
+    y = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    wt = torch.tensor(words.view(np.int32), device=gpu)
+    st = torch.tensor(scales, device=gpu)
+    mode_code = {"mxfp4": 1, "mxfp8": 2, "nvfp4": 3}[mode]
+    _lib.call("gdn_quantized_matmul_scheme", _lib.ptr(xt), _lib.ptr(wt), _lib.ptr(st), None, 0, _lib.ptr(y),
+              _lib.GDN_F32, None, M, N, K, bits, gs, mode_code, None, 0, _lib.stream_ptr(gpu))
+    got = y.cpu().numpy()
+    nan_cols = np.isnan(ref).any(axis=0)
+    assert nan_cols.sum() >= (3 if mode == "mxfp8" else 1)
+    assert np.isnan(got[:, nan_cols]).all()
+    ok = ~nan_cols
+    err = np.abs(got[:, ok] - ref[:, ok])
+    assert (err <= 2.0 ** -20 * np.abs(ref[:, ok]) + 1e-5 * np.abs(ref[:, ok]).max()).all(), err.max()
