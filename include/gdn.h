@@ -312,7 +312,9 @@ int gdn_quantized_matmul(const void *x, int x_dtype, const void *w, const void *
  * needs at most that), so it splits exactly as gdn_quantized_matmul does
  * with a full workspace and gives the same bits. A call needing more
  * returns GDN_EINVAL. The first call on a GPU looks up that GPU's copy of
- * the array (hipGetSymbolAddress); no call allocates or frees memory. Calls
+ * the array (hipGetSymbolAddress, which may load the library's code object
+ * there): make that first call eagerly, before capturing calls into a HIP
+ * graph on that GPU. No call allocates or frees memory. Calls
  * that overlap on one GPU share its scratch and race: the caller orders
  * them (one stream, or events). Arguments and results as
  * gdn_quantized_matmul without workspace and workspace_bytes.

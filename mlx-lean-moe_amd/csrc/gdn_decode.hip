@@ -44,6 +44,7 @@
 // half): twice the loads in flight per CU, one front-end, the head's outputs
 // together in LDS for the norm.
 #include "gdn_common.h"
+#include "gdn_conv.h"
 #include "gdn_host.h"
 
 namespace gdn {
@@ -155,14 +156,15 @@ GDN_DEV ConvTaps load_taps(const typename Act::storage* __restrict__ x,
 }
 
 // conv (cross-correlation, last tap on the current token) + SiLU, with the
-// weights and the result held in the activation dtype.
+// weights and the result held in the activation dtype: the prefill's conv
+// chain (conv_chain: the same bits), and SiLU from libm's expf and an IEEE
+// divide (within about two float ulps; the prefill's silu_hw, within about
+// twenty, can round a value near a bf16 boundary the other way).
 template <class Act>
 GDN_DEV float conv_silu(const ConvTaps& t) {
-    float acc = Act::round(t.w.x) * t.x0;
-    acc += Act::round(t.w.y) * t.x1;
-    acc += Act::round(t.w.z) * t.x2;
-    acc += Act::round(t.w.w) * t.x3;
-    acc = Act::round(acc);
+    const float w[4] = {Act::round(t.w.x), Act::round(t.w.y), Act::round(t.w.z), Act::round(t.w.w)};
+    const float x[4] = {t.x0, t.x1, t.x2, t.x3};
+    const float acc = Act::round(conv_chain(4, [&](int j) { return float2{w[j], x[j]}; }));
     return Act::round(silu(acc));
 }
 
@@ -273,12 +275,14 @@ __global__ __launch_bounds__(kDecodeThreads * kSub) void decode_kernel(
     if (wg < 2) {
         // rms_norm(x, 1e-6) rounded once from its exact value: the sum of
         // squares (exact in double for activation-dtype inputs), the
-        // reciprocal root and the products in double; then the scale, whose
-        // product with a 16-bit value is exact in float32
+        // reciprocal root and the products in double (rms_rr); then the
+        // scale, whose product with a 16-bit value is exact in float32. The
+        // state's 1e-3 bound over chained steps needs q and k as the oracle
+        // rounds them; the prefill's float32 rms_norm8 is within one bf16
+        // ulp of these values
         float* arr = wg == 0 ? qs : ks;
         const float x0 = arr[l], x1 = arr[l + 64];
-        const double ss = group_sum<kWave>(double(x0) * x0 + double(x1) * x1);
-        const double rr = rsqrt(ss / kD + 1e-6);
+        const double rr = rms_rr(group_sum<kWave>(double(x0) * x0 + double(x1) * x1), kD);
         const float inv = 1.f / sqrtf(float(kD));
         const float sc = Act::round(wg == 0 ? inv * inv : inv);
         arr[l] = Act::round(sc * round_once(x0 * rr, Act::code));

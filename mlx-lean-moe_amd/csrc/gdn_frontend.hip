@@ -64,33 +64,50 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_kernel(
     const int run = cu ? find_run(cu, N, t) : int(t / L_uniform);
     const int64_t start = cu ? cu[run] : run * L_uniform;
     const int64_t pos = t - start;  // position inside the run
+    // the conv and SiLU of each channel, with the tiled kernel's instruction
+    // sequence (conv_chain, silu_act; for float32 that is the decode step's)
     for (int c = tid; c < C; c += kFrontThreads) {
-        float acc = 0.f;
-        for (int j = 0; j < K; ++j) {
+        float acc[1] = {Act::round(conv_chain(K, [&](int j) {
             const int64_t idx = pos + j;  // index into concat(state, run tokens)
             const float x = idx < S
                 ? Act::round(load_any(cs_in, (int64_t(run) * S + idx) * C + c, conv_dtype))
                 : Act::load(qkv, (start + idx - S) * qs + c);
-            acc += Act::round(w[int64_t(c) * K + j]) * x;
-        }
-        acc = Act::round(acc);
-        conv_out[c] = Act::round(silu(acc));
+            return float2{Act::round(w[int64_t(c) * K + j]), x};
+        }))};
+        silu_act<Act::code>(acc);
+        conv_out[c] = Act::round(acc[0]);
     }
     __syncthreads();
 
+    // the q/k scaling: 128-wide bf16 heads with the tiled kernels' rms_norm8
+    // (lane l takes channels 8 (l % 16) .. + 7, the wave's four DPP rows the
+    // same head, the first storing it); others in double, each value rounded
+    // once (rms_rr), as the decode step scales them
     const int wave = tid / kWave, lane = tid % kWave;
     const float inv = 1.f / sqrtf(float(Dk));
     const float scale_q = Act::round(inv * inv), scale_k = Act::round(inv);
     for (int head = wave; head < 2 * Hk; head += kFrontThreads / kWave) {
         const float* src = conv_out + head * Dk;
-        float ss = 0.f;
-        for (int e = lane; e < Dk; e += kWave) ss += src[e] * src[e];
-        ss = group_sum<kWave>(ss);
-        const float r = 1.f / sqrtf(ss / float(Dk) + 1e-6f);
         const bool is_q = head < Hk;
         const float sc = is_q ? scale_q : scale_k;
         typename Act::storage* dst = is_q ? qo + (t * Hk + head) * Dk : ko + (t * Hk + head - Hk) * Dk;
-        for (int e = lane; e < Dk; e += kWave) Act::store(dst, e, sc * Act::round(src[e] * r));
+        if (Act::code == GDN_BF16 && Dk == 128) {
+            const int c8 = 8 * (lane & 15);
+            float o[8], n[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = src[c8 + e];
+            rms_norm8(o, n);
+            if (lane < 16) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) Act::store(dst, c8 + e, sc * n[e]);
+            }
+        } else {
+            double ss = 0.0;
+            for (int e = lane; e < Dk; e += kWave) ss = fma(double(src[e]), double(src[e]), ss);
+            const double rr = rms_rr(group_sum<kWave>(ss), Dk);
+            for (int e = lane; e < Dk; e += kWave)
+                Act::store(dst, e, sc * round_once(double(src[e]) * rr, Act::code));
+        }
     }
     const float* vsrc = conv_out + 2 * Hk * Dk;
     for (int e = tid; e < Hv * Dv; e += kFrontThreads) Act::store(vo, t * Hv * Dv + e, vsrc[e]);

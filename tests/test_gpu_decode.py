@@ -170,6 +170,57 @@ def _frontend_vs_oracle(gpu, dims, qkv, conv, w, cu, conv_dev_dtype, pass_cu=Tru
         assert_within_bf16_ulps(v[s0:s1].float().cpu().numpy(), out[:, 2 * qkd:].reshape(-1, Hv, 128), 2)
 
 
+def test_frontend_every_bf16_value_silu_and_qk_scaling(gpu):
+    """Every finite bf16 value through the tiled front-end: conv weights
+    (0, 0, 0, 1) make the conv the identity, so the 4096 v channels of 16
+    tokens carry all 65 280 finite bf16 values, and the q and k channels the
+    same values again. SiLU (the float32 sequence every kernel shares) is
+    within one bf16 ulp of silu(x) in float64 rounded once, equal in all but
+    a few near a rounding boundary — except below about -88.7, where e^-x
+    overflows float32 and the result is -0 for exact values under 2e-37 in
+    magnitude. The q/k scaling of those SiLU values (the kernel's own v;
+    rms_norm8, which the decode step shares) is within one bf16 ulp of the
+    exact value rounded once for every row inside float32's range, and
+    equal to it for all but a few of the rows its eps does not dominate."""
+
+    dims = DIMS_PROD
+    vals = (np.arange(1 << 16, dtype=np.uint32) << 16).view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    per_tok = dims.num_value_heads * 128
+    T = -(-vals.size // per_tok)
+    vv = np.zeros(T * per_tok, np.float32)
+    vv[:vals.size] = vals
+    vv = vv.reshape(T, per_tok)
+    qkv = np.concatenate([vv, vv], axis=1)  # q | k (2 x 2048) and v (4096) the same values
+    w = np.zeros((dims.conv_dim, 4), np.float32)
+    w[:, 3] = 1.0
+    conv = np.zeros((1, 3, dims.conv_dim), np.float32)
+    q, k, v, _ = gdn.conv_frontend(_t(qkv, gpu, torch.bfloat16), _t(conv, gpu, torch.bfloat16), _t(w, gpu),
+                                   dims)
+    got_v = v.float().cpu().numpy().reshape(T, per_tok)
+    exact = R.bf16_round(R.silu(vv.astype(np.float64)))
+    tiny = (vv < -88.7) & (np.abs(exact) < 2e-37)
+    assert (got_v[tiny] == 0).all()
+    assert_within_bf16_ulps(got_v[~tiny], exact[~tiny], 1)
+    assert (got_v[~tiny] != exact[~tiny]).sum() <= 16, int((got_v[~tiny] != exact[~tiny]).sum())
+    half = dims.num_key_heads * 128
+    pre_q = got_v[:, :half].reshape(T, -1, 128).astype(np.float64)
+    pre_k = got_v[:, half:].reshape(T, -1, 128).astype(np.float64)
+    with np.errstate(over="ignore"):
+        qe, ke = R.qk_scale(pre_q, pre_k, "bf16")
+    checked = 0
+    for got, ref, pre in ((q, qe, pre_q), (k, ke, pre_k)):
+        got = got.float().cpu().numpy()
+        amax = np.abs(pre).max(axis=-1, keepdims=True)
+        ms = (pre * pre).mean(axis=-1, keepdims=True)
+        in_range = np.broadcast_to((amax < 1e18) & ((amax > 1e-18) | (amax == 0)), got.shape)
+        assert_within_bf16_ulps(got[in_range], ref[in_range], 1)
+        norm_rows = np.broadcast_to((amax < 1e18) & (ms > 1e-6 * 2.0 ** -20), got.shape)
+        checked += int(norm_rows.sum())
+        assert (got[norm_rows] != ref[norm_rows]).mean() < 1e-3
+    assert checked > 10_000
+
+
 @pytest.mark.parametrize("Hk,Hv", [(16, 32), (3, 6), (1, 1)])
 def test_frontend_production_heads_ragged_runs_match_oracle(gpu, Hk, Hv):
     """The tiled front-end (128-wide heads, 4 taps, bf16): runs that are

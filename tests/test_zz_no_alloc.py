@@ -95,3 +95,41 @@ def test_noalloc_matches_the_workspace_entry_point_on_two_calls(gpu):
     rc = lib.gdn_quantized_matmul_noalloc(None, _lib.GDN_BF16, None, None, None, _lib.GDN_BF16, None,
                                           _lib.GDN_BF16, None, 4, 64, 64, 4, 64, None)
     assert rc == _lib.GDN_EINVAL
+
+
+@pytest.mark.gpu
+def test_noalloc_captured_in_a_graph_replays_the_workspace_entry_points_bits(gpu):
+    """A noalloc call captured in a HIP graph (torch.cuda.graph), after one
+    eager call on the device (the first call looks up the scratch's address,
+    which is not a call to make inside a capture): three replays, each after
+    eager work that leaves other partial blocks in the scratch, give
+    gdn_quantized_matmul's bits with a full workspace, on the out_proj shape
+    at 64 rows (8 splits, the whole scratch) with a residual."""
+
+    lib = _lib.load()
+    M, N, K, bits, gs = 64, 2048, 4096, 4, 64
+    x, words, scales, biases, residual = _case(gpu, M, N, K, bits, gs, seed=77)
+    need = lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, M, N, K, bits, gs)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    ref = _run(lib, "gdn_quantized_matmul", gpu, x, words, scales, biases, residual, M, N, K, bits, gs, ws)
+    # the eager call that sets the device up, outside any capture
+    first = _run(lib, "gdn_quantized_matmul_noalloc", gpu, x, words, scales, biases, residual, M, N, K,
+                 bits, gs)
+    torch.cuda.synchronize()
+    assert torch.equal(first, ref)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.gdn_quantized_matmul_noalloc(
+            x.data_ptr(), _lib.GDN_BF16, words.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+            _lib.GDN_BF16, y.data_ptr(), _lib.GDN_BF16, residual.data_ptr(), M, N, K, bits, gs,
+            torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.gdn_last_error().decode()
+    other = _case(gpu, 16, 1024, 2048, 4, 64, seed=78)
+    for i in range(3):
+        print(f"noalloc graph replay {i}", flush=True)
+        y.fill_(float("nan"))
+        _run(lib, "gdn_quantized_matmul_noalloc", gpu, *other[:4], None, 16, 1024, 2048, 4, 64)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), i
