@@ -503,6 +503,11 @@ class PrefillWorkload:
         nbytes = gated_delta.prefill_workspace_bytes(N, T, Hk, Hv, d, d)
         self.ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         self.T, self.flops = T, prefill_flops(T, Hv)
+        # algorithmic HBM bytes of one call: q, k, v, a, b (and the initial
+        # states) read once, y and the final states written once
+        es = torch.finfo(dtype).bits // 8
+        self.bytes = (T * (2 * Hk * d + Hv * d + 2 * Hv) * es + T * Hv * d * 2
+                      + N * Hv * d * d * 4 * (1 if self.state_in is None else 2))
         from mlx_lean_moe_amd import _lib
 
         self._fn = _lib.load().gdn_prefill_chunked
@@ -685,6 +690,7 @@ def bench_prefill(dev, N, L, Hk, Hv, steps, warmup, lens=None, dtype=torch.bfloa
         "call_us": call_ms * 1e3,
         "isolated_call_us": isolated_ms * 1e3,
         "flops_per_call": w.flops,
+        "bytes_per_call": w.bytes,
         "tflops": tflops,
         "mfma_frac": tflops / BF16_PEAK_TFLOPS,
     }
@@ -900,6 +906,8 @@ def decode_roofline(r, small):
 
 
 def prefill_roofline(r):
+    intensity = r["flops_per_call"] / r["bytes_per_call"]
+    attainable = min(BF16_PEAK_TFLOPS, intensity * HBM_PEAK_GBS / 1e3)
     return {
         "bound": "mfma",
         "achieved": r["tflops"],
@@ -911,6 +919,12 @@ def prefill_roofline(r):
         "kernel_us": r["call_us"],
         "isolated_launch_us": r["isolated_call_us"],
         "algorithmic_flops_per_launch": r["flops_per_call"],
+        # below the ridge point the attainable rate is the HBM roofline
+        # I * 8 TB/s (I = algorithmic flops per algorithmic byte)
+        "algorithmic_bytes_per_launch": r["bytes_per_call"],
+        "intensity_flop_per_byte": intensity,
+        "attainable": attainable,
+        "frac_of_attainable": r["tflops"] / attainable,
     }
 
 
