@@ -198,6 +198,21 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
 // of 8 kSlice (kSteps steps), K / group_size <= kDecGroups and a multiple of
 // the 16-byte piece's entry count, and 16-byte aligned operands.
 //
+// kDirect (4-bit codes, 64-k slices, 2 or 4 steps): the codes skip the
+// LDS. Wave w takes the contiguous k range [64 kSteps w, 64 kSteps (w + 1))
+// of the workgroup's range (its slice of step s is the range's s-th 64 k),
+// so each column's codes for a wave are one run of 32 kSteps bytes: lane
+// (column c = l % 16, quarter q = l / 16) loads 16-byte piece 4 i + q of
+// that run (instruction i of each 16-column tile, all at the start). A
+// piece holds 32 codes, four 8-code dwords: the lower half-wave's pieces
+// belong to step 2 i, the upper's to step 2 i + 1, and one
+// v_permlane32_swap of dwords kb and 2 + kb gives both steps' fragment kb.
+// Lane quarter q then holds the slice's k 32 (q & 1) + 16 (q >> 1) + 8 kb
+// .. +7 (the x fragments are read in the same order), and the x tile of a
+// step gathers the 8 waves' slices. Freed of the weight tile, the LDS holds
+// two x tiles at 64 rows: one barrier a step, and the next step's x is
+// staged while the other waves compute.
+//
 // Split K: with gridDim.y = S > 1, workgroup (t, j) takes the k range
 // [j K / S, (j + 1) K / S) of column tile t (kSteps steps of it) and stores
 // its float32 block at partial[j][M][N]; qlinear_split_sum_kernel adds the
@@ -239,7 +254,7 @@ GDN_DEV bf16x8 code_fragment(const uint32_t* words, CodeConsts k) {
     }
 }
 
-template <int kBits, int kSteps, int kMT, int kSlice, int kCols, bool kXF32>
+template <int kBits, int kSteps, int kMT, int kSlice, int kCols, bool kXF32, bool kDirect = false>
 __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     const void* __restrict__ xp, const uint32_t* __restrict__ w, const void* __restrict__ scales,
     const void* __restrict__ biases, int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N,
@@ -253,13 +268,17 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     constexpr int kWPC = kStep * kBits / 32;     // packed words of one column per step
     constexpr int kWS = kWPC + 4;                // word row stride of the weight tile
     constexpr int kXLoads = kRows * kStep / 8 / 512;   // 8-element x chunks per thread per step
-    constexpr int kWLoads = kCols * kWPC / 4 / 512;    // 16-byte weight pieces per thread per step
+    constexpr int kWLoads = kDirect ? 1 : kCols * kWPC / 4 / 512;  // 16-byte weight pieces per thread per step
+    static_assert(!kDirect || (kBits == 4 && kSlice == 64 && (kSteps == 2 || kSteps == 4)),
+                  "direct code fragments: 4-bit codes, 64-k slices, 2 or 4 steps");
+    // first k of wave wv's slice of step s, in the workgroup's range
+    auto slice_k = [](int wv_, int s_) { return kDirect ? kSlice * (wv_ * kSteps + s_) : kStep * s_ + kSlice * wv_; };
     // float32 x is staged as two bf16 tiles, hi = bf16(x) and lo =
     // bf16(x - hi) (together x to ~16 significant bits), each fragment
     // taking two MFMAs into the same accumulator
     constexpr int kXParts = kXF32 ? 2 : 1;
     constexpr int kXBytes = kXParts * kRows * kXS * 2;
-    constexpr int kWBytes = kCols * kWS * 4;
+    constexpr int kWBytes = kDirect ? 0 : kCols * kWS * 4;
     constexpr int kPBytes = 4 * kMT * kTN * 64 * 16;  // 4 partial blocks of kMT x kTN tiles of float4 per lane
     // a group spans at least one slice, so the k range holds at most
     // 8 kSteps groups (and at most kDecGroups, the host's limit)
@@ -270,6 +289,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     // for two workgroups per CU with 32 columns
     constexpr int kBudget = kCols == 32 ? 80 * 1024 : 160 * 1024;
     constexpr int kBufs = 2 * (kXBytes + kWBytes) + kSBBytes <= kBudget ? 2 : 1;
+    static_assert(!kDirect || kBufs == 2, "direct code fragments are for double-buffered x tiles");
     constexpr int kMain = kBufs * (kXBytes + kWBytes) > kPBytes ? kBufs * (kXBytes + kWBytes) : kPBytes;
     constexpr int kBQ = (kSteps + 3) / 4;        // bias MFMAs (four of a wave's slices each) per tile
     static_assert(kXLoads >= 1 && kWLoads >= 1, "step too small for 512 threads");
@@ -324,11 +344,15 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
 #pragma unroll
     for (int i = 0; i < kXLoads; ++i) {
         const int r = tid / kChunksPerRow + i * kXRowStep;
-        xoffs[i] = ((r < M ? r : M - 1) * K + 8 * (tid % kChunksPerRow)) * esx;
+        // chunk ch of a step's tile: 8 k of wave ch / 8's slice (kDirect), or
+        // of the step's contiguous k
+        const int ch = tid % kChunksPerRow;
+        const int kc = kDirect ? (ch >> 3) * kSteps * kSlice + 8 * (ch & 7) : 8 * ch;
+        xoffs[i] = ((r < M ? r : M - 1) * K + kc) * esx;
     }
     xchunk_t xv[kXLoads];
     auto fetch_x = [&](int s) {
-        const int soff = (k0 + kStep * s) * esx;
+        const int soff = (k0 + (kDirect ? kSlice : kStep) * s) * esx;
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
             const int o = xoffs[i];
@@ -368,6 +392,19 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     };
     fetch_x(0);
 
+    // kDirect: the wave's code pieces for every step, requested now
+    // (instruction i of tile tn: piece 4 i + lq of column 16 tn + lr)
+    u32x4 wd[kDirect ? kSteps / 2 : 1][kTN];
+    if constexpr (kDirect) {
+#pragma unroll
+        for (int tn = 0; tn < kTN; ++tn) {
+            const int col = n0 + 16 * tn + lr;
+            const int o = (col < N ? col : N - 1) * wpr4 + slice_k(wv, 0) / 2 + 16 * lq;
+#pragma unroll
+            for (int i = 0; i < kSteps / 2; ++i)
+                wd[i][tn] = __builtin_amdgcn_raw_buffer_load_b128(wr, o + 64 * i, k0 / 2, 0);
+        }
+    }
     // packed weights of every step: piece i of a step is 16-byte piece wpc of
     // column wc0 + i kWColStep (clamped)
     constexpr int kPiecesPerCol = kWPC / 4, kWColStep = 512 / kPiecesPerCol;
@@ -389,9 +426,12 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
         for (int i = 0; i < kWLoads; ++i)
             wq[s % kPre][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[i], (k0 * kBits / 8) + 4 * kWPC * s, 0);
     };
+    if constexpr (!kDirect) {
 #pragma unroll
-    for (int s = 0; s < kPre; ++s) load_w(s);
+        for (int s = 0; s < kPre; ++s) load_w(s);
+    }
     auto stage_w = [&](int buf, int s) {
+        if constexpr (kDirect) return;
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i)
             *reinterpret_cast<u32x4*>(&ws(buf)[(wc0 + i * kWColStep) * kWS + 4 * wpc]) = wq[s % kPre][i];
@@ -444,8 +484,23 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
     auto compute = [&](int buf, int s) {
         const uint16_t* xb = xs(buf);
         const uint32_t* wb = ws(buf);
-        const int g = (kStep * s + kSlice * wv) / group_size;
+        const int g = slice_k(wv, s) / group_size;
         bf16x8 a[kXParts][kMT][kKB];
+        if constexpr (kDirect) {
+            // steps 2 i and 2 i + 1 of every tile: dwords kb and 2 + kb swapped
+            // across the half-waves give fragment kb of both
+            if (s % 2 == 0) {
+#pragma unroll
+                for (int tn = 0; tn < kTN; ++tn)
+#pragma unroll
+                    for (int kb = 0; kb < kKB; ++kb) {
+                        const auto r = __builtin_amdgcn_permlane32_swap(wd[s / 2][tn][kb], wd[s / 2][tn][2 + kb],
+                                                                       false, false);
+                        wd[s / 2][tn][kb] = r[0];
+                        wd[s / 2][tn][2 + kb] = r[1];
+                    }
+            }
+        }
 #pragma unroll
         for (int tm = 0; tm < kMT; ++tm) {
             // ones times the x fragment as the B operand: every element of
@@ -455,8 +510,9 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
             for (int h = 0; h < kXParts; ++h)
 #pragma unroll
                 for (int kb = 0; kb < kKB; ++kb) {
+                    const int ch = kDirect ? 32 * (lq & 1) + 16 * (lq >> 1) + 8 * kb : 32 * kb + 8 * lq;
                     a[h][tm][kb] = *reinterpret_cast<const bf16x8*>(
-                        &xb[(h * kRows + 16 * tm + lr) * kXS + kSlice * wv + 32 * kb + 8 * lq]);
+                        &xb[(h * kRows + 16 * tm + lr) * kXS + kSlice * wv + ch]);
                     X = mfma_bf16(ones, a[h][tm][kb], X);
                 }
             if (lq == (s & 3)) xa[s / 4][tm] = X[0];
@@ -467,8 +523,14 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
             const float sp = kQScale * sbs[c * (gl + 1) + g];
             bf16x8 bq[kKB];
 #pragma unroll
-            for (int kb = 0; kb < kKB; ++kb)
-                bq[kb] = code_fragment<kBits>(&wb[c * kWS + (kSlice * wv + 32 * kb + 8 * lq) * kBits / 32], kc);
+            for (int kb = 0; kb < kKB; ++kb) {
+                if constexpr (kDirect) {
+                    const uint32_t word = wd[s / 2][tn][(s % 2) * 2 + kb];
+                    bq[kb] = code_fragment<kBits>(&word, kc);
+                } else {
+                    bq[kb] = code_fragment<kBits>(&wb[c * kWS + (kSlice * wv + 32 * kb + 8 * lq) * kBits / 32], kc);
+                }
+            }
 #pragma unroll
             for (int tm = 0; tm < kMT; ++tm) {
                 f32x4 P = zero;
@@ -519,7 +581,7 @@ __global__ __launch_bounds__(512) void qlinear_decode_kernel(
 #pragma unroll
     for (int q = 0; q < kBQ; ++q) {
         const int st = 4 * q + lq;
-        const int g = (kStep * st + kSlice * wv) / group_size;
+        const int g = slice_k(wv, st) / group_size;
 #pragma unroll
         for (int tn = 0; tn < kTN; ++tn) {
             const int c = 16 * tn + lr;
@@ -669,9 +731,14 @@ int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const
                         !overlaps(partial, int64_t(splits) * M * N * 4, x, int64_t(M) * K * (kXF32 ? 4 : 2)),
                     "gdn_quantized_matmul: workspace overlaps x or y");
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
-#define GDN_DEC(STEPS)                                                                              \
-    hipLaunchKernelGGL((qlinear_decode_kernel<kBits, STEPS, kMT, kSlice, kCols, kXF32>), grid, dim3(512), 0, s, \
-                       x, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, partial)
+    // 17-64 rows of bf16 x against 4-bit codes in 64-k slices take the code
+    // fragments straight from memory (two x tiles in the LDS) at 2 or 4 steps
+#define GDN_DEC(STEPS)                                                                                       \
+    hipLaunchKernelGGL((qlinear_decode_kernel<kBits, STEPS, kMT, kSlice, kCols, kXF32,                        \
+                                              kBits == 4 && kSlice == 64 && kMT >= 2 && !kXF32 &&         \
+                                                  (STEPS == 2 || STEPS == 4)>),                           \
+                       grid, dim3(512), 0, s, x, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K,   \
+                       group_size, partial)
     switch (ks / splits) {
         case 1: GDN_DEC(1); break;
         case 2: GDN_DEC(2); break;
