@@ -314,10 +314,15 @@ int gdn_quantized_matmul(const void *x, int x_dtype, const void *w, const void *
  * returns GDN_EINVAL. The first call on a GPU looks up that GPU's copy of
  * the array (hipGetSymbolAddress, which may load the library's code object
  * there): make that first call eagerly, before capturing calls into a HIP
- * graph on that GPU. No call allocates or frees memory. Calls
- * that overlap on one GPU share its scratch and race: the caller orders
- * them (one stream, or events). Arguments and results as
- * gdn_quantized_matmul without workspace and workspace_bytes.
+ * graph on that GPU (that call also creates the GPU's one ordering
+ * event). No call allocates or frees memory. The calls that use the
+ * scratch take it in turn: one on a different stream than the previous
+ * scratch user first makes its stream wait (hipStreamWaitEvent) for that
+ * call, so calls from several streams and host threads do not race. A call
+ * made while its stream is being captured neither waits nor records (a
+ * capture cannot wait on work outside it): replays of such a graph are
+ * ordered against calls on other streams by the caller. Arguments and
+ * results as gdn_quantized_matmul without workspace and workspace_bytes.
  * No counterpart in the reference (MLX's kernels allocate their own
  * scratch): for callers that cannot allocate device memory, such as code
  * under HIP graph capture, tight serving loops and harnesses that forbid

@@ -1242,35 +1242,42 @@ constexpr int64_t kScratchBytes = int64_t(kCUs) * 64 * 64 * 4;
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
+// Per device: the scratch's address, and the order of the calls that use
+// it. Calls on one stream are ordered by the stream; a call on another
+// stream than the previous scratch user's first waits (on the GPU) for the
+// event recorded after that call, so calls from several streams take the
+// scratch in turn instead of racing on it. Calls made while their stream
+// is being captured into a graph neither wait nor record (a capture may
+// not wait on work outside it): a graph's replays are ordered against
+// eager calls on other streams by the caller.
+struct ScratchState {
+    void* ptr = nullptr;
+    hipEvent_t done = nullptr;          // recorded after the last eager scratch user
+    hipStream_t last = nullptr;         // that call's stream
+    bool used = false;
+};
 std::mutex g_scratch_mutex;
-void* g_scratch_ptr[kMaxDevices] = {};
+ScratchState g_scratch[kMaxDevices];
 
-// The scratch array's address on the device that runs `stream`, looked up
-// once per device with that device current.
-int scratch_for(hipStream_t stream, void** ptr) {
-    int dev = -1;
-    hipError_t err = hipStreamGetDevice(stream, &dev);
-    if (err != hipSuccess) return fail(int(err), "gdn_quantized_matmul_noalloc: hipStreamGetDevice: %s",
-                                       hipGetErrorString(err));
-    GDN_REQUIRE(dev >= 0 && dev < kMaxDevices, "gdn_quantized_matmul_noalloc: device %d out of range", dev);
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if (!g_scratch_ptr[dev]) {
-        int current = -1;
-        err = hipGetDevice(&current);
-        if (err == hipSuccess && current != dev) err = hipSetDevice(dev);
-        void* p = nullptr;
-        if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (current >= 0 && current != dev) {
-            const hipError_t back = hipSetDevice(current);
-            if (err == hipSuccess) err = back;
-        }
-        if (err != hipSuccess || !p)
-            return fail(err != hipSuccess ? int(err) : GDN_EINVAL,
-                        "gdn_quantized_matmul_noalloc: scratch address on device %d: %s", dev,
-                        hipGetErrorString(err));
-        g_scratch_ptr[dev] = p;
+// Set-up on the first call on a device, with that device current: the
+// scratch array's address (hipGetSymbolAddress) and the ordering event.
+int scratch_setup(int dev, ScratchState& st) {
+    int current = -1;
+    hipError_t err = hipGetDevice(&current);
+    if (err == hipSuccess && current != dev) err = hipSetDevice(dev);
+    void* p = nullptr;
+    if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipEvent_t ev = nullptr;
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (current >= 0 && current != dev) {
+        const hipError_t back = hipSetDevice(current);
+        if (err == hipSuccess) err = back;
     }
-    *ptr = g_scratch_ptr[dev];
+    if (err != hipSuccess || !p)
+        return fail(err != hipSuccess ? int(err) : GDN_EINVAL,
+                    "gdn_quantized_matmul_noalloc: scratch set-up on device %d: %s", dev, hipGetErrorString(err));
+    st.ptr = p;
+    st.done = ev;
     return 0;
 }
 
@@ -1295,10 +1302,40 @@ extern "C" int gdn_quantized_matmul_noalloc(const void* x, int x_dtype, const vo
                     "gdn_quantized_matmul_noalloc: this call needs %lld bytes of split-K scratch; the "
                     "library holds %lld (use gdn_quantized_matmul with a workspace)",
                     static_cast<long long>(need), static_cast<long long>(kScratchBytes));
-    void* ptr = nullptr;
-    if (int rc = scratch_for(as_stream(stream), &ptr)) return rc;
-    return quantized_matmul(x, x_dtype, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, bits,
-                            group_size, need > 0 ? ptr : nullptr, need, stream);
+    if (need == 0)  // no split: the scratch is not touched
+        return quantized_matmul(x, x_dtype, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, bits,
+                                group_size, nullptr, 0, stream);
+    const hipStream_t s = as_stream(stream);
+    int dev = -1;
+    hipError_t err = hipStreamGetDevice(s, &dev);
+    if (err != hipSuccess)
+        return fail(int(err), "gdn_quantized_matmul_noalloc: hipStreamGetDevice: %s", hipGetErrorString(err));
+    GDN_REQUIRE(dev >= 0 && dev < kMaxDevices, "gdn_quantized_matmul_noalloc: device %d out of range", dev);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(s, &capture);
+    if (err != hipSuccess)
+        return fail(int(err), "gdn_quantized_matmul_noalloc: hipStreamIsCapturing: %s", hipGetErrorString(err));
+    const bool eager = capture == hipStreamCaptureStatusNone;
+    // held from the wait to the record, so that calls from several host
+    // threads take the scratch in the order they enqueue
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ScratchState& st = g_scratch[dev];
+    if (!st.ptr)
+        if (int rc = scratch_setup(dev, st)) return rc;
+    if (eager && st.used && st.last != s) {
+        err = hipStreamWaitEvent(s, st.done, 0);
+        if (err != hipSuccess)
+            return fail(int(err), "gdn_quantized_matmul_noalloc: hipStreamWaitEvent: %s", hipGetErrorString(err));
+    }
+    const int rc = quantized_matmul(x, x_dtype, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K,
+                                    bits, group_size, st.ptr, need, stream);
+    if (rc != 0 || !eager) return rc;
+    err = hipEventRecord(st.done, s);
+    if (err != hipSuccess)
+        return fail(int(err), "gdn_quantized_matmul_noalloc: hipEventRecord: %s", hipGetErrorString(err));
+    st.last = s;
+    st.used = true;
+    return 0;
 }
 
 namespace gdn {

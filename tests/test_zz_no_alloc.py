@@ -133,3 +133,37 @@ def test_noalloc_captured_in_a_graph_replays_the_workspace_entry_points_bits(gpu
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, ref), i
+
+
+@pytest.mark.gpu
+def test_noalloc_calls_from_two_streams_take_the_scratch_in_turn(gpu):
+    """Calls on two streams, each enqueued right after the other's, both
+    using the whole scratch (the out_proj shape at 64 rows, 8 splits): the
+    second stream waits on the GPU for the first one's call, so every
+    result has gdn_quantized_matmul's bits with a workspace of its own.
+    Five rounds, alternating which stream goes first."""
+
+    lib = _lib.load()
+    M, N, K, bits, gs = 64, 2048, 4096, 4, 64
+    need = lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, M, N, K, bits, gs)
+    assert need == SCRATCH_BYTES
+    cases = [_case(gpu, M, N, K, bits, gs, seed=90 + j) for j in range(2)]
+    refs = []
+    for x, words, scales, biases, residual in cases:
+        ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+        refs.append(_run(lib, "gdn_quantized_matmul", gpu, x, words, scales, biases, residual, M, N, K,
+                         bits, gs, ws))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    for r in range(5):
+        print(f"noalloc two-stream round {r}", flush=True)
+        order = (0, 1) if r % 2 == 0 else (1, 0)
+        got = {}
+        for j in order:
+            with torch.cuda.stream(streams[j]):
+                x, words, scales, biases, residual = cases[j]
+                got[j] = _run(lib, "gdn_quantized_matmul_noalloc", gpu, x, words, scales, biases, residual,
+                              M, N, K, bits, gs)
+        torch.cuda.synchronize()
+        for j in (0, 1):
+            assert torch.equal(got[j], refs[j]), (r, j)
