@@ -256,10 +256,18 @@ GDN_DEV bf16x8 code_fragment(const uint32_t* words, CodeConsts k) {
 
 template <int kBits, int kSteps, int kMT, int kSlice, int kCols, bool kXF32, bool kDirect = false>
 __global__ __launch_bounds__(512) void qlinear_decode_kernel(
-    const void* __restrict__ xp, const uint32_t* __restrict__ w, const void* __restrict__ scales,
-    const void* __restrict__ biases, int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N,
-    int K, int group_size, float* __restrict__ partial) {
+    const void* __restrict__ x_all, const uint32_t* __restrict__ w, const void* __restrict__ scales,
+    const void* __restrict__ biases, int sb_dtype, void* y_all, int y_dtype, const void* residual_all, int M_all,
+    int N, int K, int group_size, float* __restrict__ partial) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    // Row blocks: workgroup (t, j, z) takes rows [16 kMT z, 16 kMT (z + 1))
+    // of x, y and the residual (gridDim.z = 1: all M rows).
+    const int row0 = int(blockIdx.z) * 16 * kMT;
+    const int M = gridDim.z > 1 ? (M_all - row0 < 16 * kMT ? M_all - row0 : 16 * kMT) : M_all;
+    const void* xp = static_cast<const char*>(x_all) + int64_t(row0) * K * (kXF32 ? 4 : 2);
+    const int esy = y_dtype == GDN_F32 ? 4 : 2;
+    void* y = static_cast<char*>(y_all) + int64_t(row0) * N * esy;
+    const void* residual = residual_all ? static_cast<const char*>(residual_all) + int64_t(row0) * N * esy : nullptr;
     constexpr int kStep = 8 * kSlice;            // k per step
     constexpr int kKB = kSlice / 32;             // MFMA k blocks per wave per step
     constexpr int kRows = 16 * kMT;
@@ -721,16 +729,17 @@ int decode_splits(int tiles, int ks, int K, int group_size, int per_piece, int M
 template <int kBits, int kMT, int kSlice, int kCols, bool kXF32>
 int launch_decode_mt(const void* x, const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
                      void* y, int y_dtype, const void* residual, int M, int N, int K, int group_size,
-                     void* workspace, int64_t ws_bytes, hipStream_t s) {
+                     void* workspace, int64_t ws_bytes, hipStream_t s, int row_blocks = 1) {
     const int tiles = (N + kCols - 1) / kCols, ks = K / (8 * kSlice);
-    const int splits = decode_splits(tiles, ks, K, group_size, sb_dtype == GDN_F32 ? 4 : 8, M, N,
-                                     workspace ? ws_bytes : 0);
+    const int splits = row_blocks > 1 ? 1
+                                      : decode_splits(tiles, ks, K, group_size, sb_dtype == GDN_F32 ? 4 : 8, M, N,
+                                                      workspace ? ws_bytes : 0);
     float* partial = splits > 1 ? static_cast<float*>(workspace) : nullptr;
     if (partial)
         GDN_REQUIRE(!overlaps(partial, int64_t(splits) * M * N * 4, y, int64_t(M) * N * dtype_size(y_dtype)) &&
                         !overlaps(partial, int64_t(splits) * M * N * 4, x, int64_t(M) * K * (kXF32 ? 4 : 2)),
                     "gdn_quantized_matmul: workspace overlaps x or y");
-    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits), static_cast<unsigned>(row_blocks));
     // 17-64 rows of bf16 x against 4-bit codes in 64-k slices take the code
     // fragments straight from memory (two x tiles in the LDS) at 2 or 4 steps
 #define GDN_DEC(STEPS)                                                                                       \
@@ -1041,11 +1050,22 @@ int launch_gemv(const void* x, bool x_f32, const uint32_t* w, const void* scales
 // over all CUs. 33-64 rows keep 64 columns (the LDS holds one workgroup).
 // float32 x (twice the x tiles) runs up to 32 rows: 32 columns up to 16
 // rows, 64 beyond.
+// 17-64 rows of bf16 x against 4-bit codes in 64-k slices, for a
+// projection with few column tiles (the layer's out_proj): 16-row blocks of
+// the 16-row kernel (grid z), all in one launch, with no split of K.
+int decode_row_blocks(bool x_f32, int M, int N, int bits, int group_size) {
+    if (x_f32 || M <= 16 || bits != 4 || decode_slice(group_size) != 64) return 1;
+    const int rb = (M + 15) / 16, tiles = (N + 31) / 32;
+    return (N + 63) / 64 < 128 && int64_t(tiles) * rb <= kCUs ? rb : 1;
+}
+
 int launch_decode(const void* x, bool x_f32, const uint32_t* w, const void* scales, const void* biases,
                   int sb_dtype, void* y, int y_dtype, const void* residual, int M, int N, int K, int bits,
                   int group_size, void* workspace, int64_t ws_bytes, hipStream_t s) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
 #define GDN_ARGS x, w, scales, biases, sb_dtype, y, y_dtype, residual, M, N, K, group_size, workspace, ws_bytes, s
+    if (const int rb = decode_row_blocks(x_f32, M, N, bits, group_size); rb > 1)
+        return launch_decode_mt<4, 1, 64, 32, false>(GDN_ARGS, rb);
 #define GDN_MT(BITS, SLICE, NARROW)                                                       \
     do {                                                                                  \
         if (x_f32) {                                                                      \
@@ -1068,6 +1088,7 @@ int launch_decode(const void* x, bool x_f32, const uint32_t* w, const void* scal
 
 // Workspace bytes launch_decode uses for a call (0: it does not split K).
 int64_t decode_workspace_bytes(bool x_f32, int sb_dtype, int M, int N, int K, int bits, int group_size) {
+    if (decode_row_blocks(x_f32, M, N, bits, group_size) > 1) return 0;
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4, slice = decode_slice(group_size);
     const int cols = decode_cols(x_f32, mt, bits, group_size);
     const int splits = decode_splits((N + cols - 1) / cols, K / (8 * slice), K, group_size,

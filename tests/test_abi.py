@@ -92,16 +92,22 @@ def test_empty_work_is_a_no_op():
 
 
 def test_quantized_matmul_workspace_size():
-    """K is split only where the decode kernel runs few column tiles: the
-    layer's out_proj (N = 2048: 32 tiles of 64 columns at 64 rows) takes 8
-    splits of float32 (M, N) blocks, the stacked input projection (N =
-    12352) none; shapes the decode kernel does not take need none, and
-    neither does one row of 4-bit codes (the matrix-vector kernel)."""
+    """K is split only where the decode kernel runs few column tiles: 8-bit
+    codes of 64 rows over 2048 columns (32 tiles of 64) take 4 splits of
+    float32 (M, N) blocks; out_proj's shape in 4-bit group-64 codes at
+    17-64 rows runs as 16-row blocks with no split (none), one 16-row block
+    splits 4 ways, and the stacked input projection (N = 12352) does not
+    split; shapes the decode kernel does not take need none, and neither
+    does one row of 4-bit codes (the matrix-vector kernel)."""
 
     lib = _lib.load()
     size = lambda *a: lib.gdn_quantized_matmul_workspace_size(*a)
     bf, f32 = _lib.GDN_BF16, _lib.GDN_F32
-    assert size(bf, bf, 64, 2048, 4096, 4, 64) == 8 * 64 * 2048 * 4
+    assert size(bf, bf, 64, 2048, 2048, 8, 64) == 4 * 64 * 2048 * 4  # 32 tiles, 4 steps
+    assert size(bf, bf, 64, 8192, 2048, 8, 64) == 2 * 64 * 8192 * 4  # 128 tiles: 2 splits
+    assert size(bf, bf, 64, 2048, 4096, 4, 64) == 0                # 4 row blocks of 16
+    assert size(bf, bf, 17, 2048, 4096, 4, 64) == 0                # 2 row blocks
+    assert size(bf, bf, 16, 2048, 4096, 4, 64) == 4 * 16 * 2048 * 4  # one block: split
     assert size(bf, bf, 2, 2048, 4096, 4, 64) == 4 * 2 * 2048 * 4  # 64 tiles of 32 columns
     assert size(bf, bf, 1, 2048, 4096, 4, 64) == 0                 # one row: matrix-vector kernel
     assert size(bf, bf, 1, 2048, 2048, 8, 64) == 4 * 2048 * 4      # (not for 8-bit codes)

@@ -142,10 +142,10 @@ def test_one_row_runs_the_matrix_vector_kernel_exactly(gpu, N, K, gs, sb, x32):
 
 
 @pytest.mark.parametrize("M,N,K,bits,gs,sb,x32,splits", [
-    (64, 2048, 4096, 4, 64, "bf16", False, 8),   # the layer's out_proj: 32 column tiles
-    (16, 2048, 4096, 4, 64, "bf16", False, 4),
+    (64, 8192, 2048, 8, 64, "bf16", False, 2),   # 128 column tiles of 64
+    (16, 2048, 4096, 4, 64, "bf16", False, 4),   # out_proj at 16 rows: 64 tiles of 32
     (1, 1000, 2048, 8, 32, "f16", False, 8),     # ragged last tile
-    (40, 100, 4096, 4, 64, "f32", False, 8),
+    (40, 100, 2048, 8, 64, "f32", False, 4),
     (5, 300, 1024, 4, 32, "bf16", True, 4),      # float32 x
 ])
 def test_split_k_matches_the_unsplit_kernel_and_the_oracle(gpu, M, N, K, bits, gs, sb, x32, splits):
@@ -184,6 +184,51 @@ def test_split_k_matches_the_unsplit_kernel_and_the_oracle(gpu, M, N, K, bits, g
     # through quantized_linear (its own workspace), in x's dtype
     y = gdn.quantized_linear(xt, W, gdn.QuantScheme(bits, gs))
     np.testing.assert_array_equal(y.float().cpu().numpy(), torch.tensor(outs[1]).to(xdt).float().numpy())
+
+
+@pytest.mark.parametrize("M,N,K,sb", [
+    (64, 2048, 4096, "bf16"),   # the layer's out_proj: 64 column tiles x 4 row blocks
+    (40, 2048, 4096, "f16"),    # ragged last row block (8 rows)
+    (17, 100, 4096, "f32"),     # one row in the second block; ragged last column tile
+])
+def test_row_blocks_match_the_oracle_in_one_launch(gpu, M, N, K, sb):
+    """17-64 rows of 4-bit group-64 codes with few column tiles run as
+    16-row blocks of the 16-row kernel in one launch: no workspace is asked
+    for or used (the same bits with and without one), every row block
+    meets the oracle's bound, and the residual is added in the store as the
+    unfused add of two bf16 arrays."""
+
+    bits, gs = 4, 64
+    rng = np.random.default_rng(M * 7 + N)
+    words, s, b = _weights(rng, N, K, bits, gs, sb)
+    x = R.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    ref = Q.quantized_matmul(x, words, s, b, bits, gs, w_round="f32")
+    W = _dev_weights(gpu, words, s, b, sb)
+    xt = torch.tensor(x, device=gpu).to(torch.bfloat16)
+    lib = _lib.load()
+    assert lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.dtype_code(_TORCH[sb]), M, N, K,
+                                                   bits, gs) == 0
+    ws = torch.full((1 << 20,), float("nan"), device=gpu)
+    outs = []
+    for w_ptr, w_len in ((None, 0), (_lib.ptr(ws), 4 << 20)):
+        y = torch.empty(M, N, device=gpu)
+        _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.GDN_BF16, _lib.ptr(W["weight"]),
+                  _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
+                  _lib.ptr(y), _lib.GDN_F32, None, M, N, K, bits, gs, w_ptr, w_len, _lib.stream_ptr(gpu))
+        outs.append(y.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    assert torch.isnan(ws).all()  # untouched
+    tol = 1e-5 * np.abs(ref).max() + 1e-6
+    for r0 in range(0, M, 16):
+        assert np.abs(outs[0][r0:r0 + 16] - ref[r0:r0 + 16]).max() <= tol, r0
+    # bf16 y with a residual: the product rounded, then the sum rounded
+    res = torch.randn(M, N, device=gpu).to(torch.bfloat16)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    _lib.call("gdn_quantized_matmul", _lib.ptr(xt), _lib.GDN_BF16, _lib.ptr(W["weight"]),
+              _lib.ptr(W["scales"]), _lib.ptr(W["biases"]), _lib.dtype_code(W["scales"].dtype),
+              _lib.ptr(y), _lib.GDN_BF16, _lib.ptr(res), M, N, K, bits, gs, None, 0, _lib.stream_ptr(gpu))
+    unfused = (torch.tensor(outs[0], device=gpu).to(torch.bfloat16) + res).cpu()
+    assert torch.equal(y.cpu(), unfused)
 
 
 @pytest.mark.parametrize("bits,gs,sb,out", [(4, 64, "bf16", "bf16"), (8, 32, "f16", "f32"),

@@ -21,8 +21,9 @@ SCRATCH_BYTES = 4 << 20
 def test_every_decode_shape_fits_the_scratch():
     """The workspace the full split takes, over decode-kernel shapes (rows
     1-64, the layer's projection widths and depths, both bit widths and all
-    group sizes), never exceeds the 4 MiB scratch; the out_proj shape at 64
-    rows takes all of it."""
+    group sizes), never exceeds the 4 MiB scratch; 64 rows of 8192 columns
+    in 8-bit codes take all of it (2 splits of 128 column tiles), and
+    out_proj's shape in 4-bit codes none (16-row blocks, no split)."""
 
     lib = _lib.load()
     worst = 0
@@ -34,8 +35,10 @@ def test_every_decode_shape_fits_the_scratch():
             assert 0 <= need <= SCRATCH_BYTES, (M, N, K, bits, gs, sb, xd, need)
             worst = max(worst, need)
     assert worst == SCRATCH_BYTES
+    assert lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, 64, 8192, 2048,
+                                                   8, 64) == SCRATCH_BYTES
     assert lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, 64, 2048, 4096,
-                                                   4, 64) == SCRATCH_BYTES
+                                                   4, 64) == 0
 
 
 def _case(dev, M, N, K, bits, gs, seed):
@@ -66,14 +69,14 @@ def _run(lib, fn, dev, x, words, scales, biases, residual, M, N, K, bits, gs, wo
 @pytest.mark.gpu
 def test_noalloc_matches_the_workspace_entry_point_on_two_calls(gpu):
     """Two calls in a row, each against gdn_quantized_matmul with a full
-    workspace (same split, so the same bits): the layer's out_proj at 64
-    rows (8 splits, the whole scratch) with a residual, then a smaller call
+    workspace (same split, so the same bits): 64 rows of 8192 columns in
+    8-bit codes (2 splits, the whole scratch) with a residual, then a smaller call
     (16 rows of a 1024 x 2048 projection, fewer and smaller partial
     blocks) that reads none of what the first left in the scratch; and a
     one-row call (no split, no scratch)."""
 
     lib = _lib.load()
-    shapes = [(64, 2048, 4096, 4, 64, True), (16, 1024, 2048, 4, 64, False),
+    shapes = [(64, 8192, 2048, 8, 64, True), (16, 1024, 2048, 4, 64, False),
               (1, 2048, 4096, 8, 32, False)]
     for i, (M, N, K, bits, gs, with_res) in enumerate(shapes):
         print(f"noalloc case {i}: M={M} N={N} K={K} bits={bits} group={gs}", flush=True)
@@ -103,11 +106,11 @@ def test_noalloc_captured_in_a_graph_replays_the_workspace_entry_points_bits(gpu
     eager call on the device (the first call looks up the scratch's address,
     which is not a call to make inside a capture): three replays, each after
     eager work that leaves other partial blocks in the scratch, give
-    gdn_quantized_matmul's bits with a full workspace, on the out_proj shape
-    at 64 rows (8 splits, the whole scratch) with a residual."""
+    gdn_quantized_matmul's bits with a full workspace, on 64 rows of 8192
+    columns in 8-bit codes (2 splits, the whole scratch) with a residual."""
 
     lib = _lib.load()
-    M, N, K, bits, gs = 64, 2048, 4096, 4, 64
+    M, N, K, bits, gs = 64, 8192, 2048, 8, 64
     x, words, scales, biases, residual = _case(gpu, M, N, K, bits, gs, seed=77)
     need = lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, M, N, K, bits, gs)
     ws = torch.empty(need, dtype=torch.uint8, device=gpu)
@@ -138,13 +141,13 @@ def test_noalloc_captured_in_a_graph_replays_the_workspace_entry_points_bits(gpu
 @pytest.mark.gpu
 def test_noalloc_calls_from_two_streams_take_the_scratch_in_turn(gpu):
     """Calls on two streams, each enqueued right after the other's, both
-    using the whole scratch (the out_proj shape at 64 rows, 8 splits): the
-    second stream waits on the GPU for the first one's call, so every
-    result has gdn_quantized_matmul's bits with a workspace of its own.
-    Five rounds, alternating which stream goes first."""
+    using the whole scratch (64 rows of 8192 columns in 8-bit codes, 2
+    splits): the second stream waits on the GPU for the first one's call,
+    so every result has gdn_quantized_matmul's bits with a workspace of its
+    own. Five rounds, alternating which stream goes first."""
 
     lib = _lib.load()
-    M, N, K, bits, gs = 64, 2048, 4096, 4, 64
+    M, N, K, bits, gs = 64, 8192, 2048, 8, 64
     need = lib.gdn_quantized_matmul_workspace_size(_lib.GDN_BF16, _lib.GDN_BF16, M, N, K, bits, gs)
     assert need == SCRATCH_BYTES
     cases = [_case(gpu, M, N, K, bits, gs, seed=90 + j) for j in range(2)]
