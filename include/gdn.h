@@ -293,8 +293,10 @@ int gdn_gated_rmsnorm(const void *x, int x_dtype, const void *z, int z_dtype, in
  *      workgroups, which store float32 partial products there, and a second
  *      kernel adds them in a fixed order (deterministic; the sum's order,
  *      and so its last bits, differ from the unsplit kernel's). With less,
- *      it splits less or not at all. Calls sharing a workspace must not
- *      overlap.
+ *      it splits less or not at all. 17-64 rows of bf16 x against 4-bit
+ *      codes in 64-k slices with few column tiles (out_proj's shape) run
+ *      instead as 16-row blocks in one launch and take no workspace (its
+ *      size is 0 there). Calls sharing a workspace must not overlap.
  * Replaces mx.quantized_matmul(..., mode="affine") in quantized_linear
  * (model/moe_block.py:44-55), used for the layer's projections
  * (model/qwen3_5/linear_attention.py:96-101,125).
