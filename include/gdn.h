@@ -52,7 +52,8 @@ typedef enum {
  * residual, 8 the prefill's gate row stride, 9 the front-end's qkv row stride,
  * 10 the gated norm's z layout, 11 gdn_quantized_matmul_noalloc, 12 the
  * prefill's float32 q/k/v, 13 gdn_prefill_fused, 14 gdn_dequantize's mode, 15
- * gdn_quantized_matmul_scheme and its workspace size). */
+ * gdn_quantized_matmul_scheme and its workspace size, 16 conv_arrivals as
+ * counters whose bit 16 is a parity of the half bit). */
 int gdn_abi_version(void);
 
 /* Message describing the calling thread's last non-zero return. */
@@ -149,18 +150,23 @@ int gdn_scan(const void *q, const void *k, int qk_dtype, const void *v, int v_dt
  *   conv_half:      NULL, or (pool) int32 (needs slots): the pool's conv state
  *                   is one (2 pool, K-1, C) array of two halves, passed as both
  *                   conv_state_in and conv_state_out; slot s holds its current
- *                   state at row s + pool * (conv_half[s] & 1) and row b rolls
- *                   it into the other half, row s + pool * (1 - (conv_half[s] & 1)).
- *                   Without conv_arrivals the bits are only read (gdn_pool_advance
- *                   flips them after the step).
+ *                   state at row s + pool * h(s) and row b rolls it into the
+ *                   other half, row s + pool * (1 - h(s)), where h(s) is
+ *                   conv_half[s] & 1 (XOR bit 16 of conv_arrivals[s] when the
+ *                   counters are given). Without conv_arrivals the bits are only
+ *                   read (gdn_pool_advance flips them after the step).
  *   row_strides:    NULL (dense inputs), or host int64[4]: the row strides, in
  *                   elements, of qkv, z, a and b (each at least its row width
  *                   C, Hv * Dv, Hv, Hv), so that slices of one stacked
  *                   projection output are read in place.
- *   conv_arrivals:  NULL, or (pool) int32 counters, all zero between calls (needs
- *                   conv_half): the step flips conv_half[slots[b]] itself (the
- *                   last of row b's workgroups to finish, counted here, flips
- *                   it and resets the count), so no gdn_pool_advance follows.
+ *   conv_arrivals:  NULL, or (pool) int32 counters, zero at first (needs
+ *                   conv_half and a power-of-two Hv): the step adds 2^16 to the
+ *                   counter of each decoded slot (in equal shares over the
+ *                   row's workgroups, so bit 16 flips when the last of them has
+ *                   read the half), which flips h(s), so no gdn_pool_advance
+ *                   follows. The bits below 16 are zero between calls. A pool
+ *                   whose steps pass the counters must pass them on every step
+ *                   (a step without them would read conv_half alone).
  *   A row whose slot falls outside the pool writes NaN to its output and
  *   touches no state.
  * Specialised for Dk = Dv = 128, K = 4; act_dtype in {F32, BF16}.

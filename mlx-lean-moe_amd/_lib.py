@@ -16,7 +16,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgdn.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 GDN_F32, GDN_BF16, GDN_F16 = 0, 1, 2
 GDN_EINVAL, GDN_EUNSUPPORTED = -1, -2

@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(const void* __re
 
 using namespace gdn;
 
-extern "C" int gdn_abi_version(void) { return 15; }
+extern "C" int gdn_abi_version(void) { return 16; }
 
 extern "C" const char* gdn_last_error(void) { return g_last_error; }
 

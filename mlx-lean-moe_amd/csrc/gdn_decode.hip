@@ -50,6 +50,9 @@
 namespace gdn {
 
 constexpr int kDecodeThreads = 256;
+// What a step adds to a decoded slot's conv_arrivals counter, in equal
+// shares over the row's workgroups (Hv * kSplit of them: a power of two).
+constexpr int kArrivalStep = 1 << 16;
 constexpr int kD = 128;   // Dk = Dv
 constexpr int kTaps = 4;  // conv kernel K
 
@@ -220,7 +223,9 @@ __global__ __launch_bounds__(kDecodeThreads * kSub) void decode_kernel(
     }
     int ci = sl, co = b;
     if (conv_half) {
-        const int hb = conv_half[sl] & 1;
+        // with the counters, bit 16 of the slot's counter flips once per
+        // step (kArrivalStep below): the half is the bit XOR that parity
+        const int hb = (conv_half[sl] ^ (arrivals ? arrivals[sl] >> 16 : 0)) & 1;
         ci = sl + pool * hb;
         co = sl + pool * (1 - hb);
     }
@@ -272,6 +277,17 @@ __global__ __launch_bounds__(kDecodeThreads * kSub) void decode_kernel(
         gate_beta = beta_of(bv, Act::code);
     }
     __syncthreads();
+    // Every thread has read the slot's half (its conv loads used it): thread
+    // 0 adds this workgroup's share of the step's 2^16 to the slot's counter,
+    // without waiting for the result. Bit 16 changes only with the last of
+    // the row's Hv * kSplit shares, after every workgroup of the row has
+    // read it, so the next launch reads the other half. (The form before,
+    // where the last workgroup to count in flipped the bit and reset the
+    // count, waited for the returned count and the flip: 0.7 us of a
+    // one-sequence step, ~2 us at B=64.)
+    if (arrivals && tid == 0)
+        __hip_atomic_fetch_add(&arrivals[sl], kArrivalStep / (Hv * kSplit), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     if (wg < 2) {
         // rms_norm(x, 1e-6) rounded once from its exact value: the sum of
         // squares (exact in double for activation-dtype inputs), the
@@ -318,13 +334,6 @@ __global__ __launch_bounds__(kDecodeThreads * kSub) void decode_kernel(
         else ys[row] = g * tot + delta_pair * kq;
     }
     __syncthreads();
-    // Every thread has read the slot's half bit (its conv loads used it). The
-    // last of the row's Hv * kSplit workgroups to get here flips it and resets
-    // the count, so the next launch reads the half this one wrote.
-    if (arrivals && tid == 0 && atomicAdd(&arrivals[sl], 1) == Hv * kSplit - 1) {
-        atomicXor(&conv_half[sl], 1);
-        atomicExch(&arrivals[sl], 0);
-    }
     // H. update and store the tile.
     float4* So = reinterpret_cast<float4*>(S_out + sh * kD * kD);
 #pragma unroll
@@ -384,6 +393,9 @@ extern "C" int gdn_decode_step(const void* qkv, const void* conv_state_in, void*
     GDN_REQUIRE(pool >= 1, "gdn_decode_step: bad pool size %d", pool);
     GDN_REQUIRE(!conv_half || slots, "gdn_decode_step: conv_half needs slots");
     GDN_REQUIRE(!conv_arrivals || conv_half, "gdn_decode_step: conv_arrivals needs conv_half");
+    if (conv_arrivals && ((Hv & (Hv - 1)) || Hv > kArrivalStep / 16))
+        return fail(GDN_EUNSUPPORTED, "gdn_decode_step: conv_arrivals needs a power-of-two Hv up to %d (got %d)",
+                    kArrivalStep / 16, Hv);
     const int64_t C = 2LL * Hk * kD + int64_t(Hv) * kD;
     const int64_t row_bytes = (kTaps - 1) * C * dtype_size(act_dtype);
     // with conv_half both conv pointers are the pool's two-half array (a

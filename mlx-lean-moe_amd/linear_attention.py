@@ -300,9 +300,10 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
     state at row ``s + P * conv_half[s]`` and rolls it into the other half,
     so nothing is left to copy back (``conv_out`` must be ``conv_state`` or
     None). The bits are read, not flipped (:meth:`RecurrentStatePool.advance`
-    flips them after the step), unless ``conv_arrivals`` is given as well:
-    the pool's ``P`` int32 counters, zero between steps, with which the
-    kernel flips the decoded slots' bits itself. ``slots`` and ``conv_half`` given as host
+    flips them after the step), unless ``conv_arrivals`` is given as well
+    (power-of-two ``Hv``): the pool's ``P`` int32 counters, to which the
+    kernel adds 2^16 per decoded slot, flipping its half (the bit XOR bit 16
+    of the counter). ``slots`` and ``conv_half`` given as host
     sequences are checked on the host; given as int32 device tensors they
     are used as they are (no host round trip), and the caller guarantees the
     slots are distinct — the kernel itself still refuses slots outside the
@@ -337,6 +338,9 @@ def fused_decode_step(qkv, z, a, b, conv_state, ssm_state, conv_weight, A_log, d
         conv_rows = 2 * P
         conv_out = conv_state
     if conv_arrivals is not None:
+        Hv = dims.num_value_heads
+        if Hv & (Hv - 1):
+            raise ValueError(f"conv_arrivals needs a power-of-two number of value heads (got {Hv})")
         if half_t is None or half_t is not conv_half:
             raise ValueError("conv_arrivals needs conv_half as an int32 device tensor")
         if (not isinstance(conv_arrivals, torch.Tensor) or conv_arrivals.device != device
@@ -581,11 +585,13 @@ class Qwen3_5LinearAttention:
                              "activation dtype (float32 or bfloat16)")
         slot_list = list(range(rows)) if slots is None else check_slots(slots, rows, pool.batch)
         slot_t = pool.device_slots(slot_list)
+        # the kernel flips the slots' halves itself where Hv is a power of two
+        counted = d.num_value_heads & (d.num_value_heads - 1) == 0
         out, _, _ = fused_decode_step(
             qkv, z, a, b, pool.conv_buf, pool.ssm_state, self.conv1d_weight, self.A_log,
             self.dt_bias, self.norm_weight, self.rms_norm_eps, d, slots=slot_t,
-            conv_half=pool.conv_half_dev, conv_arrivals=pool.conv_arrivals)
-        pool.advance(slot_list, device_flipped=True)
+            conv_half=pool.conv_half_dev, conv_arrivals=pool.conv_arrivals if counted else None)
+        pool.advance(slot_list, slot_t, device_flipped=counted)
         return self._proj(out.reshape(rows, d.value_dim), self.out_proj, residual)
 
 

@@ -33,6 +33,11 @@ class RecurrentCache:
     def state(self) -> tuple[torch.Tensor, torch.Tensor]:
         return self.conv_state, self.ssm_state
 
+    def device_halves(self) -> torch.Tensor:
+        """The slots' current halves as the decode kernel reads them: the
+        device bit, XOR bit 16 of the slot's counter."""
+        return (self.conv_half_dev ^ (self.conv_arrivals >> 16)) & 1
+
     def update(self, conv_state: torch.Tensor, ssm_state: torch.Tensor, advance: int) -> None:
         self.conv_state = conv_state
         self.ssm_state = ssm_state
@@ -49,10 +54,12 @@ class RecurrentStatePool:
     slot ``s`` currently lives in row ``s + B * conv_half[s]``; a decode reads
     that row and writes the rolled state into the slot's other half, then
     the slot's half flips (no copy, and slots decode independently). The
-    bits live on the device (``conv_half_dev``, read by the decode kernel,
-    which also flips them with the help of the zeroed ``conv_arrivals``
-    counters, or flipped by ``advance``) with a host copy (``conv_half``)
-    for host-side reads."""
+    bits live on the device (``conv_half_dev``, read by the decode kernel, or
+    flipped by ``advance``) with a host copy (``conv_half``) for host-side
+    reads. A decode step given the ``conv_arrivals`` counters flips a slot's
+    half itself: it adds 2^16 to the slot's counter, and the device half is
+    the bit XOR bit 16 of the counter (:meth:`device_halves`); a pool's steps
+    then pass the counters every time."""
 
     def __init__(self, batch: int, conv_kernel_dim: int, conv_dim: int, num_value_heads: int,
                  value_head_dim: int, key_head_dim: int, dtype: torch.dtype = torch.bfloat16,
@@ -69,6 +76,7 @@ class RecurrentStatePool:
         # NumPy views of the two host arrays: a decode step's bookkeeping
         # costs ~1 us through them (a torch CPU index op costs several)
         self._half_np, self._size_np = self.conv_half.numpy(), self.size.numpy()
+        self._counted = False  # a step has flipped halves through conv_arrivals
 
     @property
     def batch(self) -> int:
@@ -84,6 +92,11 @@ class RecurrentStatePool:
 
     def state(self) -> tuple[torch.Tensor, torch.Tensor]:
         return self.conv_state, self.ssm_state
+
+    def device_halves(self) -> torch.Tensor:
+        """The slots' current halves as the decode kernel reads them: the
+        device bit, XOR bit 16 of the slot's counter."""
+        return (self.conv_half_dev ^ (self.conv_arrivals >> 16)) & 1
 
     def device_slots(self, slots: list[int]) -> torch.Tensor:
         """``slots`` as an int32 device array, kept per active set (a serving
@@ -102,8 +115,15 @@ class RecurrentStatePool:
         """After a decode of ``slots`` (distinct; ``slot_t`` the same as an
         int32 device array, if the caller has it): their conv state now lives
         in the other half, and each holds one more token. ``device_flipped``:
-        the decode kernel has flipped the device bits already (it was given
-        ``conv_arrivals``); only the host copy and sizes change."""
+        the decode kernel has flipped the halves already (it was given
+        ``conv_arrivals``); only the host copy and sizes change. Once a step
+        has, the bits alone no longer give a slot's half, so flipping them
+        here instead is refused."""
+        if device_flipped:
+            self._counted = True
+        elif self._counted:
+            raise ValueError("this pool's decode steps flip the halves through conv_arrivals; "
+                             "pass them on every step (advance(..., device_flipped=True))")
         self.flip_host(np.asarray(slots, dtype=np.int64))
         if device_flipped:
             return

@@ -76,3 +76,15 @@ def assert_within_bf16_ulps(got, ref, ulps: int = 1) -> None:
     bad = err > tol
     assert not bad.any(), (f"{int(bad.sum())} of {bad.size} values beyond {ulps} bf16 ulp; "
                            f"worst {err.max():.3g} at |ref| {np.abs(ref).flat[err.argmax()]:.3g}")
+
+
+def device_halves(half, arrivals):
+    """The conv halves a decode step reads from a pool's bits and arrival
+    counters: the bit XOR bit 16 of the counter."""
+    return (half ^ (arrivals >> 16)) & 1
+
+
+def counters_settled(arrivals) -> bool:
+    """Between steps the counters' bits below 16 are zero (every workgroup
+    of every step added its share)."""
+    return not bool((arrivals & 0xFFFF).any())

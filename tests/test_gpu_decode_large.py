@@ -22,7 +22,7 @@ import torch
 
 import mlx_lean_moe_amd as gdn
 from oracle import cref
-from tests.helpers import assert_bf16_out_close, layer_params
+from tests.helpers import assert_bf16_out_close, counters_settled, device_halves, layer_params
 
 pytestmark = pytest.mark.gpu
 
@@ -158,17 +158,17 @@ def test_decode_hv64_pool_with_half_bits_and_arrivals_matches_c_oracle(gpu):
             x["qkv"], conv_ref, conv_w, x["a"], x["b"], A_log, dt_bias, state_ref, x["z"], norm_w,
             1e-6, (Hk, Hv, D, D), True)
         assert_bf16_out_close(out.float().cpu().numpy(), out_ref)
-        bits = half.cpu().numpy()
+        bits = device_halves(half, arrivals).cpu().numpy()
         expect_bits = bits0.copy()
         expect_bits[idx] ^= (step + 1) & 1
         np.testing.assert_array_equal(bits, expect_bits)
-        assert not arrivals.any()
+        assert counters_settled(arrivals)
         rows = torch.from_numpy(idx + P * bits[idx]).to(gpu)
         np.testing.assert_array_equal(conv_buf[rows].float().cpu().numpy(), conv_ref)
         assert _state_rel_err(state_dev[torch.from_numpy(idx).to(gpu)], state_ref) < 1e-3, step
     keep = torch.from_numpy(untouched).to(gpu)
     assert torch.equal(state_dev[keep], _dev(state0[untouched], gpu))
-    np.testing.assert_array_equal(half.cpu().numpy()[untouched], bits0[untouched])
+    np.testing.assert_array_equal(device_halves(half, arrivals).cpu().numpy()[untouched], bits0[untouched])
 
 
 def test_decode_b64_hv32_256_chained_steps_match_c_oracle(gpu):

@@ -23,7 +23,7 @@ import torch
 
 import mlx_lean_moe_amd as gdn
 from oracle import cref
-from tests.helpers import assert_bf16_out_close, layer_params, max_rel
+from tests.helpers import assert_bf16_out_close, counters_settled, device_halves, layer_params, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -149,9 +149,9 @@ def test_split_decode_on_a_pool_flips_each_slot_once_per_step(gpu):
         ref_conv[idx], ref_state[idx] = nc, ns
         flips[idx] ^= 1
         assert_bf16_out_close(out.float().cpu().numpy(), out_ref)
-        bits = half.cpu().numpy()
+        bits = device_halves(half, arrivals).cpu().numpy()
         np.testing.assert_array_equal(bits, bits0 ^ flips)
-        assert not arrivals.any()
+        assert counters_settled(arrivals)
         cur = torch.from_numpy(np.arange(P) + P * bits).to(gpu)
         np.testing.assert_array_equal(conv_buf[cur].float().cpu().numpy(), ref_conv)
         assert max_rel(state.cpu().numpy(), ref_state) < 1e-5, step
@@ -205,8 +205,8 @@ def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu, act):
             conv_buf, pool, *params[:3], None, 1e-6, DIMS, slots=slots, conv_half=half,
             conv_arrivals=arrivals, y_dtype=torch.bfloat16)
         assert torch.equal(out, outs[step]), step
-        np.testing.assert_array_equal(half.cpu().numpy(), bits0 ^ ((step + 1) & 1))
-        assert not arrivals.any()
-    cur = torch.from_numpy(slot_of + P * half.cpu().numpy()[slot_of]).to(gpu)
+        np.testing.assert_array_equal(device_halves(half, arrivals).cpu().numpy(), bits0 ^ ((step + 1) & 1))
+        assert counters_settled(arrivals)
+    cur = torch.from_numpy(slot_of + P * device_halves(half, arrivals).cpu().numpy()[slot_of]).to(gpu)
     assert torch.equal(conv_buf[cur], cv_norm)
     assert torch.equal(pool[torch.from_numpy(slot_of).to(gpu)], st_norm)

@@ -12,7 +12,7 @@ import torch
 
 import mlx_lean_moe_amd as gdn
 from mlx_lean_moe_amd import _lib
-from tests.helpers import layer_inputs, layer_params
+from tests.helpers import counters_settled, device_halves, layer_inputs, layer_params
 from tests.test_gpu_layer import HIDDEN, _build
 
 pytestmark = pytest.mark.gpu
@@ -86,8 +86,9 @@ def test_conv_half_rolls_into_the_other_half_without_a_copy(gpu):
         assert torch.equal(buf[r], written[r] if r in written else before[r]), r
     assert torch.equal(c["state"][idx], ref_state)
     assert half.tolist() == bits
-    # with the arrival counters the kernel flips the decoded slots' bits, and
-    # a second step reads the halves the first one wrote
+    # with the arrival counters the kernel flips the decoded slots' halves
+    # (2^16 added to their counters, bit 16 the parity; the bits are only
+    # read), and a second step reads the halves the first one wrote
     half[4] = 1  # the step above left slot 4 in half 1 and slot 1 in half 0
     half[1] = 0
     arrivals = torch.zeros(P, dtype=torch.int32, device=gpu)
@@ -95,7 +96,8 @@ def test_conv_half_rolls_into_the_other_half_without_a_copy(gpu):
     out2, _, _ = gdn.fused_decode_step(
         c["qkv"], c["z"], c["a"], c["b"], buf, state2, c["conv_w"], c["A_log"], c["dt_bias"],
         c["norm_w"], 1e-6, DIMS, slots=slots, conv_half=half, conv_arrivals=arrivals)
-    assert half.tolist() == bits and not arrivals.any()
+    assert half.tolist() != bits and device_halves(half, arrivals).tolist() == bits
+    assert arrivals.tolist() == [65536 if i in (4, 1) else 0 for i in range(P)]
     ref2 = gdn.fused_decode_step(c["qkv"], c["z"], c["a"], c["b"], ref_conv.clone(), ref_state.clone(),
                                  c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"], 1e-6, DIMS)
     assert torch.equal(out2, ref2[0])
@@ -197,16 +199,43 @@ def test_pooled_decode_after_chunked_prefill_matches_per_sequence_calls(gpu):
         out = layer.decode_batch(x, pool, slots=active)
         ref = torch.stack([layer(x[i], caches[slots.index(s)]) for i, s in enumerate(active)])
         torch.testing.assert_close(out.float(), ref.float(), rtol=0, atol=0)
-        # the decode kernel flipped the decoded slots' bits itself and left
-        # its arrival counters at zero
-        assert pool.conv_half_dev.cpu().tolist() == pool.conv_half.tolist()
-        assert not pool.conv_arrivals.any()
+        # the decode kernel flipped the decoded slots' halves itself (its
+        # counters' bit 16) and left the counters' low bits at zero
+        assert pool.device_halves().cpu().tolist() == pool.conv_half.tolist()
+        assert counters_settled(pool.conv_arrivals)
     for slot, cache in zip(slots, caches):
         torch.testing.assert_close(pool.ssm_state[slot], cache.ssm_state, rtol=0, atol=0)
         torch.testing.assert_close(pool.conv_state[slot], cache.conv_state, rtol=0, atol=0)
         assert int(pool.size[slot]) == cache.size
     for free in (0, 3, 5):
         assert not pool.ssm_state[free].any() and not pool.conv_state[free].any()
+
+
+def test_pooled_decode_with_non_power_of_two_heads(gpu):
+    """Hv = 6 value heads: the kernel cannot split a step's 2^16 into equal
+    shares, so decode_batch leaves the counters alone and flips the bits
+    with gdn_pool_advance; the steps still equal per-sequence calls."""
+
+    dims = gdn.LinearAttentionDims(2, 6, 128, 128, 4)
+    layer, _ = _build(9, dims, gpu, dtype=torch.bfloat16)
+    rng = np.random.default_rng(109)
+    pool = gdn.RecurrentStatePool(4, 4, dims.conv_dim, dims.num_value_heads, 128, 128,
+                                  dtype=torch.bfloat16, device=gpu)
+    slots = [3, 0]
+    caches = [layer.new_cache(torch.bfloat16) for _ in slots]
+    for slot, cache in zip(slots, caches):
+        layer(torch.tensor(rng.standard_normal((3, HIDDEN)), dtype=torch.bfloat16, device=gpu), cache)
+        pool.load(slot, cache)
+    for _ in range(3):
+        x = torch.tensor(rng.standard_normal((2, HIDDEN)), dtype=torch.bfloat16, device=gpu)
+        out = layer.decode_batch(x, pool, slots=slots)
+        ref = torch.stack([layer(x[i], caches[i]) for i in range(2)])
+        torch.testing.assert_close(out.float(), ref.float(), rtol=0, atol=0)
+        assert pool.conv_half_dev.cpu().tolist() == pool.conv_half.tolist()
+        assert not pool.conv_arrivals.any()
+    for slot, cache in zip(slots, caches):
+        torch.testing.assert_close(pool.conv_state[slot], cache.conv_state, rtol=0, atol=0)
+        torch.testing.assert_close(pool.ssm_state[slot], cache.ssm_state, rtol=0, atol=0)
 
 
 def test_decode_graph_replays_equal_eager_decode(gpu):
@@ -239,8 +268,9 @@ def test_decode_graph_replays_equal_eager_decode(gpu):
     torch.testing.assert_close(graphed.ssm_state, eager.ssm_state, rtol=0, atol=0)
     torch.testing.assert_close(graphed.conv_state, eager.conv_state, rtol=0, atol=0)
     assert torch.equal(graphed.size, eager.size) and torch.equal(graphed.conv_half, eager.conv_half)
-    assert torch.equal(graphed.conv_half_dev, eager.conv_half_dev)
-    assert graphed.conv_half_dev.cpu().tolist() == graphed.conv_half.tolist()
+    assert torch.equal(graphed.device_halves(), eager.device_halves())
+    assert graphed.device_halves().cpu().tolist() == graphed.conv_half.tolist()
+    assert counters_settled(graphed.conv_arrivals)
 
 
 def test_decode_graph_outlives_the_pools_slot_cache(gpu):

@@ -182,6 +182,14 @@ def test_pool_host_bookkeeping_flips_bits_and_sizes():
     assert pool.conv_half.tolist() == [0, 0, 1, 0, 1, 0] and pool.size.tolist() == [0, 2, 1, 0, 1, 0]
     pool.flip_host(np.array([1, 2]), tokens=-1)
     assert pool.conv_half.tolist() == [0, 1, 0, 0, 1, 0] and pool.size.tolist() == [0, 1, 0, 0, 1, 0]
+    # once a step has flipped halves through the arrival counters, flipping
+    # the bits alone (gdn_pool_advance) is refused: it would read them wrong
+    pool._counted = False
+    pool.advance([3], device_flipped=True)
+    assert pool.conv_half.tolist() == [0, 1, 0, 1, 1, 0]
+    with pytest.raises(ValueError, match="conv_arrivals"):
+        pool.advance([3])
+    assert pool.conv_half.tolist() == [0, 1, 0, 1, 1, 0]
 
 
 @pytest.mark.parametrize("bad", ["short", "long", "start", "end", "order", "uneven"])
