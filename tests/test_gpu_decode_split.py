@@ -165,8 +165,8 @@ def test_pair_split_at_many_heads_matches_one_workgroup_per_head(gpu, act):
     and ssm state equal the same steps taken with the gated norm (one
     workgroup per head at every B), bit for bit. Then the same steps through
     a 64-slot pool in reverse slot order, the kernel flipping each slot's conv
-    half bit once per step (2 * Hv arrivals per slot): the same outputs and
-    states, and the arrival counters back at zero."""
+    half once per step (2 * Hv shares of 2^16 per slot): the same outputs and
+    states, and the counters' bits below 16 back at zero."""
 
     bf16 = act == "bf16"
     B, adt = 64, torch.bfloat16 if bf16 else torch.float32
