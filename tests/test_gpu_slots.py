@@ -117,6 +117,39 @@ def test_conv_half_rolls_into_the_other_half_without_a_copy(gpu):
                               conv_half=bits[:2])
 
 
+def test_arrival_counters_carry_across_the_sign_and_wrap(gpu):
+    """The counters' bit 16 keeps flipping once per step where a count
+    crosses 2^31 (int32 sign) and wraps at 2^32: two chained steps read and
+    write the halves the shares select, as the dense reference steps do."""
+
+    P, slots = 4, [1, 2]
+    c = _pool_case(17, P, len(slots), torch.bfloat16, gpu)
+    # bits 0; counters with bit 16 set: both slots currently in half 1
+    half = torch.zeros(P, dtype=torch.int32, device=gpu)
+    arrivals = torch.tensor([0, 0x7FFF0000, -0x10000, 0], dtype=torch.int32, device=gpu)
+    buf = torch.zeros((2 * P,) + tuple(c["conv"].shape[1:]), dtype=c["conv"].dtype, device=gpu)
+    for s_ in slots:
+        buf[P + s_] = c["conv"][s_]
+    idx = torch.tensor(slots, device=gpu)
+    conv_g, state_g = c["conv"][idx].clone(), c["state"][idx].clone()
+    state = c["state"].clone()
+    for step in range(2):
+        ref_out, conv_g, state_g = gdn.fused_decode_step(
+            c["qkv"], c["z"], c["a"], c["b"], conv_g, state_g, c["conv_w"], c["A_log"], c["dt_bias"],
+            c["norm_w"], 1e-6, DIMS)
+        out, _, _ = gdn.fused_decode_step(
+            c["qkv"], c["z"], c["a"], c["b"], buf, state, c["conv_w"], c["A_log"], c["dt_bias"],
+            c["norm_w"], 1e-6, DIMS, slots=slots, conv_half=half, conv_arrivals=arrivals)
+        assert torch.equal(out, ref_out), step
+        now = device_halves(half, arrivals).tolist()
+        assert now == [0, step % 2, step % 2, 0], (step, now)
+        for i, s_ in enumerate(slots):
+            assert torch.equal(buf[s_ + P * now[s_]], conv_g[i]), (step, s_)
+        assert torch.equal(state[idx], state_g)
+    assert arrivals.tolist() == [0, 0x7FFF0000 + 2 * 0x10000 - 2 ** 32, 0x10000, 0]
+    assert half.tolist() == [0] * P
+
+
 def test_pool_advance_flips_the_bits_of_the_decoded_slots(gpu):
     pool = gdn.RecurrentStatePool(300, 4, DIMS.conv_dim, DIMS.num_value_heads, 128, 128,
                                   dtype=torch.bfloat16, device=gpu)
