@@ -67,6 +67,11 @@ def test_invalid_arguments_return_einval_without_launching():
                                  128, 128, 4, 1, slots, 4, slots, (ctypes.c_int64 * 4)(*strides), None,
                                  None)
         assert rc == _lib.GDN_EINVAL and what in _err(lib), (what, _err(lib))
+    # the kernel flips the halves through conv_arrivals only where the step's
+    # 2^16 splits evenly over the row's workgroups: a power-of-two Hv
+    rc = lib.gdn_decode_step(fake[0], fake[1], fake[1], *fake[3:12], 1e-6, fake[11], 0, 1, 2, 6, 128, 128,
+                             4, 1, slots, 4, slots, None, slots, None)
+    assert rc == _lib.GDN_EUNSUPPORTED and "power-of-two" in _err(lib), _err(lib)
     # a gate row stride below Hv
     rc = lib.gdn_prefill_chunked(*fake[:3], 1, *fake[3:5], 1, 3, *fake[5:7], 0, None, fake[7], fake[8], 0,
                                  None, 1, 64, 2, 4, 128, 128, fake[9], 1 << 30, None)
