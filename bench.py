@@ -1191,7 +1191,7 @@ def main(argv=None):
                           **({"sequential_scan_us": r["sequential_scan_us"]} if f32 else {})}))
         return 0
 
-    raise SystemExit(f"workload {args.workload} is not available in this build")
+    raise SystemExit(f"unknown workload {args.workload}")
 
 
 if __name__ == "__main__":
