@@ -804,14 +804,17 @@ GDN_DEV int kr_off(int r, int G) { return r * kHD + ((G ^ kswz(r)) << 3); }
 
 // Output waves: staged operands into LDS, in the layouts the state waves
 // read them with (and, for float32 input, their own Q rows).
-// The 8 floats whose bits a and b hold (4 each) as bf16 hi + lo.
+// The 8 floats whose bits a and b hold (4 each) as bf16 hi + lo, split in
+// pairs (split_bf16x2: the same bits as split_bf16 on each).
 GDN_DEV void split8_bits(const bf16x8& a, const bf16x8& b, bf16x8& hi, bf16x8& lo) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
-    u16x8 h, r;
+    u32x4 h, r;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        uint16_t hj, rj;
-        split_bf16(j < 4 ? fa[j] : fb[j - 4], hj, rj);
+    for (int j = 0; j < 4; ++j) {
+        const float x0 = j < 2 ? fa[2 * j] : fb[2 * j - 4], x1 = j < 2 ? fa[2 * j + 1] : fb[2 * j - 3];
+        uint32_t hj, rj;
+        split_bf16x2(x0, x1, hj, rj);
         h[j] = hj;
         r[j] = rj;
     }
@@ -839,14 +842,11 @@ template <bool kF32>
 GDN_DEV void stage_v(const StagedOperands& op, StatePassLds<kF32>& sm, int w, int l) {
     const int o = (16 * w + (l >> 2)) * kSliceRows + 4 * (l & 3);
     if constexpr (kF32) {
-        const float x[4] = {__uint_as_float(op.v[0]), __uint_as_float(op.v[1]), __uint_as_float(op.vl[0]),
-                            __uint_as_float(op.vl[1])};
-        uint16_t h[4], r[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) split_bf16(x[j], h[j], r[j]);
-        const uint2 ph = pack4(h), pr = pack4(r);
-        *reinterpret_cast<u32x2*>(sm.Vs + o) = u32x2{ph.x, ph.y};
-        *reinterpret_cast<u32x2*>(sm.Vs_lo + o) = u32x2{pr.x, pr.y};
+        uint32_t h0, r0, h1, r1;
+        split_bf16x2(__uint_as_float(op.v[0]), __uint_as_float(op.v[1]), h0, r0);
+        split_bf16x2(__uint_as_float(op.vl[0]), __uint_as_float(op.vl[1]), h1, r1);
+        *reinterpret_cast<u32x2*>(sm.Vs + o) = u32x2{h0, h1};
+        *reinterpret_cast<u32x2*>(sm.Vs_lo + o) = u32x2{r0, r1};
     } else {
         *reinterpret_cast<u32x2*>(sm.Vs + o) = op.v;
     }
