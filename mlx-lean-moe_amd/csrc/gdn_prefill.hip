@@ -281,6 +281,17 @@ struct ConvIn {
 // the raw projection rows and a conv state in bf16 or float32.
 constexpr int kInBF16 = 0, kInF32 = 1, kInConvBF16 = 2, kInConvF32 = 3;
 
+// Workgroup id -> (chunk-and-key-head item, first value head e0 of the
+// key head's group): a workgroup takes kHeads consecutive value heads of one
+// key head, which share the chunk's K K^T and K Q^T; ids go over 8 items,
+// then over the head sets, then over the next 8 items.
+template <int kHeads>
+GDN_DEV void chunk_item(int id, int r, int& item, int& e0) {
+    const int rh = r / kHeads;
+    e0 = ((id >> 3) % rh) * kHeads;
+    item = (id / (8 * rh)) * 8 + (id & 7);
+}
+
 // kInF32: q and k are float32, entering the MFMAs as bf16 high parts plus
 // residuals (hi.hi + hi.lo + lo.hi), with two more LDS tiles for the
 // residuals; kInBF16: bf16, used as they are. kInConv*: each workgroup runs
@@ -290,8 +301,9 @@ constexpr int kInBF16 = 0, kInF32 = 1, kInConvBF16 = 2, kInConvF32 = 3;
 // its rows with the previous three in registers (a run's first rows take
 // them from its conv state) into the K / Q tiles; the first value head of
 // each key head also stores q and k for the state pass (v: conv_v_block).
-// `id` is the workgroup's index in the (chunk, head) order below.
-template <int kIn>
+// `id` is the workgroup's index in chunk_item's order. The workgroup records
+// kHeads value heads in turn from one set of products.
+template <int kIn, int kHeads>
 GDN_DEV void prefill_chunk_body(
     const void* __restrict__ q_in, const void* __restrict__ k_in, const void* __restrict__ ga,
     const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
@@ -313,24 +325,28 @@ GDN_DEV void prefill_chunk_body(
 
     const int r = Hv / Hk;
     if (id < 0) id = blockIdx.x;
-    const int e = (id >> 3) % r;
-    const int item = (id / (8 * r)) * 8 + (id & 7);  // (chunk, key head)
-    const int g = item / Hk, hk = item % Hk, hv = hk * r + e;
+    int item, e0;  // (chunk, key head), first value head of the set
+    chunk_item<kHeads>(id, r, item, e0);
+    const int g = item / Hk, hk = item % Hk, hv0 = hk * r + e0;
     if (g >= rl.total()) return;
     const ChunkPos pos = locate_chunk(rl, g);
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-    char* rec = records + (int64_t(g) * Hv + hv) * kRecBytes;
+    auto rec_of = [&](int h) { return records + (int64_t(g) * Hv + hv0 + h) * kRecBytes; };
 
     // The gate inputs of wave 0 (lane = token) go out first, as raw words
     // decoded where they are used, so that the gates' prefix sum does not
     // wait behind the K and Q loads.
-    uint32_t ga_raw = 0, gb_raw = 0;
+    uint32_t ga_raw[kHeads] = {}, gb_raw[kHeads] = {};
     if (w == 0) {
         const int lc = l < pos.len ? l : pos.len - 1;
-        const int64_t i = (pos.t0 + lc) * gate_stride + hv;
-        ga_raw = gate_mode == 1 || gb_dtype == GDN_F32 ? static_cast<const uint32_t*>(ga)[i]
-                                                       : static_cast<const uint16_t*>(ga)[i];
-        gb_raw = gb_dtype == GDN_F32 ? static_cast<const uint32_t*>(gb)[i] : static_cast<const uint16_t*>(gb)[i];
+#pragma unroll
+        for (int h = 0; h < kHeads; ++h) {
+            const int64_t i = (pos.t0 + lc) * gate_stride + hv0 + h;
+            ga_raw[h] = gate_mode == 1 || gb_dtype == GDN_F32 ? static_cast<const uint32_t*>(ga)[i]
+                                                              : static_cast<const uint16_t*>(ga)[i];
+            gb_raw[h] = gb_dtype == GDN_F32 ? static_cast<const uint32_t*>(gb)[i]
+                                            : static_cast<const uint16_t*>(gb)[i];
+        }
     }
 
     // K and Q of the chunk: every load issued before the first LDS store
@@ -373,16 +389,18 @@ GDN_DEV void prefill_chunk_body(
             }
         }
     }
-    // Gates (wave 0, lane = token): l2 = inclusive prefix sum of log2 g
-    // (exp2 of differences gives the decays).
-    if (w == 0) {
+    // Gates of value head hv0 + h (wave 0, lane = token): l2 = inclusive
+    // prefix sum of log2 g (exp2 of differences gives the decays).
+    auto gates = [&](int h) {
+        const int hv = hv0 + h;
+        char* rec = rec_of(h);
         float lg, beta;
-        const float gbv = raw_to_f32(gb_raw, gb_dtype);
+        const float gbv = raw_to_f32(gb_raw[h], gb_dtype);
         if (gate_mode == 0) {
-            lg = log_forget_gate(raw_to_f32(ga_raw, gb_dtype), A_log[hv], dt_bias[hv]);
+            lg = log_forget_gate(raw_to_f32(ga_raw[h], gb_dtype), A_log[hv], dt_bias[hv]);
             beta = beta_of(gbv, gb_dtype);
         } else {
-            const float gv = __uint_as_float(ga_raw);
+            const float gv = __uint_as_float(ga_raw[h]);
             lg = gv > 0.f ? logf(gv) : kLogGateFloor;
             beta = gbv;
         }
@@ -398,7 +416,8 @@ GDN_DEV void prefill_chunk_body(
         const float lC = __shfl(lg, kChunk - 1, kWave);
         reinterpret_cast<float*>(rec + kRecEl)[l] = exp2f(lg);
         reinterpret_cast<float*>(rec + kRecEd)[l] = exp2f(lC - lg);
-    }
+    };
+    if (w == 0) gates(0);
     if constexpr (kConv) {
         // conv, SiLU and the scaled norm of rows 8 crg .. 8 crg + 7 into the
         // tile; the first value head of the key head also stores them
@@ -417,7 +436,7 @@ GDN_DEV void prefill_chunk_body(
             for (int e = 0; e < 8; ++e) o[e] = sc * n[e];
             const uint4 p = pack8(o);
             *reinterpret_cast<uint4*>(tile + row * kKS + cseg * 8) = row < pos.len ? p : make_uint4(0, 0, 0, 0);
-            if (e == 0 && row < pos.len) *reinterpret_cast<uint4*>(out + (pos.t0 + row) * Hk * kHD) = p;
+            if (e0 == 0 && row < pos.len) *reinterpret_cast<uint4*>(out + (pos.t0 + row) * Hk * kHD) = p;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 win[0][j] = win[1][j];
@@ -481,44 +500,53 @@ GDN_DEV void prefill_chunk_body(
     }
     __syncthreads();  // K/Q tiles are dead from here on
 
-    // A (row i, column j) into LDS and P (query j, key i) straight from the
-    // accumulators into its fragments: lane (l%16, l/16) of wave w holds keys
-    // 16w + 4(l/16) .. +3 of query 16jt + l%16, which is half of the 16-byte
-    // entry (query row l%16, keys 8g .. 8g+7) of fragment (jt, w/2), with
-    // g = 2(w%2) + (l/16)/2, half (l/16)%2. Fragments above the diagonal
-    // (jt < 2 <= w) are skipped.
-    const float4 li = *reinterpret_cast<const float4*>(l2_sh + 16 * w + 4 * lq);
-    const float4 bi = *reinterpret_cast<const float4*>(beta_sh + 16 * w + 4 * lq);
-    const float l2i[4] = {li.x, li.y, li.z, li.w}, betai[4] = {bi.x, bi.y, bi.z, bi.w};
-    uint16_t* p_hi = reinterpret_cast<uint16_t*>(rec + kRecPHi);
-    uint16_t* p_lo = reinterpret_cast<uint16_t*>(rec + kRecPLo);
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        const int j = 16 * jt + lr;
-        const float l2j = l2_sh[j];
-        uint16_t ph[4], pl[4];
+    for (int h = 0; h < kHeads; ++h) {
+        if (h > 0) {
+            __syncthreads();  // the previous head's readers of l2_sh, beta_sh, As and Ts are done
+            if (w == 0) gates(h);
+            __syncthreads();
+        }
+        char* rec = rec_of(h);
+        // A (row i, column j) into LDS and P (query j, key i) straight from the
+        // accumulators into its fragments: lane (l%16, l/16) of wave w holds keys
+        // 16w + 4(l/16) .. +3 of query 16jt + l%16, which is half of the 16-byte
+        // entry (query row l%16, keys 8g .. 8g+7) of fragment (jt, w/2), with
+        // g = 2(w%2) + (l/16)/2, half (l/16)%2. Fragments above the diagonal
+        // (jt < 2 <= w) are skipped.
+        const float4 li = *reinterpret_cast<const float4*>(l2_sh + 16 * w + 4 * lq);
+        const float4 bi = *reinterpret_cast<const float4*>(beta_sh + 16 * w + 4 * lq);
+        const float l2i[4] = {li.x, li.y, li.z, li.w}, betai[4] = {bi.x, bi.y, bi.z, bi.w};
+        uint16_t* p_hi = reinterpret_cast<uint16_t*>(rec + kRecPHi);
+        uint16_t* p_lo = reinterpret_cast<uint16_t*>(rec + kRecPLo);
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            const int i = 16 * w + 4 * lq + ii;
-            const float d = l2i[ii] - l2j;  // <= 0 for i >= j, >= 0 for i <= j
-            const float dki = exp2f(i > j ? d : -d);
-            As[i * kFS + j] = i > j ? betai[ii] * kk[jt][ii] * dki : 0.f;
-            split_bf16(i <= j ? kq[jt][ii] * dki : 0.f, ph[ii], pl[ii]);
+        for (int jt = 0; jt < 4; ++jt) {
+            const int j = 16 * jt + lr;
+            const float l2j = l2_sh[j];
+            uint16_t ph[4], pl[4];
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = 16 * w + 4 * lq + ii;
+                const float d = l2i[ii] - l2j;  // <= 0 for i >= j, >= 0 for i <= j
+                const float dki = exp2f(i > j ? d : -d);
+                As[i * kFS + j] = i > j ? betai[ii] * kk[jt][ii] * dki : 0.f;
+                split_bf16(i <= j ? kq[jt][ii] * dki : 0.f, ph[ii], pl[ii]);
+            }
+            if (w < 2 || jt >= 2) {
+                const int f = 2 * jt + (w >> 1), ln = 16 * (2 * (w & 1) + (lq >> 1)) + lr;
+                const int off = (64 * f + ln) * 8 + 4 * (lq & 1);
+                *reinterpret_cast<uint2*>(p_hi + off) = pack4(ph);
+                *reinterpret_cast<uint2*>(p_lo + off) = pack4(pl);
+            }
         }
-        if (w < 2 || jt >= 2) {
-            const int f = 2 * jt + (w >> 1), ln = 16 * (2 * (w & 1) + (lq >> 1)) + lr;
-            const int off = (64 * f + ln) * 8 + 4 * (lq & 1);
-            *reinterpret_cast<uint2*>(p_hi + off) = pack4(ph);
-            *reinterpret_cast<uint2*>(p_lo + off) = pack4(pl);
-        }
+        __syncthreads();
+        if (w == 0) diag_inverse(As, Ts, l);  // T's diagonal blocks
+        __syncthreads();
+        offdiag_inverse(As, Ts, w, l);
+        // Tb = T diag(beta), split into bf16 hi + lo.
+        store_fragments(Ts, reinterpret_cast<uint16_t*>(rec + kRecTbHi),
+                        reinterpret_cast<uint16_t*>(rec + kRecTbLo), beta_sh, tid, 256);
     }
-    __syncthreads();
-    if (w == 0) diag_inverse(As, Ts, l);  // T's diagonal blocks
-    __syncthreads();
-    offdiag_inverse(As, Ts, w, l);
-    // Tb = T diag(beta), split into bf16 hi + lo.
-    store_fragments(Ts, reinterpret_cast<uint16_t*>(rec + kRecTbHi),
-                    reinterpret_cast<uint16_t*>(rec + kRecTbLo), beta_sh, tid, 256);
 }
 
 // The fused chunk pass's v part, done by each chunk workgroup after its
@@ -531,9 +559,8 @@ GDN_DEV void prefill_chunk_body(
 // channels of hv, and with the first value head the q and k channels of hk;
 // 48 pieces of 8 channels a group.
 template <int kConvDt>
-GDN_DEV void conv_v_block(RunLayout rl, const ConvIn& cv, int id, int Hk, int Hv) {
-    const int r = Hv / Hk, e = (id >> 3) % r;
-    const int item = (id / (8 * r)) * 8 + (id & 7);  // (chunk, key head)
+GDN_DEV void conv_v_block(RunLayout rl, const ConvIn& cv, int item, int e, int Hk, int Hv) {
+    const int r = Hv / Hk;
     const int g = item / Hk, hk = item % Hk, hv = hk * r + e;
     if (g >= rl.total()) return;
     const ChunkPos pos = locate_chunk(rl, g);
@@ -597,16 +624,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
     int Hk, int Hv) {
-    prefill_chunk_body<kInBF16>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
+    prefill_chunk_body<kInBF16, 1>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
                                 records, Hk, Hv);
 }
 
+template <int kHeads>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_chunk_f32_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ ga,
     const void* __restrict__ gb, int gb_dtype, int64_t gate_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int gate_mode, RunLayout rl, char* __restrict__ records,
     int Hk, int Hv) {
-    prefill_chunk_body<kInF32>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
+    prefill_chunk_body<kInF32, kHeads>(q, k, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl,
                                records, Hk, Hv);
 }
 
@@ -618,9 +646,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     const void* __restrict__ ga, const void* __restrict__ gb, int gb_dtype, int64_t gate_stride,
     const float* __restrict__ A_log, const float* __restrict__ dt_bias, RunLayout rl,
     char* __restrict__ records, int Hk, int Hv, ConvIn cv) {
-    prefill_chunk_body<kConvDt == GDN_F32 ? kInConvF32 : kInConvBF16>(
+    prefill_chunk_body<kConvDt == GDN_F32 ? kInConvF32 : kInConvBF16, 1>(
         nullptr, nullptr, ga, gb, gb_dtype, gate_stride, A_log, dt_bias, 0, rl, records, Hk, Hv, cv);
-    conv_v_block<kConvDt>(rl, cv, blockIdx.x, Hk, Hv);
+    int item, e;
+    chunk_item<1>(blockIdx.x, Hv / Hk, item, e);
+    conv_v_block<kConvDt>(rl, cv, item, e, Hk, Hv);
 }
 
 // The new conv state of each empty run (no chunk writes it): its old state,
@@ -1307,8 +1337,13 @@ extern "C" int gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     }
     const int64_t nchunks = chunks_bound(T_total, N);
     const int64_t items = (nchunks * Hk + 7) / 8 * 8;
-    hipLaunchKernelGGL(f32 ? prefill_chunk_f32_kernel : prefill_chunk_kernel,
-                       dim3(unsigned(items * (Hv / Hk))), dim3(256), 0, s, q, k, ga, gb,
+    // value heads per chunk workgroup: with float32 input two where a key
+    // head has an even number (with bf16 input the second head's products
+    // would spill)
+    const bool pairs = f32 && (Hv / Hk) % 2 == 0;
+    const dim3 cgrid(unsigned(items * (Hv / Hk) / (pairs ? 2 : 1)));
+    hipLaunchKernelGGL(f32 ? (pairs ? prefill_chunk_f32_kernel<2> : prefill_chunk_f32_kernel<1>) : prefill_chunk_kernel,
+                       cgrid, dim3(256), 0, s, q, k, ga, gb,
                        gb_dtype, gate_stride, A_log, dt_bias, gate_mode, rl, records, Hk, Hv);
     if (int rc = check_launch("gdn_prefill_chunked/chunk")) return rc;
     const dim3 sgrid(unsigned(int64_t(N) * Hv * kSlices));
