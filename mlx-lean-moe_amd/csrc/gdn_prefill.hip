@@ -258,12 +258,16 @@ GDN_DEV void offdiag_inverse(float* As, float* Ts, int w, int l) {
     __syncthreads();
 }
 
-// One workgroup per (chunk, value head). K K^T and K Q^T depend only on the
-// key head, but recomputing them per value head (32 MFMAs per wave) keeps
-// each workgroup small enough for several to share a CU. Workgroup ids go
-// round-robin over the 8 XCDs, so the r = Hv/Hk value heads of one
-// (chunk, key head) take ids 8 apart: same XCD, dispatched together, so all
-// but the first read that chunk's K and Q from the XCD's L2.
+// One workgroup per (chunk, value head), or with float32 input per (chunk,
+// two value heads of one key head). K K^T and K Q^T depend only on the key
+// head; with bf16 input recomputing them per value head (32 MFMAs per wave)
+// keeps each workgroup within the 128 registers that let four share a CU
+// (holding them for a second head spills), while the float32 products
+// (three MFMAs each, from split operands) are worth sharing at two
+// workgroups per CU. Workgroup ids go round-robin over the 8 XCDs, so the
+// workgroups of one (chunk, key head) take ids 8 apart: same XCD,
+// dispatched together, so all but the first read that chunk's K and Q from
+// the XCD's L2.
 //
 // The raw projection rows and conv parameters of the fused chunk pass, which
 // computes q, k and v itself (the prefill front-end, linear_attention.py:61-79,
